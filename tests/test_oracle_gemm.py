@@ -1,0 +1,149 @@
+"""Pins of the oracle's dequant-then-matmul GEMM and of the weight repack (CPU)."""
+import numpy as np
+import pytest
+
+from oracle import mfma_model as MM
+from oracle import mxfp4_oracle as O
+from vllm_sly_radiance_amd import synthetic
+
+
+def _case(M, N, K, seed):
+    x = synthetic.activations(M, K, seed)
+    w, ws = synthetic.weights(N, K, seed + 1000)
+    q, s = O.quant_per_token(x)
+    return x, q, s, w, ws
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 16, 32), (8, 48, 256), (17, 64, 640), (5, 33, 96)])
+def test_gemm_f32_vs_exact_f64(M, N, K):
+    _, q, s, w, ws = _case(M, N, K, M + N + K)
+    ref = O.gemm_ref_f32(q, s, w, ws).astype(np.float64)
+    exact = O.gemm_exact_f64(q, s, w, ws)
+    terms = O.gemm_abs_terms(q, s, w, ws)
+    # fp32 accumulation: error <= K * 2^-24 * sum|terms| (worst case), far below it in practice
+    assert np.all(np.abs(ref - exact) <= K * 2.0 ** -24 * terms + 1e-30)
+
+
+def test_gemm_one_hot_known_answer():
+    M, N, K = 2, 16, 64
+    q = np.zeros((M, K), np.uint8)
+    s = np.float32([0.5, 2.0])
+    w = np.zeros((N, K // 2), np.uint8)
+    ws = np.full((N, K // 32), 127, np.uint8)
+    q[0, 33] = 0x38                       # e4m3 1.0 at k = 33 (odd -> high nibble of byte 16)
+    q[1, 2] = 0x40                        # e4m3 2.0 at k = 2
+    w[5, 16] = 0x70                       # row 5, k = 33: code 7 (6.0) in the high nibble
+    ws[5, 1] = 126                        # block 1 of row 5: 2^-1
+    w[9, 1] = 0x0B                        # row 9, k = 2: code 0xB (-1.5) in the low nibble
+    y = O.gemm_exact_f64(q, s, w, ws)
+    expect = np.zeros((M, N))
+    expect[0, 5] = 1.0 * 6.0 * 0.5 * 0.5
+    expect[1, 9] = 2.0 * -1.5 * 2.0
+    assert np.array_equal(y, expect)
+    assert np.array_equal(O.gemm_ref_f32(q, s, w, ws), expect.astype(np.float32))
+
+
+def test_gemm_is_linear_in_the_token_scale():
+    _, q, s, w, ws = _case(4, 32, 128, 3)
+    y1 = O.gemm_exact_f64(q, s, w, ws)
+    y2 = O.gemm_exact_f64(q, s * np.float32(4.0), w, ws)
+    assert np.array_equal(y2, 4.0 * y1)
+
+
+def test_gemm_block_scale_exponent_shift():
+    # raising every block exponent of one row by 3 multiplies that output column by exactly 8
+    _, q, s, w, ws = _case(3, 32, 256, 4)
+    ws2 = ws.copy()
+    ws2[7] += 3
+    y1 = O.gemm_exact_f64(q, s, w, ws)
+    y2 = O.gemm_exact_f64(q, s, w, ws2)
+    assert np.array_equal(y2[:, 7], 8.0 * y1[:, 7])
+    others = [c for c in range(32) if c != 7]
+    assert np.array_equal(y2[:, others], y1[:, others])
+
+
+def test_linear_ref_rounds_to_bf16():
+    x, q, s, w, ws = _case(3, 40, 160, 5)
+    yb, y, q2, s2 = O.linear_ref(x, w, ws)
+    assert np.array_equal(q, q2) and np.array_equal(s, s2)
+    assert np.array_equal(yb, O.f32_to_bf16(y))
+
+
+# ---- repack ----------------------------------------------------------------------------------
+@pytest.mark.parametrize("N,K", [(16, 512), (48, 1024), (33, 96), (17408 // 64, 5120)])
+def test_repack_round_trip(N, K):
+    w, ws = synthetic.weights(N, K, N + K)
+    wq, sq = O.repack(w, ws)
+    Np, Kp = O.padded_dims(N, K)
+    assert wq.size == Np * Kp // 2 and sq.size == Np * Kp // 32
+    w2, ws2 = O.unrepack(wq, sq, N, K)
+    assert np.array_equal(w, w2) and np.array_equal(ws, ws2)
+
+
+def test_repack_is_a_byte_permutation():
+    # distinct byte "ids" in: every id comes out exactly once (nothing merged or dropped)
+    N, K = 32, 1024
+    ids = np.arange(N * K // 2, dtype=np.int64)
+    w = (ids % 251).astype(np.uint8).reshape(N, K // 2)
+    wq, _ = O.repack(w, np.full((N, K // 32), 127, np.uint8))
+    # track positions through the permutation with a second, offset id pattern
+    w_hi = ((ids // 251) % 256).astype(np.uint8).reshape(N, K // 2)
+    wq_hi, _ = O.repack(w_hi, np.full((N, K // 32), 127, np.uint8))
+    pairs = wq.astype(np.int64) + 251 * wq_hi.astype(np.int64)
+    assert np.array_equal(np.sort(pairs), ids)
+
+
+def test_repack_granule_lane_holds_one_mx_block():
+    # lane l of granule (nt, kt) = 16 checkpoint bytes of row nt*16 + l%16, block kt*4 + l//16
+    N, K = 32, 1024
+    w, ws = synthetic.weights(N, K, 11)
+    wq, sq = O.repack(w, ws)
+    wq = wq.reshape(N // 16, K // 128, 64, 16)
+    sq = sq.reshape(N // 16, K // 512, 64, 4)
+    for nt, kt, lane in [(0, 0, 0), (1, 3, 17), (0, 7, 63), (1, 5, 40)]:
+        n, kb = nt * 16 + lane % 16, kt * 4 + lane // 16
+        assert np.array_equal(wq[nt, kt, lane], w[n, kb * 16:kb * 16 + 16])
+        assert sq[nt, kt // 4, lane, kt % 4] == ws[n, kb]
+
+
+def test_repack_pads_with_zero_weights_and_unit_scales():
+    N, K = 20, 96
+    w, ws = synthetic.weights(N, K, 12)
+    wq, sq = O.repack(w, ws)
+    w_full, ws_full = O.unrepack(wq, sq, 32, 512)
+    assert not w_full[N:].any() and not w_full[:, K // 2:].any()
+    assert np.all(ws_full[N:] == 127) and np.all(ws_full[:, K // 32:] == 127)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 16, 128), (8, 32, 512), (19, 48, 1024), (3, 20, 96)])
+def test_mfma_model_over_repacked_bytes_equals_dequant_oracle(M, N, K):
+    """The GEMM computed from the repacked bytes through the MFMA operand model is the exact GEMM:
+    this pins the repack to the lane layout the kernels feed the hardware."""
+    _, q, s, w, ws = _case(M, N, K, 7 * M + N)
+    wq, sq = O.repack(w, ws)
+    y = MM.gemm_via_granules(q, s, wq, sq, M, N, K)
+    assert np.array_equal(y, O.gemm_exact_f64(q, s, w, ws))
+
+
+def test_mfma_model_detects_a_transposed_lane_map():
+    # a plausible layout mistake (k-block and column swapped inside the lane index) must not pass
+    M, N, K = 4, 16, 128
+    _, q, s, w, ws = _case(M, N, K, 21)
+    wq, sq = O.repack(w, ws)
+    g = wq.reshape(1, 4, 4, 16, 16).transpose(0, 1, 3, 2, 4).reshape(-1)   # lane = r*4 + h
+    assert not np.array_equal(MM.gemm_via_granules(q, s, g, sq, M, N, K),
+                              O.gemm_exact_f64(q, s, w, ws))
+
+
+def test_mfma_tile_one_hot_lane_map():
+    # one nonzero per operand: D must light up exactly at the documented (row, col)
+    a = np.zeros((64, 32), np.uint8)
+    b = np.zeros((64, 16), np.uint8)
+    a[16 * 2 + 5, 7] = 0x38          # A[row 5][k = 64 + 7] = 1.0
+    b[16 * 2 + 11, 3] = 0x70         # B[k = 64 + 7][col 11] = 6.0 (odd k -> high nibble of byte 3)
+    D = MM.mfma_tile(a, b, np.full(64, 127, np.uint8), np.full(64, 127, np.uint8))
+    assert D[5, 11] == 6.0 and np.count_nonzero(D) == 1
+    r, c = MM.d_lane_map()
+    lanes = MM.d_to_lanes(D)
+    lane, reg = np.argwhere(lanes != 0)[0]
+    assert (r[lane, reg], c[lane, reg]) == (5, 11)
