@@ -1,0 +1,123 @@
+/* C ABI of the MI355X (gfx950) MXFP4 W4A8 linear-layer library, libw4a8_mxfp4.so.
+ *
+ * Plain pointers, sizes and a HIP stream (as void*); no torch or C++ types cross this boundary.
+ * Device pointers are HIP device addresses owned by the caller (torch allocates every buffer in the
+ * Python host layer); the library never allocates device memory. Launches are asynchronous on the
+ * given stream and contain no allocation, so they are HIP-graph-capture safe.
+ *
+ * Errors: every entry point validates its arguments BEFORE launching anything and returns
+ * W4A8_OK (0) or a nonzero status; w4a8_last_error() then describes the failure (thread-local).
+ * Launch failures are checked with hipGetLastError after every launch (the reference never checks,
+ * sly/mxfp4/radiance_mxfp4_fp8.hip:1505-1512). This replaces the reference's std::runtime_error
+ * thrown from launch_impl (sly/mxfp4/radiance_mxfp4_fp8.hip:1378-1385), which pybind11 surfaced as
+ * a Python RuntimeError; the Python layer raises RuntimeError from the status.
+ *
+ * Formats: activations bf16 / e4m3fn [M, K] row-major with one fp32 scale per token; weights are
+ * the checkpoint's packed e2m1 [N, K/2] (low nibble = even k) with e8m0 scales [N, K/32], repacked
+ * once into "MFMA granules" (w4a8_repack). Output is bf16 [M, N] row-major.
+ */
+#ifndef W4A8_MXFP4_H_
+#define W4A8_MXFP4_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define W4A8_ABI_VERSION 1
+
+enum {
+  W4A8_OK = 0,
+  W4A8_EINVAL = 1,    /* bad shape, pointer, alignment or plan */
+  W4A8_ESCRATCH = 2,  /* a split-K plan was forced without enough registered scratch */
+  W4A8_EHIP = 3       /* the HIP runtime reported an error at launch */
+};
+
+enum { W4A8_KERNEL_AUTO = 0, W4A8_KERNEL_SKINNY = 1, W4A8_KERNEL_TILE = 2 };
+
+/* ABI version of the loaded library (W4A8_ABI_VERSION). */
+int w4a8_abi_version(void);
+
+/* Description of the last failure on the calling thread ("" if none). */
+const char* w4a8_last_error(void);
+
+/* Capability probe, the counterpart of psw_reader_mode (sly/mxfp4/radiance_mxfp4_fp8.hip:2392):
+ * the repacked weight layout this library reads. 1 = MFMA granules (16 n x 128 k, scale dwords
+ * per 4 k-tiles). */
+int w4a8_layout_version(void);
+
+/* Bytes of the repacked weight (wq) and scale (sq) buffers for an N x K layer: N is padded to 16
+ * and K to 512. Replaces the shape contract of permute_w / psw_pack_w_ / psw_fold_ws, which kept
+ * [N, K/2] and [K/32, N] (sly/mxfp4/radiance_mxfp4.py:181-226, :311-316). */
+int w4a8_packed_bytes(int N, int K, size_t* wq_bytes, size_t* sq_bytes);
+
+/* (1) Dynamic per-token activation quantizer: bf16 x [M, K] (row stride ldx elements) ->
+ * e4m3fn q [M, K] (contiguous) and fp32 scale [M]:
+ *   scale = max(amax(|x|) * fl32(1/448), 1/(448*512)),  q = e4m3_rne(clamp(x / scale, +-448)).
+ * Replaces the activation quant of radiance::mxfp4_linear: vllm's scaled_fp8_quant with
+ * use_per_token_if_dynamic (sly/mxfp4/radiance_mxfp4.py:726-730) and its pure-torch form
+ * _traced_quant (sly/mxfp4/radiance_mxfp4.py:392-396), whose arithmetic this follows bit for bit. */
+int w4a8_quant_per_token(const void* x, long ldx, void* q, float* scale, int M, int K,
+                         void* stream);
+
+/* (2) One-time weight repack: checkpoint w [N, K/2] + ws [N, K/32] -> wq, sq (w4a8_packed_bytes).
+ * Out of place; the caller may copy the result back into the checkpoint storage when the sizes
+ * match. Replaces the load-time repack of process_weights_after_loading: scale transpose,
+ * make_row_ref, permute_w, psw_pack_w_, psw_fold_ws (sly/mxfp4/radiance_mxfp4.py:1083-1171). */
+int w4a8_repack(const void* w, const void* ws, void* wq, void* sq, int N, int K, void* stream);
+
+/* Register caller-owned split-K scratch for the current device: fp32 partials and int counters.
+ * The counters must be zeroed once by the caller; the kernel's last-arriving workgroup resets each
+ * counter it used, so they stay zeroed. Launches that overlap on one device race on it. Replaces
+ * set_decode_scratch (sly/mxfp4/radiance_mxfp4_fp8.hip:1356-1360, registered from
+ * sly/mxfp4/radiance_mxfp4.py:1054-1080). Pass NULLs to unregister. */
+int w4a8_set_scratch(void* partial, size_t partial_bytes, void* counters, size_t counter_bytes);
+
+/* (3) The GEMM: c[M, N] bf16 = (a[M, K] e4m3 * a_scale[m]) . dequant(wq, sq)^T, fp32 accumulate.
+ * Picks the kernel from (M, N, K) (w4a8_plan). Replaces launch / launch_impl
+ * (sly/mxfp4/radiance_mxfp4_fp8.hip:1375-1700): same operands, the weight in the granule layout
+ * instead of fragment order + PSW + folded scales + wref. */
+int w4a8_gemm(const void* a, const float* a_scale, const void* wq, const void* sq, void* c, int M,
+              int N, int K, void* stream);
+
+/* The plan w4a8_gemm would use: kernel (W4A8_KERNEL_*), variant index and K split. Counterpart of
+ * the reference's band/split policy (sly/mxfp4/radiance_mxfp4_fp8.hip:1252-1343, :1390-1500) and
+ * its Python replica band_map (sly/mxfp4/band_map.py:31-95). */
+int w4a8_plan(int M, int N, int K, int* kernel, int* variant, int* split_k);
+
+/* w4a8_gemm with an explicit plan, for sweeps and tests (the reference forces cells through the
+ * RADIANCE_MXFP4_DECODE_KS / _BK environment knobs, sly/mxfp4/radiance_mxfp4_fp8.hip:1464-1475).
+ * split_k > 1 needs registered scratch of w4a8_scratch_bytes(); kernel 2 ignores split_k. */
+int w4a8_gemm_planned(const void* a, const float* a_scale, const void* wq, const void* sq, void* c,
+                      int M, int N, int K, int kernel, int variant, int split_k, void* stream);
+
+/* Number of instantiated variants of a kernel family, and their parameters:
+ * skinny: p = {MT (16-token fragments), NT (n-tiles per workgroup), waves, unroll};
+ * tile:   p = {WM, WN (MFMA tiles per wave), BM, BN (workgroup tile)}. */
+int w4a8_variant_count(int kernel);
+int w4a8_variant_info(int kernel, int variant, int* p0, int* p1, int* p2, int* p3);
+
+/* Scratch a (skinny variant, split_k) plan needs for N columns: partial bytes and counter bytes. */
+int w4a8_scratch_bytes(int variant, int N, int split_k, size_t* partial_bytes,
+                       size_t* counter_bytes);
+
+/* Quantize + GEMM in one call (two launches on the stream): the body of radiance::mxfp4_linear
+ * (sly/mxfp4/radiance_mxfp4.py:644-816) minus the output allocation, which stays with the caller
+ * (torch.empty at sly/mxfp4/radiance_mxfp4.py:737). q [M, K] and scale [M] are caller workspace. */
+int w4a8_linear(const void* x, long ldx, void* q, float* scale, const void* wq, const void* sq,
+                void* c, int M, int N, int K, void* stream);
+
+/* Diagnostic: register-resident throughput probe of the scaled MFMA (fp4 A x fp8 B) the GEMMs
+ * issue; shape 0 = 16x16x128, 1 = 32x32x64. Launches `blocks` workgroups of 4 waves that write
+ * blocks*4 checksums to out; *flop receives the FLOP performed, the caller times the launch. The
+ * counterpart of the reference's register-resident fp8 WMMA measurement, quoted at
+ * sly/mxfp4/radiance_mxfp4_fp8.hip:6-10. */
+int w4a8_mfma_probe(int shape, float* out, int blocks, int iters, double* flop, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* W4A8_MXFP4_H_ */

@@ -1,0 +1,60 @@
+"""Shared helpers for the GPU parity tests: host<->device transfers and the GEMM tolerance.
+
+GEMM tolerance (stated by the benchmark brief, applied against the oracle's fp32-accumulated
+reference `ref` = _exact_ref restated in oracle.mxfp4_oracle.gemm_ref_f32):
+  1. relative L2:  ||out - bf16(ref)||_2 / ||bf16(ref)||_2 <= 1e-3
+  2. per element:  |out - ref| <= 2 * ulp_bf16(ref) + 2^-24 * sqrt(K) * sum_k |xr_k * w_k|
+The second term of (2) is the fp32 accumulation-order allowance: two fp32 sums of the same K
+terms in different orders differ by about u * sqrt(K) * sum|terms| (u = 2^-24), which only matters
+for outputs that cancel to far below their terms; everywhere else (2) is the plain 2-ulp bound.
+"""
+import numpy as np
+import torch
+
+from oracle import mxfp4_oracle as O
+
+REL_L2_MAX = 1e-3
+ULP_MAX = 2.0
+
+
+def to_dev(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def bf16_dev(bits: np.ndarray) -> torch.Tensor:
+    return to_dev(bits.view(np.int16)).view(torch.bfloat16)
+
+
+def host_u16(t: torch.Tensor) -> np.ndarray:
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def host_u8(t: torch.Tensor) -> np.ndarray:
+    return t.view(torch.uint8).cpu().numpy()
+
+
+def stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def gemm_errors(out_bits: np.ndarray, q, s, w, ws):
+    """(rel_l2, worst ratio of |out - ref| to the per-element allowance, max ulp error)."""
+    K = w.shape[1] * 2
+    ref = O.gemm_ref_f32(q, s, w, ws).astype(np.float64)
+    refb = O.bf16_to_f32(O.f32_to_bf16(ref.astype(np.float32))).astype(np.float64)
+    out = O.bf16_to_f32(out_bits).astype(np.float64)
+    if not np.all(np.isfinite(out)):
+        return np.inf, np.inf, np.inf
+    rel = np.linalg.norm(out - refb) / max(np.linalg.norm(refb), 1e-300)
+    terms = O.gemm_abs_terms(q, s, w, ws)
+    ulp = O.bf16_ulp(ref)
+    allow = ULP_MAX * ulp + 2.0 ** -24 * np.sqrt(K) * terms
+    err = np.abs(out - ref)
+    return rel, float(np.max(err / allow)), float(np.max(err / ulp))
+
+
+def assert_gemm_close(out_bits: np.ndarray, q, s, w, ws, what: str = ""):
+    rel, ratio, ulps = gemm_errors(out_bits, q, s, w, ws)
+    assert rel <= REL_L2_MAX and ratio <= 1.0, \
+        f"{what}: rel_l2={rel:.3e} (max {REL_L2_MAX}), worst/allowance={ratio:.3f}, max_ulp={ulps:.2f}"
+    return rel, ulps

@@ -1,0 +1,128 @@
+"""The C-ABI library on the CPU: it loads, exports every symbol include/w4a8_mxfp4.h declares, and
+rejects bad arguments before touching a GPU (no compute call is made here)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from vllm_sly_radiance_amd import _native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "w4a8_mxfp4.h")
+
+
+def declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(w4a8_\w+)\s*\(", src, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.fail(f"{_native.LIB_PATH} missing: run __graft_entry__.build() first")
+    return _native.load_cdll()
+
+
+def test_header_declares_the_bound_surface():
+    assert declared_functions() == sorted(_native.SIGNATURES)
+
+
+def test_every_declared_symbol_is_exported(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", _native.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {ln.split()[-1] for ln in out.splitlines() if " T " in ln}
+    missing = [f for f in declared_functions() if f not in exported]
+    assert not missing, missing
+    # nothing but the C ABI leaks out (C++ internals stay hidden)
+    extra = sorted(s for s in exported if not s.startswith("w4a8_") and not s.startswith("_"))
+    assert not extra, extra
+
+
+def test_library_is_built_for_gfx950_only(lib, tmp_path):
+    # --offloading extracts the device images next to its input: work on a copy in tmp_path
+    copy = tmp_path / "lib.so"
+    copy.write_bytes(open(_native.LIB_PATH, "rb").read())
+    out = subprocess.run(["/opt/rocm/llvm/bin/llvm-objdump", "--offloading", str(copy)],
+                         capture_output=True, text=True, cwd=tmp_path)
+    if out.returncode != 0:
+        pytest.skip("llvm-objdump --offloading unavailable")
+    arches = set(re.findall(r"amdhsa--(gfx\w+)", out.stdout))
+    assert arches == {"gfx950"}, arches
+
+
+def test_abi_and_layout_version(lib):
+    assert lib.w4a8_abi_version() == _native.ABI_VERSION
+    assert lib.w4a8_layout_version() == 1
+
+
+def test_packed_bytes(lib):
+    a, b = ctypes.c_size_t(), ctypes.c_size_t()
+    assert lib.w4a8_packed_bytes(17408, 5120, ctypes.byref(a), ctypes.byref(b)) == 0
+    assert (a.value, b.value) == (17408 * 5120 // 2, 17408 * 5120 // 32)
+    assert lib.w4a8_packed_bytes(33, 96, ctypes.byref(a), ctypes.byref(b)) == 0
+    assert (a.value, b.value) == (48 * 512 // 2, 48 * 512 // 32)
+    assert lib.w4a8_packed_bytes(16, 48, ctypes.byref(a), ctypes.byref(b)) != 0
+    assert b"multiple of 32" in lib.w4a8_last_error()
+
+
+@pytest.mark.parametrize("M,N,K,msg", [(8, 5120, 5000, b"multiple of the 32-element"),
+                                       (-1, 16, 128, b"M >= 0"), (8, 0, 128, b"N > 0")])
+def test_gemm_rejects_bad_shapes_before_launch(lib, M, N, K, msg):
+    rc = lib.w4a8_gemm(None, None, None, None, None, M, N, K, None)
+    assert rc == 1 and msg in lib.w4a8_last_error()
+
+
+def test_gemm_rejects_null_and_misaligned_pointers(lib):
+    assert lib.w4a8_gemm(None, None, None, None, None, 8, 16, 128, None) == 1
+    assert b"null pointer" in lib.w4a8_last_error()
+    rc = lib.w4a8_gemm(4096 + 8, 4096, 4096, 4096, 4096, 8, 16, 128, None)
+    assert rc == 1 and b"misaligned" in lib.w4a8_last_error()
+
+
+def test_gemm_with_m_zero_is_a_no_op(lib):
+    assert lib.w4a8_gemm(None, None, None, None, None, 0, 16, 128, None) == 0
+
+
+def test_planned_rejects_unknown_kernel_and_variant(lib):
+    p = 1 << 20
+    assert lib.w4a8_gemm_planned(p, p, p, p, p, 8, 16, 128, 7, 0, 1, None) == 1
+    assert b"unknown kernel" in lib.w4a8_last_error()
+    assert lib.w4a8_gemm_planned(p, p, p, p, p, 8, 16, 128, 1, 999, 1, None) == 1
+    assert b"out of range" in lib.w4a8_last_error()
+    # a skinny variant refuses an M it does not cover
+    assert lib.w4a8_gemm_planned(p, p, p, p, p, 40, 16, 128, 1, 0, 1, None) == 1
+    assert b"covers M <=" in lib.w4a8_last_error()
+
+
+def test_split_k_without_scratch_is_refused(lib):
+    p = 1 << 20
+    assert lib.w4a8_set_scratch(None, 0, None, 0) in (0, 3)   # 3: no HIP device on this host
+    rc = lib.w4a8_gemm_planned(p, p, p, p, p, 8, 16, 4096, 1, 0, 4, None)
+    assert rc == 2 and b"w4a8_set_scratch" in lib.w4a8_last_error()
+
+
+def test_plan_bands(lib):
+    k, v, s = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    for M, kernel in [(1, 1), (8, 1), (64, 1), (65, 2), (4096, 2)]:
+        assert lib.w4a8_plan(M, 17408, 5120, ctypes.byref(k), ctypes.byref(v), ctypes.byref(s)) == 0
+        assert k.value == kernel and v.value >= 0 and s.value >= 1
+    assert lib.w4a8_plan(8, 17408, 5000, ctypes.byref(k), ctypes.byref(v), ctypes.byref(s)) == 1
+
+
+def test_variant_tables(lib):
+    sk = [(lib.w4a8_variant_count(1))]
+    assert sk[0] > 0 and lib.w4a8_variant_count(2) > 0 and lib.w4a8_variant_count(9) == -1
+    a = [ctypes.c_int() for _ in range(4)]
+    assert lib.w4a8_variant_info(2, 0, *[ctypes.byref(x) for x in a]) == 0
+    wm, wn, bm, bn = (x.value for x in a)
+    assert bm == 32 * wm and bn == 32 * wn
+
+
+def test_quant_and_repack_validate(lib):
+    assert lib.w4a8_quant_per_token(None, 8, None, None, 4, 8, None) == 1
+    assert lib.w4a8_quant_per_token(None, 8, None, None, 0, 8, None) == 0
+    assert lib.w4a8_quant_per_token(4096, 4, 4096, 4096, 4, 8, None) == 1   # ldx < K
+    assert lib.w4a8_repack(None, None, None, None, 16, 100, None) == 1

@@ -1,0 +1,309 @@
+"""GPU parity of the three gfx950 kernels against the oracle, through the C ABI.
+
+Bar: activation codes, per-token scales and repacked bytes bit-exact; bf16 GEMM outputs within the
+tolerance in tests/_check.py (rel-L2 <= 1e-3, <= 2 bf16 ulp of the fp32-accumulated reference plus
+the fp32 accumulation-order allowance)."""
+import functools
+import hashlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import mfma_model as MM
+from oracle import mxfp4_oracle as O
+from tests._check import assert_gemm_close, bf16_dev, host_u16, host_u8, stream, to_dev
+from vllm_sly_radiance_amd import _native, synthetic
+
+pytestmark = pytest.mark.gpu
+
+SKINNY, TILE = _native.KERNEL_SKINNY, _native.KERNEL_TILE
+
+
+@pytest.fixture(scope="module")
+def scratch(gpu_lib):
+    """Split-K scratch for every plan these tests force (up to 16 splits, N <= 36864)."""
+    partial = torch.empty(36864 // 16 * 16 * 4 * 64 * 4, dtype=torch.float32, device="cuda")
+    counters = torch.zeros(36864 // 16 + 8, dtype=torch.int32, device="cuda")
+    _native.set_scratch(partial.data_ptr(), partial.numel() * 4, counters.data_ptr(),
+                        counters.numel() * 4)
+    yield partial, counters
+    _native.set_scratch(None, 0, None, 0)
+
+
+@functools.lru_cache(maxsize=4)
+def cached_weights(N, K, seed):
+    return synthetic.weights(N, K, seed)
+
+
+def gpu_quant(x_bits, ldx=None):
+    M, K = x_bits.shape
+    if ldx is None or ldx == K:
+        x = bf16_dev(x_bits)
+        ldx = K
+    else:
+        pad = np.zeros((M, ldx), np.uint16)
+        pad[:, :K] = x_bits
+        x = bf16_dev(pad)
+    q = torch.empty((M, K), dtype=torch.uint8, device="cuda")
+    s = torch.empty((M,), dtype=torch.float32, device="cuda")
+    _native.quant_per_token(x.data_ptr(), ldx, q.data_ptr(), s.data_ptr(), M, K, stream())
+    torch.cuda.synchronize()
+    return host_u8(q), s.cpu().numpy()
+
+
+def gpu_repack(w, ws):
+    N, K = w.shape[0], w.shape[1] * 2
+    wb, sb = _native.packed_bytes(N, K)
+    wd, sd = to_dev(w), to_dev(ws)
+    wq = torch.empty(wb, dtype=torch.uint8, device="cuda")
+    sq = torch.empty(sb, dtype=torch.uint8, device="cuda")
+    _native.repack(wd.data_ptr(), sd.data_ptr(), wq.data_ptr(), sq.data_ptr(), N, K, stream())
+    return wq, sq
+
+
+def gpu_gemm(q, s, wq, sq, N, K, kernel=0, variant=-1, split_k=0):
+    M = q.shape[0]
+    qd, sd = to_dev(q), to_dev(s.astype(np.float32))
+    out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+    _native.gemm(qd.data_ptr(), sd.data_ptr(), wq.data_ptr(), sq.data_ptr(), out.data_ptr(), M, N,
+                 K, stream(), kernel, variant, split_k)
+    torch.cuda.synchronize()
+    return host_u16(out)
+
+
+def canon_nan(c):
+    return np.where((c & 0x7F) == 0x7F, 0x7F, c)
+
+
+# ---- (1) quantizer ----------------------------------------------------------------------------
+@pytest.mark.parametrize("M,K,ldx", [(1, 5120, None), (8, 5120, None), (17, 1000, None),
+                                     (64, 8704, None), (3, 17408, None), (5, 24, None),
+                                     (9, 5120, 5128), (7, 640, 641), (1, 40000, None),
+                                     (4096, 5120, None)])
+def test_quant_bit_exact(gpu_lib, M, K, ldx):
+    x = synthetic.activations(M, K, seed=M * 7 + K)
+    q, s = gpu_quant(x, ldx)
+    oq, os_ = O.quant_per_token(x)
+    assert np.array_equal(s.view(np.uint32), os_.view(np.uint32)), "scales differ"
+    bad = np.argwhere(q != oq)
+    assert bad.size == 0, f"{len(bad)} codes differ, first at {bad[:3].tolist()}"
+
+
+def test_quant_special_rows(gpu_lib):
+    K = 256
+    rows = np.zeros((8, K), np.float32)
+    rows[2, 7] = -0.0
+    rows[3, :] = np.linspace(-1e-30, 1e-30, K)
+    rows[4, :] = np.linspace(-3e38, 3e38, K)
+    rows[5, 3] = np.inf
+    rows[5, 4] = -2.0
+    rows[6, 9] = np.nan
+    rows[7, :] = 448.0
+    x = O.f32_to_bf16(rows)
+    x[2, 7] = 0x8000
+    q, s = gpu_quant(x)
+    oq, os_ = O.quant_per_token(x)
+    assert np.array_equal(np.isnan(s), np.isnan(os_))
+    fin = ~np.isnan(os_)
+    assert np.array_equal(s[fin].view(np.uint32), os_[fin].view(np.uint32))
+    assert np.array_equal(canon_nan(q), canon_nan(oq))
+    assert q[2, 7] == 0x80 and q[5, 4] == 0x80       # -0 kept; finite / inf -> -0
+
+
+def test_quant_rounding_ties_and_subnormals(gpu_lib):
+    # amax 448 gives scale exactly 1.0, so the codes are the e4m3 rounding of the inputs themselves:
+    # every e4m3 value, every tie between neighbours and one bf16 ulp either side of each tie.
+    pos = O.e4m3fn_decode(np.arange(0x7F, dtype=np.uint8)).astype(np.float64)
+    mids = ((pos[:-1] + pos[1:]) / 2).astype(np.float32)
+    mb = O.f32_to_bf16(mids).astype(np.uint16)
+    vals = np.concatenate([O.f32_to_bf16(pos.astype(np.float32)), mb, mb + 1, mb - 1])
+    vals = np.concatenate([vals, vals | 0x8000, [O.f32_to_bf16(np.float32([448.0]))[0]]])
+    K = -(-len(vals) // 8) * 8
+    row = np.zeros(K, np.uint16)
+    row[:len(vals)] = vals
+    x = np.stack([row, np.roll(row, 8)]).astype(np.uint16)
+    q, s = gpu_quant(x)
+    oq, os_ = O.quant_per_token(x)
+    assert np.all(s == 1.0) and np.array_equal(s, os_)
+    assert np.array_equal(q, oq)
+
+
+def test_quant_full_size_digest(gpu_lib):
+    # M=4096 K=5120 prefill activations: codes and scales hashed and compared with the oracle's
+    x = synthetic.activations(4096, 5120, seed=4096)
+    q, s = gpu_quant(x)
+    oq, os_ = O.quant_per_token(x)
+    h = lambda a: hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+    assert h(q) == h(oq) and h(s) == h(os_)
+
+
+# ---- (2) repack -------------------------------------------------------------------------------
+@pytest.mark.parametrize("N,K", [(17408, 5120), (5120, 8704), (48, 5120), (20, 96), (33, 640)])
+def test_repack_bit_exact(gpu_lib, N, K):
+    w, ws = synthetic.weights(N, K, seed=N + K)
+    wq, sq = gpu_repack(w, ws)
+    owq, osq = O.repack(w, ws)
+    assert np.array_equal(host_u8(wq), owq)
+    assert np.array_equal(host_u8(sq), osq)
+
+
+# ---- (3) GEMM ---------------------------------------------------------------------------------
+def one_hot_case(M, N, K, hits):
+    """Operands with one nonzero product per hit (m, n, k, code, exp): out[m, n] = value."""
+    q = np.zeros((M, K), np.uint8)
+    w = np.zeros((N, K // 2), np.uint8)
+    ws = np.full((N, K // 32), 127, np.uint8)
+    for m, n, k, code, e in hits:
+        q[m, k] = 0x38                                  # 1.0
+        w[n, k // 2] |= code << (4 * (k & 1))
+        ws[n, k // 32] = e
+    return q, w, ws
+
+
+@pytest.mark.parametrize("kernel,variant", [(0, -1), (TILE, 0), (TILE, 2)])
+def test_gemm_one_hot_lane_map(gpu_lib, kernel, variant):
+    """Single products placed across every lane group, k-block, nibble parity and scale byte: the
+    output must light up exactly at (m, n) with E2M1[code] * 2^(e-127). Pins the hardware MFMA
+    operand/result layout (oracle/mfma_model.py) and the granule repack on the device."""
+    M, N, K = 16, 64, 1024
+    rng = np.random.default_rng(5)
+    cases = []
+    for m in range(16):
+        n = (m * 5 + 3) % N
+        k = int(rng.integers(0, K))
+        cases.append((m, n, k, int(rng.integers(1, 16)), int(rng.integers(120, 134))))
+    # distinct rows, columns and k so no two products ever meet in one output
+    used_n, used_k, hits = set(), set(), []
+    for c in cases:
+        if c[1] not in used_n and c[2] not in used_k:
+            used_n.add(c[1])
+            used_k.add(c[2])
+            hits.append(c)
+    assert len(hits) >= 12
+    q, w, ws = one_hot_case(M, N, K, hits)
+    wq, sq = gpu_repack(w, ws)
+    out = O.bf16_to_f32(gpu_gemm(q, np.ones(M, np.float32), wq, sq, N, K, kernel, variant))
+    expect = np.zeros((M, N), np.float32)
+    for m, n, k, code, e in hits:
+        expect[m, n] = O.E2M1_VALUES[code] * 2.0 ** (e - 127)
+    assert np.array_equal(out, expect), np.argwhere(out != expect)[:5]
+
+
+def test_mfma_model_matches_device_on_random_granules(gpu_lib):
+    """Random codes and scales at one MFMA tile (M=N=16, K=128): the device result equals the
+    modeled MFMA (exact float64, then scaled and rounded once)."""
+    M, N, K = 16, 16, 128
+    rng = np.random.default_rng(9)
+    q = rng.integers(0, 256, (M, K), dtype=np.uint8)
+    q = np.where((q & 0x7F) == 0x7F, 0x38, q).astype(np.uint8)
+    w = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    ws = rng.integers(122, 132, (N, K // 32), dtype=np.uint8)
+    wq, sq = gpu_repack(w, ws)
+    out = gpu_gemm(q, np.ones(M, np.float32), wq, sq, N, K, SKINNY, 0, 1)
+    model = MM.gemm_via_granules(q, np.ones(M, np.float32), *O.repack(w, ws), M, N, K)
+    assert_gemm_close(out, q, np.ones(M, np.float32), w, ws, "random tile")
+    assert np.max(np.abs(O.bf16_to_f32(out) - model)) <= 2 * O.bf16_ulp(model).max()
+
+
+DECODE_SHAPES = [(5120, 5120), (17408, 5120), (5120, 8704), (48, 5120), (33, 640), (10240, 96)]
+
+
+@pytest.mark.parametrize("M", [1, 2, 8, 16, 17, 33, 64])
+@pytest.mark.parametrize("N,K", DECODE_SHAPES)
+def test_gemm_decode_band_auto_plan(gpu_lib, scratch, M, N, K):
+    x = synthetic.activations(M, K, seed=11 * M + K)
+    w, ws = cached_weights(N, K, N * 3 + K)
+    q, s = O.quant_per_token(x)
+    wq, sq = gpu_repack(w, ws)
+    out = gpu_gemm(q, s, wq, sq, N, K)
+    assert_gemm_close(out, q, s, w, ws, f"M={M} N={N} K={K} plan={_native.plan(M, N, K)}")
+
+
+def test_gemm_every_skinny_variant_and_split(gpu_lib, scratch):
+    N, K = 1040, 2560                               # 65 n-tiles: ragged against NT=2 and NT=4
+    w, ws = synthetic.weights(N, K, seed=77)
+    wq, sq = gpu_repack(w, ws)
+    for v, (mt, nt, waves, unroll) in enumerate(_native.variants(SKINNY)):
+        M = 16 * mt - 3
+        x = synthetic.activations(M, K, seed=v)
+        q, s = O.quant_per_token(x)
+        for ks in (1, 2, 4, 7):
+            out = gpu_gemm(q, s, wq, sq, N, K, SKINNY, v, ks)
+            assert_gemm_close(out, q, s, w, ws, f"variant {v} {(mt, nt, waves, unroll)} split {ks}")
+
+
+@pytest.mark.parametrize("M,N,K", [(65, 544, 1024), (300, 1040, 2560), (1000, 17408 // 8, 5120),
+                                   (129, 33, 640), (513, 5120, 8704)])
+def test_gemm_every_tile_variant(gpu_lib, M, N, K):
+    x = synthetic.activations(M, K, seed=M)
+    w, ws = synthetic.weights(N, K, seed=N)
+    q, s = O.quant_per_token(x)
+    wq, sq = gpu_repack(w, ws)
+    for v, cfg in enumerate(_native.variants(TILE)):
+        out = gpu_gemm(q, s, wq, sq, N, K, TILE, v)
+        assert_gemm_close(out, q, s, w, ws, f"M={M} N={N} K={K} tile variant {v} {cfg}")
+
+
+@pytest.mark.parametrize("N,K", [(17408, 5120), (5120, 8704)])
+def test_gemm_prefill_4096_sampled_rows(gpu_lib, N, K):
+    """M=4096 prefill GEMMs (gate_up, down): every output column, 192 sampled token rows checked
+    against the oracle (the oracle's full fp32 GEMM is minutes of CPU)."""
+    M = 4096
+    x = synthetic.activations(M, K, seed=K)
+    w, ws = synthetic.weights(N, K, seed=N)
+    q, s = O.quant_per_token(x)
+    wq, sq = gpu_repack(w, ws)
+    out = gpu_gemm(q, s, wq, sq, N, K)
+    rows = np.unique(np.concatenate([np.random.default_rng(1).choice(M, 190, replace=False),
+                                     [0, M - 1]]))
+    assert_gemm_close(out[rows], q[rows], s[rows], w, ws, f"M=4096 N={N} K={K}")
+
+
+def test_gemm_full_size_exact_properties(gpu_lib, scratch):
+    """Size-independent checks at the verify-decode and prefill shapes: doubling every token scale
+    doubles every output bit-exactly, and permuting tokens permutes output rows bit-exactly."""
+    N, K = 17408, 5120
+    w, ws = synthetic.weights(N, K, seed=1)
+    wq, sq = gpu_repack(w, ws)
+    for M in (8, 4096):
+        x = synthetic.activations(M, K, seed=M + 1)
+        q, s = O.quant_per_token(x)
+        y1 = gpu_gemm(q, s, wq, sq, N, K)
+        y2 = gpu_gemm(q, s * np.float32(2.0), wq, sq, N, K)
+        assert np.array_equal(O.bf16_to_f32(y2), 2 * O.bf16_to_f32(y1))
+        perm = np.random.default_rng(M).permutation(M)
+        y3 = gpu_gemm(q[perm], s[perm], wq, sq, N, K)
+        assert np.array_equal(y3, y1[perm])
+
+
+def test_split_k_reduction_has_no_race(gpu_lib, scratch):
+    """Race detector for the cross-workgroup split-K reduction (the reference's
+    sly/mxfp4/check_decode_splitk.py): two inputs alternate back to back with no synchronization,
+    so a partial read before its writer's release is a wrong value; every output must equal its
+    golden bit for bit."""
+    N, K = 1024, 8704
+    w, ws = synthetic.weights(N, K, seed=3)
+    wq, sq = gpu_repack(w, ws)
+    v = [i for i, c in enumerate(_native.variants(SKINNY)) if c[:3] == (1, 1, 16)][0]
+    ins = []
+    for j in range(2):
+        q, s = O.quant_per_token(synthetic.activations(8, K, seed=50 + j))
+        ins.append((to_dev(q), to_dev(s)))
+    for ks in (2, 4, 8, 16):
+        gold = []
+        for qd, sd in ins:
+            g = torch.empty((8, N), dtype=torch.bfloat16, device="cuda")
+            _native.gemm(qd.data_ptr(), sd.data_ptr(), wq.data_ptr(), sq.data_ptr(), g.data_ptr(),
+                         8, N, K, stream(), SKINNY, v, ks)
+            torch.cuda.synchronize()
+            gold.append(g)
+        outs = [torch.empty((64, 8, N), dtype=torch.bfloat16, device="cuda") for _ in range(2)]
+        for b in range(64):
+            for j, (qd, sd) in enumerate(ins):
+                _native.gemm(qd.data_ptr(), sd.data_ptr(), wq.data_ptr(), sq.data_ptr(),
+                             outs[j][b].data_ptr(), 8, N, K, stream(), SKINNY, v, ks)
+        torch.cuda.synchronize()
+        for j in range(2):
+            miss = int((outs[j] != gold[j]).flatten(1).any(1).sum())
+            assert miss == 0, f"split {ks}: {miss}/64 launches differ from golden {j}"

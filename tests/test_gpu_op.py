@@ -1,0 +1,113 @@
+"""The drop-in surface on the GPU: radiance::mxfp4_linear[_pq] and the MxFp4LinearKernel plugin's
+process_weights_after_loading + apply_weights, end to end against the oracle."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import mxfp4_oracle as O
+from tests._check import assert_gemm_close, bf16_dev, host_u16, host_u8, to_dev
+from vllm_sly_radiance_amd import radiance_mxfp4 as R
+from vllm_sly_radiance_amd import synthetic
+
+pytestmark = pytest.mark.gpu
+
+
+class Layer(torch.nn.Module):
+    def __init__(self, w, ws):
+        super().__init__()
+        self.weight = torch.nn.Parameter(to_dev(w), requires_grad=False)
+        self.weight_scale = torch.nn.Parameter(to_dev(ws), requires_grad=False)
+
+
+@pytest.fixture(scope="module")
+def kernel(gpu_lib):
+    return R.kernel_class()()
+
+
+@pytest.mark.parametrize("M,N,K", [(8, 5120, 5120), (1, 17408, 5120), (40, 5120, 8704),
+                                   (600, 2048, 5120), (7, 20, 96)])
+def test_plugin_load_and_apply(kernel, M, N, K):
+    w, ws = synthetic.weights(N, K, seed=N)
+    x = synthetic.activations(M, K, seed=M)
+    layer = Layer(w, ws)
+    storage = layer.weight.data_ptr()
+    kernel.process_weights_after_loading(layer)
+    aligned = N % 16 == 0 and K % 512 == 0
+    assert (layer.weight.data_ptr() == storage) == aligned       # repacked in place when aligned
+    assert tuple(layer.radiance_wref.shape) == (N, K, 0)
+    owq, osq = O.repack(w, ws)
+    assert np.array_equal(host_u8(layer.weight).reshape(-1), owq)
+    assert np.array_equal(host_u8(layer.weight_scale).reshape(-1), osq)
+
+    y = kernel.apply_weights(layer, bf16_dev(x))
+    assert y.dtype == torch.bfloat16 and tuple(y.shape) == (M, N)
+    q, s = O.quant_per_token(x)
+    assert_gemm_close(host_u16(y), q, s, w, ws, f"apply_weights M={M} N={N} K={K}")
+
+    # tuple (pre-quantized) contract and the quant-method name apply() give the same bits
+    qd, sd = R.quant_per_token(bf16_dev(x))
+    assert np.array_equal(host_u8(qd), q) and np.array_equal(sd.cpu().numpy(), s)
+    y_pq = kernel.apply_weights(layer, (qd, sd))
+    assert torch.equal(y_pq, y)
+    assert torch.equal(kernel.apply(layer, bf16_dev(x)), y)
+
+    bias = torch.randn(N, device="cuda", dtype=torch.bfloat16)
+    assert torch.equal(kernel.apply_weights(layer, bf16_dev(x), bias), y + bias)
+
+
+def test_leading_dims_are_flattened(kernel):
+    N, K = 64, 512
+    w, ws = synthetic.weights(N, K, seed=5)
+    layer = Layer(w, ws)
+    kernel.process_weights_after_loading(layer)
+    x = synthetic.activations(6, K, seed=6)
+    y2 = kernel.apply_weights(layer, bf16_dev(x))
+    y3 = kernel.apply_weights(layer, bf16_dev(x).view(2, 3, K))
+    assert tuple(y3.shape) == (2, 3, N) and torch.equal(y3.reshape(6, N), y2)
+
+
+def test_op_refuses_mismatched_activation(kernel):
+    N, K = 64, 512
+    w, ws = synthetic.weights(N, K, seed=7)
+    layer = Layer(w, ws)
+    kernel.process_weights_after_loading(layer)
+    x = torch.zeros(4, K + 32, device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="does not match K"):
+        kernel.apply_weights(layer, x)
+
+
+def test_op_is_one_opaque_node_under_compile(kernel):
+    N, K = 128, 1024
+    w, ws = synthetic.weights(N, K, seed=8)
+    layer = Layer(w, ws)
+    kernel.process_weights_after_loading(layer)
+    f = torch.compile(lambda t: kernel.apply_weights(layer, t), fullgraph=True, dynamic=True,
+                      backend="eager")
+    x = bf16_dev(synthetic.activations(9, K, seed=9))
+    assert torch.equal(f(x), kernel.apply_weights(layer, x))
+
+
+def test_hip_graph_capture_and_replay(kernel):
+    """The op allocates nothing natively and launches on the current stream, so it captures into a
+    HIP graph; every replay (with eager work and syncs in between) must match the eager result."""
+    N, K = 17408, 5120
+    w, ws = synthetic.weights(N, K, seed=10)
+    layer = Layer(w, ws)
+    kernel.process_weights_after_loading(layer)
+    x = bf16_dev(synthetic.activations(8, K, seed=11))
+    eager = kernel.apply_weights(layer, x)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            kernel.apply_weights(layer, x)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y = kernel.apply_weights(layer, x)
+    for i in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager), f"replay {i}"
+        _ = (x.float() * 2).sum().item()          # unrelated eager work between replays

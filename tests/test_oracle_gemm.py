@@ -137,13 +137,20 @@ def test_mfma_model_detects_a_transposed_lane_map():
 
 def test_mfma_tile_one_hot_lane_map():
     # one nonzero per operand: D must light up exactly at the documented (row, col)
-    a = np.zeros((64, 32), np.uint8)
-    b = np.zeros((64, 16), np.uint8)
-    a[16 * 2 + 5, 7] = 0x38          # A[row 5][k = 64 + 7] = 1.0
-    b[16 * 2 + 11, 3] = 0x70         # B[k = 64 + 7][col 11] = 6.0 (odd k -> high nibble of byte 3)
-    D = MM.mfma_tile(a, b, np.full(64, 127, np.uint8), np.full(64, 127, np.uint8))
-    assert D[5, 11] == 6.0 and np.count_nonzero(D) == 1
+    from oracle.mxfp4_oracle import E2M1_VALUES
+    a = np.zeros((64, 16), np.uint8)
+    b = np.zeros((64, 32), np.uint8)
+    a[16 * 2 + 11, 3] = 0x70         # A[row 11][k = 64 + 7] = 6.0 (odd k -> high nibble of byte 3)
+    b[16 * 2 + 5, 7] = 0x38          # B[k = 64 + 7][col 5] = 1.0
+    unit = np.full(64, 127, np.uint8)
+    D = MM.mfma_tile(MM.fp4_lane_values(a, unit), MM.fp8_lane_values(b, unit))
+    assert D[11, 5] == 6.0 and np.count_nonzero(D) == 1
     r, c = MM.d_lane_map()
     lanes = MM.d_to_lanes(D)
     lane, reg = np.argwhere(lanes != 0)[0]
-    assert (r[lane, reg], c[lane, reg]) == (5, 11)
+    assert (r[lane, reg], c[lane, reg]) == (11, 5) and lane == 16 * 2 + 5 and reg == 3
+    # the A-operand scale byte of lane 43 scales exactly that element
+    sa = unit.copy()
+    sa[16 * 2 + 11] = 130
+    D2 = MM.mfma_tile(MM.fp4_lane_values(a, sa), MM.fp8_lane_values(b, unit))
+    assert D2[11, 5] == 48.0 and E2M1_VALUES[7] == 6.0

@@ -1,0 +1,283 @@
+// C ABI of libw4a8_mxfp4.so: argument validation, plan selection and dispatch.
+// Declarations and the reference interfaces each entry point replaces: include/w4a8_mxfp4.h.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "w4a8_internal.h"
+#include "w4a8_mxfp4.h"
+
+#define W4A8_API extern "C" __attribute__((visibility("default")))
+
+namespace {
+
+using namespace w4a8;
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return W4A8_OK;
+  return fail(W4A8_EHIP, "%s: HIP error %d (%s)", what, (int)e, hipGetErrorString(e));
+}
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// Per-device split-K scratch (caller-owned; registered once at load time).
+struct Scratch {
+  float* partial = nullptr;
+  size_t partial_bytes = 0;
+  int* counters = nullptr;
+  size_t counter_bytes = 0;
+};
+constexpr int kMaxDevices = 64;
+Scratch g_scratch[kMaxDevices];
+
+int current_device() {
+  int d = 0;
+  if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= kMaxDevices) return -1;
+  return d;
+}
+
+int check_gemm_shape(const char* who, int M, int N, int K) {
+  if (M < 0 || N <= 0 || K <= 0)
+    return fail(W4A8_EINVAL, "%s: need M >= 0, N > 0, K > 0 (got M=%d N=%d K=%d)", who, M, N, K);
+  if (K % 32)
+    return fail(W4A8_EINVAL, "%s: K=%d is not a multiple of the 32-element MX block", who, K);
+  if ((size_t)padded_n(N) * padded_k(K) / 2 > ((size_t)1 << 40))
+    return fail(W4A8_EINVAL, "%s: N=%d K=%d is too large", who, N, K);
+  return W4A8_OK;
+}
+
+int check_gemm_ptrs(const char* who, const void* a, const float* as, const void* wq,
+                    const void* sq, const void* c) {
+  if (!a || !as || !wq || !sq || !c) return fail(W4A8_EINVAL, "%s: null pointer", who);
+  if (!aligned(a, 16) || !aligned(wq, 16) || !aligned(sq, 4) || !aligned(as, 4) || !aligned(c, 2))
+    return fail(W4A8_EINVAL,
+                "%s: misaligned operand (a and wq need 16 B, sq and a_scale 4 B, c 2 B)", who);
+  return W4A8_OK;
+}
+
+int find_skinny(int mt, int nt, int waves) {
+  for (int v = 0; v < skinny_variant_count(); ++v) {
+    const SkinnyCfg c = skinny_variant(v);
+    if (c.mt == mt && c.nt == nt && c.waves == waves) return v;
+  }
+  return -1;
+}
+
+int find_tile(int wm, int wn) {
+  for (int v = 0; v < tile_variant_count(); ++v) {
+    const TileCfg c = tile_variant(v);
+    if (c.wm == wm && c.wn == wn) return v;
+  }
+  return -1;
+}
+
+bool scratch_fits(int dev, int variant, int N, int split_k) {
+  if (split_k <= 1) return true;
+  if (dev < 0) return false;
+  const Scratch& s = g_scratch[dev];
+  return s.partial && s.counters &&
+         skinny_scratch_bytes(variant, N, split_k) <= s.partial_bytes &&
+         (size_t)skinny_counter_count(variant, N) * sizeof(int) <= s.counter_bytes;
+}
+
+// Decode / verify band: M <= 64 streams the weights once. The workgroup count should cover the
+// 256 CUs several times over; for small N the K dimension is split across workgroups too.
+void plan_impl(int M, int N, int K, int dev, int* kernel, int* variant, int* split_k) {
+  if (M <= 64) {
+    const int mt = M <= 16 ? 1 : ceil_div(M, 16);
+    const int ntiles = padded_n(N) / kNTile;
+    int waves = ntiles >= 512 ? 4 : ntiles >= 128 ? 8 : 16;
+    int v = find_skinny(mt, 1, waves);
+    int ks = 1;
+    const int kte = ceil_div(K, kKTile);
+    if (ntiles < 128) {
+      for (int c = 2; c <= 16 && ntiles * ks < 256; c *= 2)
+        if (c <= kte / 2 && scratch_fits(dev, v, N, c)) ks = c;
+    }
+    *kernel = W4A8_KERNEL_SKINNY;
+    *variant = v;
+    *split_k = ks;
+    return;
+  }
+  *kernel = W4A8_KERNEL_TILE;
+  *variant = M >= 2048 ? find_tile(8, 4) : M >= 512 ? find_tile(4, 4) : find_tile(2, 4);
+  *split_k = 1;
+}
+
+int gemm_dispatch(const void* a, const float* as, const void* wq, const void* sq, void* c, int M,
+                  int N, int K, int kernel, int variant, int split_k, void* stream) {
+  const GemmArgs g{(const uint8_t*)a, as, (const uint8_t*)wq, (const uint32_t*)sq, (uint16_t*)c,
+                   M, N, K};
+  const hipStream_t st = (hipStream_t)stream;
+  if (kernel == W4A8_KERNEL_SKINNY) {
+    if (variant < 0 || variant >= skinny_variant_count())
+      return fail(W4A8_EINVAL, "w4a8_gemm: skinny variant %d out of range", variant);
+    const SkinnyCfg cfg = skinny_variant(variant);
+    if (M > 16 * cfg.mt)
+      return fail(W4A8_EINVAL, "w4a8_gemm: skinny variant %d covers M <= %d, got M=%d", variant,
+                  16 * cfg.mt, M);
+    if (split_k < 1 || split_k > 64)
+      return fail(W4A8_EINVAL, "w4a8_gemm: split_k=%d outside 1..64", split_k);
+    float* partial = nullptr;
+    int* counters = nullptr;
+    if (split_k > 1) {
+      const int dev = current_device();
+      if (!scratch_fits(dev, variant, N, split_k))
+        return fail(W4A8_ESCRATCH,
+                    "w4a8_gemm: split_k=%d needs %zu B of partials and %zu B of counters; "
+                    "register them with w4a8_set_scratch",
+                    split_k, skinny_scratch_bytes(variant, N, split_k),
+                    (size_t)skinny_counter_count(variant, N) * sizeof(int));
+      partial = g_scratch[dev].partial;
+      counters = g_scratch[dev].counters;
+    }
+    return hip_status(launch_skinny(g, variant, split_k, partial, counters, st), "w4a8_gemm");
+  }
+  if (kernel == W4A8_KERNEL_TILE) {
+    if (variant < 0 || variant >= tile_variant_count())
+      return fail(W4A8_EINVAL, "w4a8_gemm: tile variant %d out of range", variant);
+    return hip_status(launch_tile(g, variant, st), "w4a8_gemm");
+  }
+  return fail(W4A8_EINVAL, "w4a8_gemm: unknown kernel %d", kernel);
+}
+
+}  // namespace
+
+W4A8_API int w4a8_abi_version(void) { return W4A8_ABI_VERSION; }
+
+W4A8_API const char* w4a8_last_error(void) { return g_err; }
+
+W4A8_API int w4a8_layout_version(void) { return 1; }
+
+W4A8_API int w4a8_packed_bytes(int N, int K, size_t* wq_bytes, size_t* sq_bytes) {
+  if (N <= 0 || K <= 0 || K % 32)
+    return fail(W4A8_EINVAL, "w4a8_packed_bytes: need N > 0 and K a positive multiple of 32");
+  if (wq_bytes) *wq_bytes = (size_t)padded_n(N) * padded_k(K) / 2;
+  if (sq_bytes) *sq_bytes = (size_t)padded_n(N) * padded_k(K) / 32;
+  return W4A8_OK;
+}
+
+W4A8_API int w4a8_quant_per_token(const void* x, long ldx, void* q, float* scale, int M, int K,
+                                  void* stream) {
+  if (M < 0 || K < 0) return fail(W4A8_EINVAL, "w4a8_quant_per_token: negative M or K");
+  if (M == 0) return W4A8_OK;
+  if (!x || !q || !scale) return fail(W4A8_EINVAL, "w4a8_quant_per_token: null pointer");
+  if (ldx < K) return fail(W4A8_EINVAL, "w4a8_quant_per_token: ldx=%ld < K=%d", ldx, K);
+  if (!aligned(x, 2) || !aligned(scale, 4))
+    return fail(W4A8_EINVAL, "w4a8_quant_per_token: misaligned x or scale");
+  return hip_status(launch_quant((const uint16_t*)x, ldx, (uint8_t*)q, scale, M, K,
+                                 (hipStream_t)stream),
+                    "w4a8_quant_per_token");
+}
+
+W4A8_API int w4a8_repack(const void* w, const void* ws, void* wq, void* sq, int N, int K,
+                         void* stream) {
+  if (N <= 0 || K <= 0 || K % 32)
+    return fail(W4A8_EINVAL, "w4a8_repack: need N > 0 and K a positive multiple of 32 (N=%d K=%d)",
+                N, K);
+  if (!w || !ws || !wq || !sq) return fail(W4A8_EINVAL, "w4a8_repack: null pointer");
+  if (!aligned(w, 16) || !aligned(wq, 16) || !aligned(sq, 4))
+    return fail(W4A8_EINVAL, "w4a8_repack: w and wq need 16-byte alignment, sq 4-byte");
+  return hip_status(launch_repack((const uint8_t*)w, (const uint8_t*)ws, (uint8_t*)wq,
+                                  (uint32_t*)sq, N, K, (hipStream_t)stream),
+                    "w4a8_repack");
+}
+
+W4A8_API int w4a8_set_scratch(void* partial, size_t partial_bytes, void* counters,
+                              size_t counter_bytes) {
+  const int dev = current_device();
+  if (dev < 0) return fail(W4A8_EHIP, "w4a8_set_scratch: no current HIP device");
+  if ((partial && !aligned(partial, 16)) || (counters && !aligned(counters, 4)))
+    return fail(W4A8_EINVAL, "w4a8_set_scratch: partials need 16-byte, counters 4-byte alignment");
+  Scratch& s = g_scratch[dev];
+  s.partial = (float*)partial;
+  s.partial_bytes = partial ? partial_bytes : 0;
+  s.counters = (int*)counters;
+  s.counter_bytes = counters ? counter_bytes : 0;
+  return W4A8_OK;
+}
+
+W4A8_API int w4a8_plan(int M, int N, int K, int* kernel, int* variant, int* split_k) {
+  if (int e = check_gemm_shape("w4a8_plan", M, N, K)) return e;
+  if (!kernel || !variant || !split_k) return fail(W4A8_EINVAL, "w4a8_plan: null output");
+  plan_impl(M, N, K, current_device(), kernel, variant, split_k);
+  return W4A8_OK;
+}
+
+W4A8_API int w4a8_gemm_planned(const void* a, const float* a_scale, const void* wq,
+                               const void* sq, void* c, int M, int N, int K, int kernel,
+                               int variant, int split_k, void* stream) {
+  if (int e = check_gemm_shape("w4a8_gemm", M, N, K)) return e;
+  if (M == 0) return W4A8_OK;
+  if (int e = check_gemm_ptrs("w4a8_gemm", a, a_scale, wq, sq, c)) return e;
+  if (kernel == W4A8_KERNEL_AUTO) plan_impl(M, N, K, current_device(), &kernel, &variant, &split_k);
+  return gemm_dispatch(a, a_scale, wq, sq, c, M, N, K, kernel, variant, split_k, stream);
+}
+
+W4A8_API int w4a8_gemm(const void* a, const float* a_scale, const void* wq, const void* sq,
+                       void* c, int M, int N, int K, void* stream) {
+  return w4a8_gemm_planned(a, a_scale, wq, sq, c, M, N, K, W4A8_KERNEL_AUTO, -1, 0, stream);
+}
+
+W4A8_API int w4a8_variant_count(int kernel) {
+  if (kernel == W4A8_KERNEL_SKINNY) return skinny_variant_count();
+  if (kernel == W4A8_KERNEL_TILE) return tile_variant_count();
+  fail(W4A8_EINVAL, "w4a8_variant_count: unknown kernel %d", kernel);
+  return -1;
+}
+
+W4A8_API int w4a8_variant_info(int kernel, int variant, int* p0, int* p1, int* p2, int* p3) {
+  int v[4];
+  if (kernel == W4A8_KERNEL_SKINNY && variant >= 0 && variant < skinny_variant_count()) {
+    const SkinnyCfg c = skinny_variant(variant);
+    v[0] = c.mt; v[1] = c.nt; v[2] = c.waves; v[3] = c.unroll;
+  } else if (kernel == W4A8_KERNEL_TILE && variant >= 0 && variant < tile_variant_count()) {
+    const TileCfg c = tile_variant(variant);
+    v[0] = c.wm; v[1] = c.wn; v[2] = c.bm; v[3] = c.bn;
+  } else {
+    return fail(W4A8_EINVAL, "w4a8_variant_info: no variant %d of kernel %d", variant, kernel);
+  }
+  if (p0) *p0 = v[0];
+  if (p1) *p1 = v[1];
+  if (p2) *p2 = v[2];
+  if (p3) *p3 = v[3];
+  return W4A8_OK;
+}
+
+W4A8_API int w4a8_scratch_bytes(int variant, int N, int split_k, size_t* partial_bytes,
+                                size_t* counter_bytes) {
+  if (variant < 0 || variant >= skinny_variant_count() || N <= 0 || split_k < 1)
+    return fail(W4A8_EINVAL, "w4a8_scratch_bytes: bad variant, N or split_k");
+  if (partial_bytes) *partial_bytes = skinny_scratch_bytes(variant, N, split_k);
+  if (counter_bytes)
+    *counter_bytes = split_k > 1 ? (size_t)skinny_counter_count(variant, N) * sizeof(int) : 0;
+  return W4A8_OK;
+}
+
+W4A8_API int w4a8_linear(const void* x, long ldx, void* q, float* scale, const void* wq,
+                         const void* sq, void* c, int M, int N, int K, void* stream) {
+  if (int e = check_gemm_shape("w4a8_linear", M, N, K)) return e;
+  if (M == 0) return W4A8_OK;
+  if (int e = check_gemm_ptrs("w4a8_linear", q, scale, wq, sq, c)) return e;
+  if (int e = w4a8_quant_per_token(x, ldx, q, scale, M, K, stream)) return e;
+  return w4a8_gemm(q, scale, wq, sq, c, M, N, K, stream);
+}
+
+W4A8_API int w4a8_mfma_probe(int shape, float* out, int blocks, int iters, double* flop,
+                             void* stream) {
+  if ((shape != 0 && shape != 1) || !out || !flop || blocks <= 0 || iters <= 0)
+    return fail(W4A8_EINVAL, "w4a8_mfma_probe: need shape 0/1, out, flop, blocks > 0, iters > 0");
+  return hip_status(launch_mfma_probe(shape, out, blocks, iters, flop, (hipStream_t)stream),
+                    "w4a8_mfma_probe");
+}

@@ -1,0 +1,114 @@
+// Internals shared by the MXFP4 W4A8 kernels for gfx950 (CDNA4). Not part of the C ABI.
+//
+// Weight layout ("MFMA granules"): one granule is the fp4 A operand of one
+// v_mfma_scale_f32_16x16x128_f8f6f4: 16 output columns x 128 k = 64 lanes x 16 bytes, lane l
+// holding column n0 + (l % 16) and the 32-element MX block k0/32 + l/16 as 16 consecutive
+// checkpoint bytes (low nibble = even k). Granules are stored [n-tile][k-tile][lane][16 B], so a
+// wave streams 1 KiB of contiguous HBM per 128-bit load. The e8m0 block scales ride in one dword per
+// lane per group of four k-tiles, [n-tile][k-group][lane][4 B], byte j = k-tile 4g + j; the MFMA's
+// per-lane A-scale byte is exactly the scale of that lane's block.
+//
+// Activations are row-major e4m3 [M, K] with one fp32 scale per token; the activation fragment is
+// the MFMA's fp8 B operand (lane l: token m0 + l % 16, block k0/32 + l/16, 32 bytes) with scale
+// byte 127, and the per-token scale is applied in the epilogue. D = W . X^T, so lane l, register
+// i holds output (token m0 + l % 16, column n0 + 4*(l/16) + i): four consecutive bf16 per lane.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace w4a8 {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kKTile = 128;          // k per granule
+constexpr int kKGroup = 4;           // k-tiles per scale dword
+constexpr int kKAlign = kKTile * kKGroup;
+constexpr int kNTile = 16;           // output columns per granule
+constexpr int kGranuleBytes = 1024;  // 64 lanes x 16 B
+constexpr uint32_t kUnitScales = 0x7F7F7F7Fu;   // e8m0 127 = 1.0 in every byte
+
+__host__ __device__ constexpr int ceil_div(int a, int b) { return (a + b - 1) / b; }
+__host__ __device__ constexpr int padded_n(int N) { return ceil_div(N, kNTile) * kNTile; }
+__host__ __device__ constexpr int padded_k(int K) { return ceil_div(K, kKAlign) * kKAlign; }
+
+// acc(16 n x 16 m) += W(16 x 128, e2m1, lane scale byte 0 of ws) . X^T(128 x 16, e4m3, scale 1)
+__device__ __forceinline__ v4f mfma_w4a8(const v4i w, const v8i x, const v4f acc, uint32_t ws) {
+  const v8i a = {w[0], w[1], w[2], w[3], 0, 0, 0, 0};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, x, acc, 4, 0, 0, (int)ws, 0,
+                                                         (int)kUnitScales);
+}
+
+// float -> bf16 bits, round to nearest even; NaN -> 0x7FC0 | sign
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return ((u >> 16) & 0x8000u) | 0x7FC0u;
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ v4i load_v4i(const void* p) { return *reinterpret_cast<const v4i*>(p); }
+
+__device__ __forceinline__ v4i load_v4i_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
+}
+
+// The 32 activation bytes of one B-operand lane (two 128-bit loads).
+__device__ __forceinline__ v8i load_v8i(const void* p) {
+  const v4i lo = reinterpret_cast<const v4i*>(p)[0];
+  const v4i hi = reinterpret_cast<const v4i*>(p)[1];
+  return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// Four consecutive outputs of one token, scaled and rounded, as one 8-byte store when aligned.
+__device__ __forceinline__ void store_out4(uint16_t* C, int ldc, int m, int n, int N, v4f v,
+                                           float scale, bool vec_ok) {
+  const uint32_t b0 = f32_to_bf16(v[0] * scale), b1 = f32_to_bf16(v[1] * scale);
+  const uint32_t b2 = f32_to_bf16(v[2] * scale), b3 = f32_to_bf16(v[3] * scale);
+  uint16_t* row = C + (size_t)m * ldc;
+  if (vec_ok && n + 3 < N) {
+    *reinterpret_cast<uint2*>(row + n) = make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
+  } else {
+    if (n < N) row[n] = (uint16_t)b0;
+    if (n + 1 < N) row[n + 1] = (uint16_t)b1;
+    if (n + 2 < N) row[n + 2] = (uint16_t)b2;
+    if (n + 3 < N) row[n + 3] = (uint16_t)b3;
+  }
+}
+
+// ---- host-side launchers (one per kernel family) ---------------------------------------------
+struct GemmArgs {
+  const uint8_t* a;      // e4m3 [M, K] row-major
+  const float* a_scale;  // [M]
+  const uint8_t* wq;     // granules
+  const uint32_t* sq;    // scale dwords
+  uint16_t* c;           // bf16 [M, N] row-major
+  int M, N, K;
+};
+
+hipError_t launch_quant(const uint16_t* x, long ldx, uint8_t* q, float* s, int M, int K,
+                        hipStream_t stream);
+hipError_t launch_repack(const uint8_t* w, const uint8_t* ws, uint8_t* wq, uint32_t* sq, int N,
+                         int K, hipStream_t stream);
+
+// Skinny split-K family (M <= 64). variant indexes the instantiated (MT, NT, WAVES, U) table.
+struct SkinnyCfg { int mt, nt, waves, unroll; };
+int skinny_variant_count();
+SkinnyCfg skinny_variant(int v);
+size_t skinny_scratch_bytes(int variant, int N, int split_k);
+int skinny_counter_count(int variant, int N);
+hipError_t launch_skinny(const GemmArgs& g, int variant, int split_k, float* partial,
+                         int* counters, hipStream_t stream);
+
+// Macro-tile family (large M). variant indexes the instantiated (WM, WN) table.
+struct TileCfg { int wm, wn, bm, bn; };
+int tile_variant_count();
+TileCfg tile_variant(int v);
+hipError_t launch_tile(const GemmArgs& g, int variant, hipStream_t stream);
+
+// Register-resident MFMA throughput probe (shape 0: 16x16x128, 1: 32x32x64).
+hipError_t launch_mfma_probe(int shape, float* out, int blocks, int iters, double* flop,
+                             hipStream_t stream);
+
+}  // namespace w4a8

@@ -1,0 +1,71 @@
+// Register-resident throughput probe of the gfx950 scaled MFMA with fp4 A and fp8 B operands,
+// the instruction every GEMM here issues. It pins the denominator the prefill GEMM's MFMA
+// utilisation is quoted against, as the reference pinned its own fp8 WMMA rate on gfx1201
+// (325.2 TFLOP/s register-resident, sly/mxfp4/radiance_mxfp4_fp8.hip:6-10).
+// Each wave runs 8 independent accumulator chains so the issue rate, not the dependency latency,
+// bounds it; operands never leave registers. One thread per wave writes a checksum so nothing is
+// optimised away.
+#include "w4a8_internal.h"
+
+namespace w4a8 {
+namespace {
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+__global__ __launch_bounds__(256) void mfma_rate_16x16x128(float* out, int iters) {
+  const int l = threadIdx.x;
+  const v4i w = {0x22222222 ^ l, 0x13131313, 0x31313131 ^ (l << 8), 0x02020202};
+  const v8i x = {0x38383838, 0x30303030 ^ l, 0x38303830, 0x30383038,
+                 0x38383838, 0x30303030, 0x38303830 ^ (l << 16), 0x30383038};
+  v4f acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = mfma_w4a8(w, x, acc[i], 120u + (uint32_t)i);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s += acc[i][0] + acc[i][1] + acc[i][2] + acc[i][3];
+  if ((l & 63) == 0) out[blockIdx.x * 4 + (l >> 6)] = s;
+}
+
+__global__ __launch_bounds__(256) void mfma_rate_32x32x64(float* out, int iters) {
+  const int l = threadIdx.x;
+  const v8i w = {0x22222222 ^ l, 0x13131313, 0x31313131, 0x02020202, 0, 0, 0, 0};
+  const v8i x = {0x38383838, 0x30303030 ^ l, 0x38303830, 0x30383038,
+                 0x38383838, 0x30303030, 0x38303830, 0x30383038};
+  v16f acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = v16f{};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      acc[i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w, x, acc[i], 4, 0, 0,
+                                                               120 + i, 0, (int)kUnitScales);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) s += acc[i][j];
+  if ((l & 63) == 0) out[blockIdx.x * 4 + (l >> 6)] = s;
+}
+
+}  // namespace
+
+// Launches `blocks` workgroups of 4 waves; returns the FLOP the launch performs in *flop.
+hipError_t launch_mfma_probe(int shape, float* out, int blocks, int iters, double* flop,
+                             hipStream_t stream) {
+  const double waves = 4.0 * blocks;
+  if (shape == 0) {
+    hipLaunchKernelGGL(mfma_rate_16x16x128, dim3(blocks), dim3(256), 0, stream, out, iters);
+    *flop = waves * iters * 8.0 * (2.0 * 16 * 16 * 128);
+  } else {
+    hipLaunchKernelGGL(mfma_rate_32x32x64, dim3(blocks), dim3(256), 0, stream, out, iters);
+    *flop = waves * iters * 4.0 * (2.0 * 32 * 32 * 64);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace w4a8

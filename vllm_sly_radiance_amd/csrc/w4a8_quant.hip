@@ -1,0 +1,165 @@
+// Dynamic per-token bf16 -> fp8 e4m3fn activation quantizer for gfx950.
+//
+// Semantics are those of the reference's pure-torch quantizer _traced_quant
+// (sly/mxfp4/radiance_mxfp4.py:392-396), evaluated in fp32 exactly as torch's CPU kernels do:
+//   s = max(amax(|x|) * fl32(1/448), 1/(448*512))      NaN in the row propagates to s
+//   q = e4m3_rne(clamp(x / s, -448, 448))               IEEE-correct fp32 division
+// One workgroup (4 wave64) per token. Each thread keeps its 16-byte chunks in registers across
+// the amax reduction, so the row is read from HBM once. The amax runs on the bf16 bit patterns
+// (|x| bits = x & 0x7FFF): integer max is exact, orders like the magnitudes and ranks NaN above
+// inf, which gives torch's NaN propagation for free. Wave64 butterfly, then LDS across waves.
+// Codes come from the hardware e4m3 converter (v_cvt_pk_fp8_f32, round to nearest even); inputs
+// are clamped first, so it never saturates. Rows whose scale is not finite (a NaN or inf in the
+// row) take a per-element path that maps every NaN quotient to the canonical code 0x7F.
+#include "w4a8_internal.h"
+
+namespace w4a8 {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr float kInv448 = 1.0f / 448.0f;            // fl32(1/448), folded at compile time
+constexpr float kMinScale = 1.0f / (448.0f * 512.0f);
+
+__device__ __forceinline__ uint32_t wave_max(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, 64));
+  return v;
+}
+
+// Row-wide max over the workgroup (all threads get the result).
+__device__ __forceinline__ uint32_t block_max(uint32_t v) {
+  __shared__ uint32_t red[kThreads / 64];
+  v = wave_max(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return max(max(red[0], red[1]), max(red[2], red[3]));
+}
+
+__device__ __forceinline__ uint32_t abs_bits_max8(const uint4 v) {
+  uint32_t m = max(v.x & 0x7FFFu, (v.x >> 16) & 0x7FFFu);
+  m = max(m, max(v.y & 0x7FFFu, (v.y >> 16) & 0x7FFFu));
+  m = max(m, max(v.z & 0x7FFFu, (v.z >> 16) & 0x7FFFu));
+  return max(m, max(v.w & 0x7FFFu, (v.w >> 16) & 0x7FFFu));
+}
+
+__device__ __forceinline__ float clamp448(float v) {
+  v = v > 448.0f ? 448.0f : v;                       // comparisons keep NaN
+  return v < -448.0f ? -448.0f : v;
+}
+
+__device__ __forceinline__ float lo_bf16(uint32_t d) { return __uint_as_float(d << 16); }
+__device__ __forceinline__ float hi_bf16(uint32_t d) { return __uint_as_float(d & 0xFFFF0000u); }
+
+// four quotients -> four e4m3 bytes (little-endian order: first value in byte 0)
+__device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
+}
+
+__device__ __forceinline__ uint32_t code1(float v) {
+  if (v != v) return 0x7Fu;
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v, v, 0, false) & 0xFFu;
+}
+
+__device__ __forceinline__ uint32_t pack4_any(float a, float b, float c, float d) {
+  return code1(a) | (code1(b) << 8) | (code1(c) << 16) | (code1(d) << 24);
+}
+
+template <bool kFinite>
+__device__ __forceinline__ uint32_t quant_dword(uint32_t d0, uint32_t d1, float s) {
+  const float a = clamp448(lo_bf16(d0) / s), b = clamp448(hi_bf16(d0) / s);
+  const float c = clamp448(lo_bf16(d1) / s), d = clamp448(hi_bf16(d1) / s);
+  return kFinite ? pack4(a, b, c, d) : pack4_any(a, b, c, d);
+}
+
+template <bool kFinite>
+__device__ __forceinline__ uint2 quant8(const uint4 v, float s) {
+  return make_uint2(quant_dword<kFinite>(v.x, v.y, s), quant_dword<kFinite>(v.z, v.w, s));
+}
+
+__device__ __forceinline__ float row_scale(uint32_t amax_bits) {
+  const float s = __uint_as_float(amax_bits << 16) * kInv448;
+  return s < kMinScale ? kMinScale : s;               // NaN stays NaN
+}
+
+__device__ __forceinline__ bool finite(float s) {
+  return (__float_as_uint(s) & 0x7F800000u) != 0x7F800000u;
+}
+
+// Vector path: 16-byte aligned rows, K % 8 == 0, K <= 8 * kThreads * CPT.
+template <int CPT>
+__global__ __launch_bounds__(kThreads) void quant_rows_vec(const uint16_t* __restrict__ x,
+                                                          long ldx, uint8_t* __restrict__ q,
+                                                          float* __restrict__ s, int K) {
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int nch = K >> 3;
+  const uint4* xr = reinterpret_cast<const uint4*>(x + (size_t)row * ldx);
+  uint4 v[CPT];
+  uint32_t am = 0;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = tid + i * kThreads;
+    v[i] = c < nch ? xr[c] : make_uint4(0, 0, 0, 0);
+    am = max(am, abs_bits_max8(v[i]));
+  }
+  const float sc = row_scale(block_max(am));
+  if (tid == 0) s[row] = sc;
+  uint2* qr = reinterpret_cast<uint2*>(q + (size_t)row * K);
+  if (finite(sc)) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + i * kThreads;
+      if (c < nch) qr[c] = quant8<true>(v[i], sc);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + i * kThreads;
+      if (c < nch) qr[c] = quant8<false>(v[i], sc);
+    }
+  }
+}
+
+// General path: any K, any alignment; reads the row twice (the second pass hits L2).
+__global__ __launch_bounds__(kThreads) void quant_rows_any(const uint16_t* __restrict__ x,
+                                                          long ldx, uint8_t* __restrict__ q,
+                                                          float* __restrict__ s, int K) {
+  const int row = blockIdx.x;
+  const uint16_t* xr = x + (size_t)row * ldx;
+  uint32_t am = 0;
+  for (int k = threadIdx.x; k < K; k += kThreads) am = max(am, (uint32_t)(xr[k] & 0x7FFFu));
+  const float sc = row_scale(block_max(am));
+  if (threadIdx.x == 0) s[row] = sc;
+  uint8_t* qr = q + (size_t)row * K;
+  for (int k = threadIdx.x; k < K; k += kThreads)
+    qr[k] = (uint8_t)code1(clamp448(__uint_as_float((uint32_t)xr[k] << 16) / sc));
+}
+
+}  // namespace
+
+hipError_t launch_quant(const uint16_t* x, long ldx, uint8_t* q, float* s, int M, int K,
+                        hipStream_t stream) {
+  if (M == 0) return hipSuccess;
+  const dim3 grid(M), block(kThreads);
+  const bool vec = K % 8 == 0 && ldx % 8 == 0 && ((uintptr_t)x % 16) == 0 &&
+                   ((uintptr_t)q % 8) == 0;
+  const int need = ceil_div(ceil_div(K, 8), kThreads);
+#define W4A8_QV(C) \
+  hipLaunchKernelGGL(quant_rows_vec<C>, grid, block, 0, stream, x, ldx, q, s, K)
+  if (vec && need <= 1) W4A8_QV(1);
+  else if (vec && need <= 2) W4A8_QV(2);
+  else if (vec && need <= 3) W4A8_QV(3);
+  else if (vec && need <= 4) W4A8_QV(4);
+  else if (vec && need <= 5) W4A8_QV(5);
+  else if (vec && need <= 6) W4A8_QV(6);
+  else if (vec && need <= 8) W4A8_QV(8);
+  else if (vec && need <= 10) W4A8_QV(10);
+  else if (vec && need <= 12) W4A8_QV(12);
+  else if (vec && need <= 16) W4A8_QV(16);
+  else hipLaunchKernelGGL(quant_rows_any, grid, block, 0, stream, x, ldx, q, s, K);
+#undef W4A8_QV
+  return hipGetLastError();
+}
+
+}  // namespace w4a8
