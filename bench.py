@@ -79,7 +79,8 @@ class Gemm:
 
 
 def per_launch_us(g, n, stream_obj):
-    """Average duration of single launches, each bracketed by its own HIP event pair."""
+    """Median and mean duration of single launches, each bracketed by its own HIP event pair on the
+    launch stream (includes the event overhead; a cross-check only)."""
     import torch
     st = stream_obj.cuda_stream
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
@@ -93,41 +94,50 @@ def per_launch_us(g, n, stream_obj):
     return float(np.median(t)), float(np.mean(t))
 
 
-def bench_verify(args):
+def graph_timed(g, steps, warmup):
+    """Capture one launch per weight copy into a HIP graph on a side stream, replay it on that same
+    stream (warmup, then the timed region) and return (steps run, warmup run, seconds, per-launch
+    event median/mean). The events bracket the timed replays on the stream the kernels run on."""
     import torch
-    M, N, K = VERIFY["M"], VERIFY["N"], VERIFY["K"]
-    g = Gemm(M, N, K, COPIES, seed=1)
     stream = torch.cuda.Stream()
+    n = len(g.w)
     torch.cuda.synchronize()
     with torch.cuda.stream(stream):
-        for i in range(4):
-            g.launch(i % COPIES, stream.cuda_stream)
+        for i in range(n):
+            g.launch(i, stream.cuda_stream)
     stream.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
-        for i in range(COPIES):
+        for i in range(n):
             g.launch(i, stream.cuda_stream)
-    reps = max(1, -(-args.steps // COPIES))
-    wreps = max(1, -(-args.warmup // COPIES))
-    for _ in range(wreps):
-        graph.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
+    reps = max(1, -(-steps // n))
+    wreps = max(1, -(-warmup // n))
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(reps):
-        graph.replay()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    steps = reps * COPIES
-    ms_per_step = e0.elapsed_time(e1) / steps
     with torch.cuda.stream(stream):
-        med_us, mean_us = per_launch_us(g, 256, stream)
+        for _ in range(wreps):
+            graph.replay()
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) * 1e-3
+    with torch.cuda.stream(stream):
+        med_us, mean_us = per_launch_us(g, 64, stream)
+    del graph
+    return reps * n, wreps * n, sec, med_us, mean_us
+
+
+def bench_verify(args):
+    M, N, K = VERIFY["M"], VERIFY["N"], VERIFY["K"]
+    g = Gemm(M, N, K, COPIES, seed=1)
+    steps, warm, sec, med_us, mean_us = graph_timed(g, args.steps, args.warmup)
     nbytes = gemm_bytes(M, N, K)
-    return dict(M=M, N=N, K=K, steps=steps, warmup=wreps * COPIES, ms_per_step=ms_per_step,
-                wall_s=wall, gbs=nbytes / (ms_per_step * 1e-3) / 1e9, bytes=nbytes,
-                kernel_us=mean_us, kernel_us_median=med_us, plan=g.plan)
+    us = sec / steps * 1e6
+    return dict(M=M, N=N, K=K, steps=steps, warmup=warm, ms_per_step=us * 1e-3,
+                gbs=nbytes / (us * 1e-6) / 1e9, bytes=nbytes, kernel_us=us,
+                event_pair_us_median=med_us, event_pair_us_mean=mean_us, plan=g.plan)
 
 
 def bench_prefill():
@@ -136,14 +146,11 @@ def bench_prefill():
     for name, M, N, K in PREFILL:
         copies = max(2, -(-512 * 2 ** 20 // (N * K * 17 // 32)))
         g = Gemm(M, N, K, copies, seed=7)
-        stream = torch.cuda.current_stream()
-        for i in range(3):
-            g.launch(i % copies, stream.cuda_stream)
-        med_us, mean_us = per_launch_us(g, 20, stream)
+        steps, _, sec, med_us, _ = graph_timed(g, 8 * copies, 2 * copies)
+        us = sec / steps * 1e6
         flop = 2.0 * M * N * K
-        tf = flop / (mean_us * 1e-6) / 1e12
-        res.append(dict(name=name, M=M, N=N, K=K, us=round(mean_us, 2),
-                        us_median=round(med_us, 2), tflops=round(tf, 1),
+        tf = flop / (us * 1e-6) / 1e12
+        res.append(dict(name=name, M=M, N=N, K=K, us=round(us, 2), tflops=round(tf, 1),
                         frac=round(tf / MFMA_PEAK_TFLOPS, 4), plan=g.plan))
         del g
         torch.cuda.empty_cache()
@@ -156,15 +163,13 @@ def bench_layer_m1():
     for name, N, K in LAYER_M1:
         copies = max(2, -(-512 * 2 ** 20 // (N * K * 17 // 32)))
         g = Gemm(1, N, K, copies, seed=3)
-        stream = torch.cuda.current_stream()
-        for i in range(3):
-            g.launch(i % copies, stream.cuda_stream)
-        med_us, mean_us = per_launch_us(g, 64, stream)
+        steps, _, sec, _, _ = graph_timed(g, 32 * copies, 4 * copies)
+        us = sec / steps * 1e6
         nb = gemm_bytes(1, N, K)
-        tot_us += mean_us
+        tot_us += us
         tot_bytes += nb
-        out.append(dict(name=name, N=N, K=K, us=round(mean_us, 2),
-                        gbs=round(nb / (mean_us * 1e-6) / 1e9, 1)))
+        out.append(dict(name=name, N=N, K=K, us=round(us, 2),
+                        gbs=round(nb / (us * 1e-6) / 1e9, 1), plan=g.plan))
         del g
         torch.cuda.empty_cache()
     return dict(layers=out, us_per_layer=round(tot_us, 2),
@@ -231,8 +236,9 @@ def main():
     from vllm_sly_radiance_amd import radiance_mxfp4 as R
     R.ensure_scratch(torch.device("cuda", 0))
     v = bench_verify(args)
-    print(f"[bench] verify M=8: {v['ms_per_step'] * 1e3:.2f} us/step (graph), kernel "
-          f"{v['kernel_us']:.2f} us (events), plan {v['plan']}", file=sys.stderr, flush=True)
+    print(f"[bench] verify M=8: {v['kernel_us']:.2f} us/launch in the graph-timed region, "
+          f"event pairs {v['event_pair_us_median']:.2f} us median, plan {v['plan']}",
+          file=sys.stderr, flush=True)
     prefill = layer = None
     if not args.only_verify:
         prefill = bench_prefill()
@@ -264,7 +270,7 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
         "cpu_baseline": cpu,
         "kernel_us": round(v["kernel_us"], 3),
-        "kernel_us_median": round(v["kernel_us_median"], 3),
+        "event_pair_us_median": round(v["event_pair_us_median"], 3),
         "prefill_m4096": prefill,
         "mfma_probe_tflops": probe,
         "decode_m1_layer": layer,

@@ -116,6 +116,15 @@ int w4a8_linear(const void* x, long ldx, void* q, float* scale, const void* wq, 
  * sly/mxfp4/radiance_mxfp4_fp8.hip:6-10. */
 int w4a8_mfma_probe(int shape, float* out, int blocks, int iters, double* flop, void* stream);
 
+/* Diagnostic: `count` independent scaled MFMAs (16x16x128, fp4 e2m1 A x fp8 e4m3 B, the instruction
+ * every GEMM here issues) on raw lane operands, one wave per tile: a [count][64][4] dwords (16 fp4
+ * bytes per lane), b [count][64][8] dwords (32 fp8 bytes per lane), sa / sb [count][64] scale
+ * dwords (byte 0 used), d [count][64][4] fp32 result registers. Pins the host model of the operand
+ * layout to the hardware, as the reference confirmed its gfx1201 WMMA fragment layout empirically
+ * (sly/mxfp4/radiance_mxfp4_fp8.hip:24-25). */
+int w4a8_mfma_tile(const void* a, const void* b, const void* sa, const void* sb, float* d,
+                   int count, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -137,20 +137,33 @@ def test_mfma_model_detects_a_transposed_lane_map():
 
 def test_mfma_tile_one_hot_lane_map():
     # one nonzero per operand: D must light up exactly at the documented (row, col)
-    from oracle.mxfp4_oracle import E2M1_VALUES
     a = np.zeros((64, 16), np.uint8)
     b = np.zeros((64, 32), np.uint8)
-    a[16 * 2 + 11, 3] = 0x70         # A[row 11][k = 64 + 7] = 6.0 (odd k -> high nibble of byte 3)
-    b[16 * 2 + 5, 7] = 0x38          # B[k = 64 + 7][col 5] = 1.0
-    unit = np.full(64, 127, np.uint8)
-    D = MM.mfma_tile(MM.fp4_lane_values(a, unit), MM.fp8_lane_values(b, unit))
+    a[16 * 1 + 11, 3] = 0x70         # A[row 11][k = 32 + 7] = 6.0 (odd k -> high nibble of byte 3)
+    b[16 * 2 + 5, 7] = 0x38          # B[k = 16*2 + 7][col 5] = 1.0 (low run of lane 37)
+    D = MM.mfma_tile(MM.fp4_lane_values(a), MM.fp8_lane_values(b))
     assert D[11, 5] == 6.0 and np.count_nonzero(D) == 1
     r, c = MM.d_lane_map()
     lanes = MM.d_to_lanes(D)
     lane, reg = np.argwhere(lanes != 0)[0]
     assert (r[lane, reg], c[lane, reg]) == (11, 5) and lane == 16 * 2 + 5 and reg == 3
-    # the A-operand scale byte of lane 43 scales exactly that element
-    sa = unit.copy()
-    sa[16 * 2 + 11] = 130
-    D2 = MM.mfma_tile(MM.fp4_lane_values(a, sa), MM.fp8_lane_values(b, unit))
-    assert D2[11, 5] == 48.0 and E2M1_VALUES[7] == 6.0
+    # the scale of (row 11, block 1) lives in A lane 27; that of (col 5, block 1) in B lane 21
+    unit = np.full(64, 127, np.uint8)
+    sa, sb = unit.copy(), unit.copy()
+    sa[16 * 1 + 11] = 130
+    sb[16 * 1 + 5] = 128
+    assert MM.mfma_tile(MM.fp4_lane_values(a), MM.fp8_lane_values(b), sa, sb)[11, 5] == 96.0
+    sb2 = unit.copy()
+    sb2[16 * 2 + 5] = 128            # B lane 37's own scale byte covers block 2, not this element
+    assert MM.mfma_tile(MM.fp4_lane_values(a), MM.fp8_lane_values(b), None, sb2)[11, 5] == 6.0
+
+
+def test_mfma_fp8_lane_upper_run_is_k_plus_64():
+    # byte 16 + j of B lane l is k = 64 + 16*(l // 16) + j: lane 5, byte 20 -> k = 68 (block 2),
+    # which meets nibble 4 of A lane 2*16 + row
+    a = np.zeros((64, 16), np.uint8)
+    b = np.zeros((64, 32), np.uint8)
+    b[5, 20] = 0x40                  # 2.0 at (k 68, col 5)
+    a[32 + 9, 2] = 0x05              # 3.0 at (row 9, k 64 + 4), low nibble of byte 2
+    D = MM.mfma_tile(MM.fp4_lane_values(a), MM.fp8_lane_values(b))
+    assert D[9, 5] == 6.0 and np.count_nonzero(D) == 1

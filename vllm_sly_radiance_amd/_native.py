@@ -38,6 +38,7 @@ SIGNATURES = {
     "w4a8_scratch_bytes": (_int, [_int, _int, _int, _psz, _psz]),
     "w4a8_linear": (_int, [_vp, _long, _vp, _vp, _vp, _vp, _vp, _int, _int, _int, _vp]),
     "w4a8_mfma_probe": (_int, [_int, _vp, _int, _int, _c.POINTER(_c.c_double), _vp]),
+    "w4a8_mfma_tile": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _vp]),
 }
 
 _lock = threading.Lock()
@@ -131,3 +132,7 @@ def mfma_probe(shape, out_ptr, blocks, iters, stream) -> float:
     f = _c.c_double()
     check(lib().w4a8_mfma_probe(shape, out_ptr, blocks, iters, _c.byref(f), stream))
     return f.value
+
+
+def mfma_tile(a_ptr, b_ptr, sa_ptr, sb_ptr, d_ptr, count, stream):
+    check(lib().w4a8_mfma_tile(a_ptr, b_ptr, sa_ptr, sb_ptr, d_ptr, count, stream))

@@ -281,3 +281,16 @@ W4A8_API int w4a8_mfma_probe(int shape, float* out, int blocks, int iters, doubl
   return hip_status(launch_mfma_probe(shape, out, blocks, iters, flop, (hipStream_t)stream),
                     "w4a8_mfma_probe");
 }
+
+W4A8_API int w4a8_mfma_tile(const void* a, const void* b, const void* sa, const void* sb, float* d,
+                            int count, void* stream) {
+  if (count < 0 || count > (1 << 24))
+    return fail(W4A8_EINVAL, "w4a8_mfma_tile: count=%d outside 0..2^24", count);
+  if (count == 0) return W4A8_OK;
+  if (!a || !b || !sa || !sb || !d) return fail(W4A8_EINVAL, "w4a8_mfma_tile: null pointer");
+  if (!aligned(a, 4) || !aligned(b, 4) || !aligned(sa, 4) || !aligned(sb, 4) || !aligned(d, 4))
+    return fail(W4A8_EINVAL, "w4a8_mfma_tile: operands need 4-byte alignment");
+  return hip_status(launch_mfma_tiles((const int*)a, (const int*)b, (const int*)sa,
+                                      (const int*)sb, d, count, (hipStream_t)stream),
+                    "w4a8_mfma_tile");
+}

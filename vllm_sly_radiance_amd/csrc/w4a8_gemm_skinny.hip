@@ -5,7 +5,8 @@
 //  * A workgroup owns NT n-tiles (16 columns each) and one K split; its WAVES waves take the
 //    split's k-tiles round-robin, so at any moment the waves of a workgroup stream adjacent 1 KiB
 //    granules. Each wave issues U k-tiles of loads (NT non-temporal 128-bit weight loads per k-tile,
-//    the scale dword, MT activation fragments that hit L2) before the U*MT*NT scaled MFMAs.
+//    the scale dword, MT activation fragments of two 128-bit loads each that hit L2) before the
+//    U*MT*NT scaled MFMAs.
 //  * The e8m0 block scale goes to the MFMA as the A-operand scale byte (the reference folds it into
 //    the weight byte through kMag, exact only for exponent gaps <= 8; this is exact always).
 //  * Waves reduce through LDS in wave order; K splits across workgroups (split_k > 1, used when N
@@ -65,8 +66,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny(
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
         const int m = i * 16 + xm;
-        const int kk = k * kKTile + xkb * 32;
-        if (kin && m < M && kk < K) xv[u][i] = load_v8i(A + (size_t)m * K + kk);
+        if (kin && m < M) xv[u][i] = load_x_frag(A + (size_t)m * K, k * kKTile, xkb, K);
         else xv[u][i] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
       }
     }

@@ -4,8 +4,9 @@
 // (sly/mxfp4/radiance_mxfp4_fp8.hip:326-590, :664-944), redesigned for CDNA4:
 //  * 4 wave64 in a 2 x 2 arrangement; each wave owns WM x WN MFMA tiles of 16 tokens x 16 columns,
 //    so the workgroup tile is (32 WM) tokens x (32 WN) columns, one 128-k slab per stage.
-//  * Stage = the activation slab in MFMA fragment order ([16-token block][half][lane][16 B]) plus
-//    the weight granules copied verbatim. Global loads are 128-bit and coalesced (granules are
+//  * Stage = the activation slab in MFMA fragment order ([16-token block][run][lane][16 B]; run 0
+//    holds k 16g..16g+15 and run 1 holds k 64+16g.. of fragment lane 16g + token) plus the weight
+//    granules copied verbatim. Global loads are 128-bit and coalesced (granules are
 //    contiguous 1 KiB; an activation row contributes 64 contiguous bytes per 16-lane group) and
 //    every LDS write and ds_read_b128 touches 16 consecutive 16-byte slots per quarter-wave, so
 //    neither side has bank conflicts. Two stages alternate with one barrier per slab; the next
@@ -96,7 +97,8 @@ __global__ __launch_bounds__(kThreads) void gemm_tile(
     for (int c = 0; c < S::A_CHUNKS; ++c) {
       const int ch = tid + c * kThreads;
       const int r16 = ch & 15, cc = (ch >> 4) & 7, rb = ch >> 7;
-      *reinterpret_cast<uint4*>(sA + rb * 2048 + (cc & 1) * 1024 + ((cc >> 1) * 16 + r16) * 16) =
+      // 16-byte column cc (k = 16 cc ..) of row r16 is run cc >> 2 of fragment lane (cc & 3) * 16 + r16
+      *reinterpret_cast<uint4*>(sA + rb * 2048 + (cc >> 2) * 1024 + ((cc & 3) * 16 + r16) * 16) =
           ra[c];
     }
     uint8_t* sW = sA + S::A_BYTES;

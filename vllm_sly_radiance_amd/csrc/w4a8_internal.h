@@ -9,9 +9,12 @@
 // per-lane A-scale byte is exactly the scale of that lane's block.
 //
 // Activations are row-major e4m3 [M, K] with one fp32 scale per token; the activation fragment is
-// the MFMA's fp8 B operand (lane l: token m0 + l % 16, block k0/32 + l/16, 32 bytes) with scale
-// byte 127, and the per-token scale is applied in the epilogue. D = W . X^T, so lane l, register
-// i holds output (token m0 + l % 16, column n0 + 4*(l/16) + i): four consecutive bf16 per lane.
+// the MFMA's fp8 B operand with scale byte 127, and the per-token scale is applied in the
+// epilogue. The fp8 operand does not follow the fp4 one: lane l (token m0 + l % 16, g = l / 16)
+// holds two 16-byte runs of its row, k0 + 16g .. +15 in bytes 0-15 and k0 + 64 + 16g .. +15 in
+// bytes 16-31 (measured on MI355X with one-hot operands). With unit activation scales the block
+// association of those runs does not matter. D = W . X^T, so lane l, register i holds output
+// (token m0 + l % 16, column n0 + 4*(l/16) + i): four consecutive bf16 per lane.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stddef.h>
@@ -54,10 +57,13 @@ __device__ __forceinline__ v4i load_v4i_stream(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
 }
 
-// The 32 activation bytes of one B-operand lane (two 128-bit loads).
-__device__ __forceinline__ v8i load_v8i(const void* p) {
-  const v4i lo = reinterpret_cast<const v4i*>(p)[0];
-  const v4i hi = reinterpret_cast<const v4i*>(p)[1];
+// The 32 activation bytes of one fp8 B-operand lane of the k-tile starting at k0: two 128-bit
+// loads, row[k0 + 16g ..] and row[k0 + 64 + 16g ..], each zero past K (K is a multiple of 32, so
+// a run is either wholly inside the row or wholly past it). row must be 16-byte aligned.
+__device__ __forceinline__ v8i load_x_frag(const uint8_t* row, int k0, int g, int K) {
+  const int ka = k0 + 16 * g, kb = ka + 64;
+  const v4i lo = ka < K ? *reinterpret_cast<const v4i*>(row + ka) : v4i{0, 0, 0, 0};
+  const v4i hi = kb < K ? *reinterpret_cast<const v4i*>(row + kb) : v4i{0, 0, 0, 0};
   return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
@@ -110,5 +116,8 @@ hipError_t launch_tile(const GemmArgs& g, int variant, hipStream_t stream);
 // Register-resident MFMA throughput probe (shape 0: 16x16x128, 1: 32x32x64).
 hipError_t launch_mfma_probe(int shape, float* out, int blocks, int iters, double* flop,
                              hipStream_t stream);
+// Raw scaled-MFMA tiles on caller-given lane operands (layout diagnostic).
+hipError_t launch_mfma_tiles(const int* a, const int* b, const int* sa, const int* sb, float* d,
+                             int count, hipStream_t stream);
 
 }  // namespace w4a8

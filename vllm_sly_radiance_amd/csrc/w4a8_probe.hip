@@ -52,7 +52,38 @@ __global__ __launch_bounds__(256) void mfma_rate_32x32x64(float* out, int iters)
   if ((l & 63) == 0) out[blockIdx.x * 4 + (l >> 6)] = s;
 }
 
+// One wave per tile t < count: D = the scaled MFMA of raw lane operands, as the GEMMs issue it
+// (fp4 A, fp8 B, scale byte 0 of each lane's scale dword).
+__global__ __launch_bounds__(256) void mfma_tiles(const int* __restrict__ a,
+                                                 const int* __restrict__ b,
+                                                 const int* __restrict__ sa,
+                                                 const int* __restrict__ sb,
+                                                 float* __restrict__ d, int count) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
+  if (t >= count) return;
+  const size_t tl = (size_t)t * 64 + l;
+  const int* pa = a + tl * 4;
+  const int* pb = b + tl * 8;
+  const v4i av = {pa[0], pa[1], pa[2], pa[3]};
+  const v8i bv = {pb[0], pb[1], pb[2], pb[3], pb[4], pb[5], pb[6], pb[7]};
+  const v8i a8 = {av[0], av[1], av[2], av[3], 0, 0, 0, 0};
+  const v4f acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+      a8, bv, v4f{0.f, 0.f, 0.f, 0.f}, 4, 0, 0, sa[tl], 0, sb[tl]);
+  float* pd = d + tl * 4;
+  pd[0] = acc[0];
+  pd[1] = acc[1];
+  pd[2] = acc[2];
+  pd[3] = acc[3];
+}
+
 }  // namespace
+
+hipError_t launch_mfma_tiles(const int* a, const int* b, const int* sa, const int* sb, float* d,
+                             int count, hipStream_t stream) {
+  hipLaunchKernelGGL(mfma_tiles, dim3((unsigned)ceil_div(count, 4)), dim3(256), 0, stream, a, b,
+                     sa, sb, d, count);
+  return hipGetLastError();
+}
 
 // Launches `blocks` workgroups of 4 waves; returns the FLOP the launch performs in *flop.
 hipError_t launch_mfma_probe(int shape, float* out, int blocks, int iters, double* flop,
