@@ -35,7 +35,7 @@ enum {
   W4A8_EHIP = 3       /* the HIP runtime reported an error at launch */
 };
 
-enum { W4A8_KERNEL_AUTO = 0, W4A8_KERNEL_SKINNY = 1, W4A8_KERNEL_TILE = 2 };
+enum { W4A8_KERNEL_AUTO = 0, W4A8_KERNEL_SKINNY = 1, W4A8_KERNEL_TILE = 2, W4A8_KERNEL_STREAM = 3 };
 
 /* ABI version of the loaded library (W4A8_ABI_VERSION). */
 int w4a8_abi_version(void);
@@ -95,7 +95,10 @@ int w4a8_gemm_planned(const void* a, const float* a_scale, const void* wq, const
 
 /* Number of instantiated variants of a kernel family, and their parameters:
  * skinny: p = {MT (16-token fragments), NT (n-tiles per workgroup), waves, unroll};
- * tile:   p = {WM, WN (MFMA tiles per wave), BM, BN (workgroup tile)}. */
+ * tile:   p = {WM, WN (MFMA tiles per wave), BM, BN (workgroup tile)};
+ * stream: p = {MT, U (granules per wave at most), waves, activation chunks per thread}. A stream
+ *         variant serves (M, N, K) only when a wave's run fits U and the activations fit its LDS
+ *         and register staging; forcing one that does not returns W4A8_EINVAL. */
 int w4a8_variant_count(int kernel);
 int w4a8_variant_info(int kernel, int variant, int* p0, int* p1, int* p2, int* p3);
 

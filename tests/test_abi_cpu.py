@@ -106,15 +106,22 @@ def test_split_k_without_scratch_is_refused(lib):
 
 def test_plan_bands(lib):
     k, v, s = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
-    for M, kernel in [(1, 1), (8, 1), (64, 1), (65, 2), (4096, 2)]:
-        assert lib.w4a8_plan(M, 17408, 5120, ctypes.byref(k), ctypes.byref(v), ctypes.byref(s)) == 0
-        assert k.value == kernel and v.value >= 0 and s.value >= 1
+    # M <= 16: the streaming family when a wave's run and the LDS staging fit; then skinny to 64;
+    # then macro-tile. N=17408 K=8704 would need 43-granule runs, past the largest stream variant;
+    # K=640 has fewer k-tiles per n-tile than the smallest run.
+    for M, N, K, kernel in [(1, 17408, 5120, 3), (8, 17408, 5120, 3), (16, 17408, 5120, 3),
+                            (8, 5120, 8704, 3), (8, 17408, 8704, 1), (8, 33, 640, 1),
+                            (17, 17408, 5120, 1), (64, 17408, 5120, 1), (65, 17408, 5120, 2),
+                            (4096, 17408, 5120, 2)]:
+        assert lib.w4a8_plan(M, N, K, ctypes.byref(k), ctypes.byref(v), ctypes.byref(s)) == 0
+        assert (M, N, K, k.value) == (M, N, K, kernel) and v.value >= 0 and s.value >= 1
     assert lib.w4a8_plan(8, 17408, 5000, ctypes.byref(k), ctypes.byref(v), ctypes.byref(s)) == 1
 
 
 def test_variant_tables(lib):
     sk = [(lib.w4a8_variant_count(1))]
     assert sk[0] > 0 and lib.w4a8_variant_count(2) > 0 and lib.w4a8_variant_count(9) == -1
+    assert lib.w4a8_variant_count(3) > 0
     a = [ctypes.c_int() for _ in range(4)]
     assert lib.w4a8_variant_info(2, 0, *[ctypes.byref(x) for x in a]) == 0
     wm, wn, bm, bn = (x.value for x in a)

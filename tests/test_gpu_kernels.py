@@ -18,7 +18,7 @@ from vllm_sly_radiance_amd import _native, synthetic
 
 pytestmark = pytest.mark.gpu
 
-SKINNY, TILE = _native.KERNEL_SKINNY, _native.KERNEL_TILE
+SKINNY, TILE, STREAM = _native.KERNEL_SKINNY, _native.KERNEL_TILE, _native.KERNEL_STREAM
 
 
 @pytest.fixture(scope="module")
@@ -291,6 +291,30 @@ def test_gemm_every_skinny_variant_and_split(gpu_lib, scratch):
         for ks in (1, 2, 4, 7):
             out = gpu_gemm(q, s, wq, sq, N, K, SKINNY, v, ks)
             assert_gemm_close(out, q, s, w, ws, f"variant {v} {(mt, nt, waves, unroll)} split {ks}")
+
+
+@pytest.mark.parametrize("N,K", [(17408, 5120), (1040, 2560), (33, 640), (10240, 96), (5120, 6144),
+                                 (5120, 8704), (48, 5120)])
+def test_gemm_every_stream_variant(gpu_lib, N, K):
+    """The streaming family (M <= 16) at every variant that serves (M, N, K), ragged M and N.
+    Shapes no variant serves (a run longer than the k-tiles of an n-tile: K=640, K=96) must be
+    refused by every variant and planned on another family."""
+    w, ws = cached_weights(N, K, N + 7 * K)
+    wq, sq = gpu_repack(w, ws)
+    served = any(_native.plan(M, N, K)[0] == STREAM for M in (1, 8, 16))
+    ran = 0
+    for M in (1, 3, 8, 13, 16):
+        x = synthetic.activations(M, K, seed=M + K)
+        q, s = O.quant_per_token(x)
+        for v, cfg in enumerate(_native.variants(STREAM)):
+            try:
+                out = gpu_gemm(q, s, wq, sq, N, K, STREAM, v, 1)
+            except RuntimeError as e:
+                assert "does not serve" in str(e)
+                continue
+            ran += 1
+            assert_gemm_close(out, q, s, w, ws, f"M={M} N={N} K={K} stream variant {v} {cfg}")
+    assert (ran > 0) == served
 
 
 @pytest.mark.parametrize("M,N,K", [(65, 544, 1024), (300, 1040, 2560), (1000, 17408 // 8, 5120),

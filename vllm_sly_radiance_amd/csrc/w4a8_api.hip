@@ -47,6 +47,32 @@ int current_device() {
   return d;
 }
 
+// Compute units and the dynamic LDS a workgroup may use, per device, queried once. Without a
+// device (planning on a host) the MI355X figures apply: 256 CUs, 160 KiB of LDS per workgroup.
+struct DeviceInfo {
+  int cus = 256;
+  size_t lds = 160 * 1024;
+};
+DeviceInfo g_devinfo[kMaxDevices];
+bool g_devinfo_set[kMaxDevices];
+
+DeviceInfo device_info(int dev) {
+  if (dev < 0) return DeviceInfo{};
+  if (!g_devinfo_set[dev]) {
+    DeviceInfo d;
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        v > 0)
+      d.cus = v;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess &&
+        v > 0)
+      d.lds = (size_t)v;
+    g_devinfo[dev] = d;
+    g_devinfo_set[dev] = true;
+  }
+  return g_devinfo[dev];
+}
+
 int check_gemm_shape(const char* who, int M, int N, int K) {
   if (M < 0 || N <= 0 || K <= 0)
     return fail(W4A8_EINVAL, "%s: need M >= 0, N > 0, K > 0 (got M=%d N=%d K=%d)", who, M, N, K);
@@ -91,9 +117,31 @@ bool scratch_fits(int dev, int variant, int N, int split_k) {
          (size_t)skinny_counter_count(variant, N) * sizeof(int) <= s.counter_bytes;
 }
 
-// Decode / verify band: M <= 64 streams the weights once. The workgroup count should cover the
-// 256 CUs several times over; for small N the K dimension is split across workgroups too.
+// The smallest stream variant that serves (M, N, K): fewest registers held per wave.
+int find_stream(int M, int N, int K, int dev) {
+  const DeviceInfo d = device_info(dev);
+  int best = -1;
+  for (int v = 0; v < stream_variant_count(); ++v)
+    if (stream_fits(v, M, N, K, d.cus, d.lds) &&
+        (best < 0 || stream_variant(v).t < stream_variant(best).t))
+      best = v;
+  return best;
+}
+
+// Decode / verify band: M <= 64 streams the weights once. M <= 16 takes the streaming family
+// when a variant fits (whole-K workgroups, every weight load in flight at once); otherwise the
+// skinny family, whose workgroup count should cover the 256 CUs several times over; for small N
+// the K dimension is split across workgroups too.
 void plan_impl(int M, int N, int K, int dev, int* kernel, int* variant, int* split_k) {
+  if (M <= 16) {
+    const int v = find_stream(M, N, K, dev);
+    if (v >= 0) {
+      *kernel = W4A8_KERNEL_STREAM;
+      *variant = v;
+      *split_k = 1;
+      return;
+    }
+  }
   if (M <= 64) {
     const int mt = M <= 16 ? 1 : ceil_div(M, 16);
     const int ntiles = padded_n(N) / kNTile;
@@ -148,6 +196,15 @@ int gemm_dispatch(const void* a, const float* as, const void* wq, const void* sq
     if (variant < 0 || variant >= tile_variant_count())
       return fail(W4A8_EINVAL, "w4a8_gemm: tile variant %d out of range", variant);
     return hip_status(launch_tile(g, variant, st), "w4a8_gemm");
+  }
+  if (kernel == W4A8_KERNEL_STREAM) {
+    if (variant < 0 || variant >= stream_variant_count())
+      return fail(W4A8_EINVAL, "w4a8_gemm: stream variant %d out of range", variant);
+    const DeviceInfo d = device_info(current_device());
+    if (!stream_fits(variant, M, N, K, d.cus, d.lds))
+      return fail(W4A8_EINVAL, "w4a8_gemm: stream variant %d does not serve M=%d N=%d K=%d",
+                  variant, M, N, K);
+    return hip_status(launch_stream(g, variant, d.cus, st), "w4a8_gemm");
   }
   return fail(W4A8_EINVAL, "w4a8_gemm: unknown kernel %d", kernel);
 }
@@ -233,6 +290,7 @@ W4A8_API int w4a8_gemm(const void* a, const float* a_scale, const void* wq, cons
 W4A8_API int w4a8_variant_count(int kernel) {
   if (kernel == W4A8_KERNEL_SKINNY) return skinny_variant_count();
   if (kernel == W4A8_KERNEL_TILE) return tile_variant_count();
+  if (kernel == W4A8_KERNEL_STREAM) return stream_variant_count();
   fail(W4A8_EINVAL, "w4a8_variant_count: unknown kernel %d", kernel);
   return -1;
 }
@@ -245,6 +303,9 @@ W4A8_API int w4a8_variant_info(int kernel, int variant, int* p0, int* p1, int* p
   } else if (kernel == W4A8_KERNEL_TILE && variant >= 0 && variant < tile_variant_count()) {
     const TileCfg c = tile_variant(variant);
     v[0] = c.wm; v[1] = c.wn; v[2] = c.bm; v[3] = c.bn;
+  } else if (kernel == W4A8_KERNEL_STREAM && variant >= 0 && variant < stream_variant_count()) {
+    const StreamCfg c = stream_variant(variant);
+    v[0] = c.mt; v[1] = c.t; v[2] = c.waves; v[3] = c.am;
   } else {
     return fail(W4A8_EINVAL, "w4a8_variant_info: no variant %d of kernel %d", variant, kernel);
   }

@@ -51,6 +51,11 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
   return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
+// Word 3 of a raw (stride 0) buffer resource on gfx9-family GPUs: 32-bit data format, no swizzle.
+// Loads through such a resource return 0 for offsets at or past num_records, without a memory access.
+constexpr int kBufferWord3 = 0x00020000;
+constexpr int kBufferNT = 2;                    // cache-policy operand: non-temporal (streamed once)
+
 __device__ __forceinline__ v4i load_v4i(const void* p) { return *reinterpret_cast<const v4i*>(p); }
 
 __device__ __forceinline__ v4i load_v4i_stream(const void* p) {
@@ -106,6 +111,19 @@ size_t skinny_scratch_bytes(int variant, int N, int split_k);
 int skinny_counter_count(int variant, int N);
 hipError_t launch_skinny(const GemmArgs& g, int variant, int split_k, float* partial,
                          int* counters, hipStream_t stream);
+
+// Streaming family (M <= 16, K % 512 == 0): grid = min(n-tiles, CUs), waves = (n-tile, K split)
+// pairs holding at most t granules each, activations staged in LDS. variant indexes the
+// instantiated table; mt = staged activation rows (8 or 16, M <= mt), am = activation chunks per
+// thread.
+struct StreamCfg { int mt, t, waves, am; };
+int stream_variant_count();
+StreamCfg stream_variant(int v);
+int stream_grid(int N, int cus);
+size_t stream_lds_bytes(int variant, int M, int K);
+int stream_splits(int variant, int N, int K, int cus);
+bool stream_fits(int variant, int M, int N, int K, int cus, size_t lds_limit);
+hipError_t launch_stream(const GemmArgs& g, int variant, int cus, hipStream_t stream);
 
 // Macro-tile family (large M). variant indexes the instantiated (WM, WN) table.
 struct TileCfg { int wm, wn, bm, bn; };
