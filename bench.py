@@ -50,6 +50,10 @@ def parse():
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only-verify", action="store_true", help="skip prefill and M=1 legs")
+    ap.add_argument("--profile", action="store_true",
+                    help="counter-run workload: the verify-GEMM graph replay, 4 launches of each "
+                         "prefill GEMM and one 256 MiB device copy (the counter calibration); "
+                         "prints no JSON")
     return ap.parse_args()
 
 
@@ -221,6 +225,50 @@ def cpu_baseline():
                       f"{sec:.3f} s per GEMM"}
 
 
+CALIBRATION_BYTES = 256 * 2 ** 20
+
+
+def profile_workload():
+    """The launches the committed rocprofv3 summaries are taken on: the verify GEMM (the bench's
+    graph replay: 16 warmup + 64 timed launches over 16 weight copies, plus 64 event-bracketed
+    single launches), each prefill GEMM (4 launches) and a plain 256 MiB device copy
+    (torch's copy kernel), whose FETCH_SIZE / WRITE_SIZE readings calibrate the counters: a copy
+    of B bytes fetches B and writes B."""
+    import torch
+    from vllm_sly_radiance_amd import radiance_mxfp4 as R
+    R.ensure_scratch(torch.device("cuda", 0))
+    st = torch.cuda.current_stream()
+    M, N, K = VERIFY["M"], VERIFY["N"], VERIFY["K"]
+    g = Gemm(M, N, K, COPIES, seed=1)
+    graph_timed(g, 64, 16)            # the same graph replay the bench times
+    del g
+    for _, M, N, K in PREFILL:
+        g = Gemm(M, N, K, 2, seed=7)
+        for i in range(4):
+            g.launch(i % 2, st.cuda_stream)
+        torch.cuda.synchronize()
+        del g
+    torch.cuda.empty_cache()
+    src = torch.ones(CALIBRATION_BYTES // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"[bench] profile workload done (calibration copy {CALIBRATION_BYTES} B)",
+          file=sys.stderr)
+
+
+def measured_traffic(kernel_prefix):
+    """HBM bytes per launch of the verify GEMM from the committed counter summary, or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+        k = t["kernels"][kernel_prefix]
+        return int(round(k["fetch_bytes"] + k["write_bytes"]))
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -234,6 +282,9 @@ def main():
         sys.exit(1)
     torch.cuda.set_device(0)
     from vllm_sly_radiance_amd import radiance_mxfp4 as R
+    if args.profile:
+        profile_workload()
+        return
     R.ensure_scratch(torch.device("cuda", 0))
     v = bench_verify(args)
     print(f"[bench] verify M=8: {v['kernel_us']:.2f} us/launch in the graph-timed region, "
@@ -267,7 +318,8 @@ def main():
                    "M": 8, "N": 17408, "K": 5120, "weight_copies": COPIES,
                    "plan": list(v["plan"])},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic("verify")},
         "cpu_baseline": cpu,
         "kernel_us": round(v["kernel_us"], 3),
         "event_pair_us_median": round(v["event_pair_us_median"], 3),
