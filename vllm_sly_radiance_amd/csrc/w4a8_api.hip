@@ -158,8 +158,13 @@ void plan_impl(int M, int N, int K, int dev, int* kernel, int* variant, int* spl
     *split_k = ks;
     return;
   }
+  // Prefill band (measured on MI355X): 128 x 256 tiles for wide N, 256 x 160 where N divides into
+  // 160-column tiles that fill the CUs evenly (N = 5120: 512 tiles at M = 4096), 128 x 128 below.
   *kernel = W4A8_KERNEL_TILE;
-  *variant = M >= 2048 ? find_tile(8, 4) : M >= 512 ? find_tile(4, 4) : find_tile(2, 4);
+  if (M >= 2048 && N % 160 == 0 && N <= 8192) *variant = find_tile(8, 5);
+  else if (M >= 2048) *variant = find_tile(4, 8);
+  else if (M >= 256) *variant = find_tile(4, 4);
+  else *variant = find_tile(2, 4);
   *split_k = 1;
 }
 
@@ -195,6 +200,9 @@ int gemm_dispatch(const void* a, const float* as, const void* wq, const void* sq
   if (kernel == W4A8_KERNEL_TILE) {
     if (variant < 0 || variant >= tile_variant_count())
       return fail(W4A8_EINVAL, "w4a8_gemm: tile variant %d out of range", variant);
+    if (!tile_fits(M, N, K))
+      return fail(W4A8_EINVAL, "w4a8_gemm: M=%d K=%d exceeds the tile kernel's 32-bit offsets", M,
+                  K);
     return hip_status(launch_tile(g, variant, st), "w4a8_gemm");
   }
   if (kernel == W4A8_KERNEL_STREAM) {

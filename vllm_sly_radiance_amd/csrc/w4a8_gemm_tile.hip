@@ -1,22 +1,26 @@
-// Macro-tile W4A8 GEMM for prefill M on gfx950: LDS double-buffered scaled-MFMA tiles.
+// Macro-tile W4A8 GEMM for prefill M on gfx950: scaled-MFMA tiles fed by an NS-stage LDS pipeline
+// that the loads fill directly (buffer_load ... lds), with no register staging.
 //
 // Counterpart of the reference's folded / A-tiled prefill kernels
 // (sly/mxfp4/radiance_mxfp4_fp8.hip:326-590, :664-944), redesigned for CDNA4:
-//  * 4 wave64 in a 2 x 2 arrangement; each wave owns WM x WN MFMA tiles of 16 tokens x 16 columns,
-//    so the workgroup tile is (32 WM) tokens x (32 WN) columns, one 128-k slab per stage.
-//  * Stage = the activation slab in MFMA fragment order ([16-token block][run][lane][16 B]; run 0
-//    holds k 16g..16g+15 and run 1 holds k 64+16g.. of fragment lane 16g + token) plus the weight
-//    granules copied verbatim. Global loads are 128-bit and coalesced (granules are
-//    contiguous 1 KiB; an activation row contributes 64 contiguous bytes per 16-lane group) and
-//    every LDS write and ds_read_b128 touches 16 consecutive 16-byte slots per quarter-wave, so
-//    neither side has bank conflicts. Two stages alternate with one barrier per slab; the next
-//    slab's global loads are in flight while the current slab's MFMAs issue.
-//  * The e8m0 scale dwords go straight from global (L2) to registers, one per n-fragment, issued
-//    a slab ahead; the MFMA applies them, so no dequantisation happens anywhere.
+//  * 4 wave64 in a 2 x 2 arrangement; each wave owns WM x WN MFMA tiles of 16 tokens x 16
+//    columns (up to 128 x 128 per wave), so the workgroup tile is (32 WM) tokens x (32 WN) columns
+//    and a 128-k slab is 32 WM * 128 B of activations, 2 WN weight granules and their scale dwords.
+//  * Each slab is fragment-ordered in LDS: one load instruction moves one 1 KiB unit - a weight
+//    granule verbatim, or one run of a 16-token activation fragment (lane l = 16 g + row, k 16g..
+//    or 64 + 16g..) - and the LDS-direct form writes lane l's 16 bytes at unit + 16 l, so both the
+//    fills and the ds_read_b128 fragment reads are 1 KiB contiguous per wave and conflict-free.
+//  * The fills go straight from memory to LDS, so the pipeline depth costs LDS, not registers:
+//    NS stages, slab k+NS-1 requested while slab k is multiplied. One barrier per slab; the wait
+//    before it is explicit (every wave's own fills of slab k), and the barrier is a bare s_barrier
+//    - __syncthreads' release fence would wait for the younger slabs' fills too.
+//  * Buffer resources bound every fill: the K tail, rows past M and n-tiles past N fill zeros.
+//  * The e8m0 scale dwords are filled the same way; the MFMA applies them, so no dequantisation
+//    happens anywhere.
 //  * Workgroups are renumbered so each XCD (hardware places workgroup b on XCD b % 8) gets a
 //    contiguous run of tiles, walked in groups of 8 row blocks, which keeps an XCD's activation
 //    and weight panels in its own L2.
-//  * Epilogue: lane holds 4 consecutive columns of one token; scaled by the per-token fp32 scale,
+//  * Epilogue: a lane holds 4 consecutive columns of one token; scaled by the per-token fp32 scale,
 //    rounded to bf16 and stored 8 bytes at a time.
 #include "w4a8_internal.h"
 
@@ -24,26 +28,51 @@ namespace w4a8 {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kOut = 0x7FFFFFF0;                 // an offset past every buffer resource here
 
 template <int WM, int WN>
 struct TileShape {
   static constexpr int BM = 2 * WM * 16;
   static constexpr int BN = 2 * WN * 16;
-  static constexpr int A_BYTES = BM * kKTile;          // one fp8 slab
-  static constexpr int W_BYTES = (BN / 16) * kGranuleBytes;
-  static constexpr int STAGE = A_BYTES + W_BYTES;
-  static constexpr int A_CHUNKS = A_BYTES / 16 / kThreads;   // 16-byte chunks per thread
-  static constexpr int W_CHUNKS = W_BYTES / 16 / kThreads;
-  static_assert(A_BYTES % (16 * kThreads) == 0 && W_BYTES % (16 * kThreads) == 0, "tile");
+  static constexpr int A_UNITS = 2 * WM * 2;     // 1 KiB units per slab: 16-token blocks x 2 runs
+  static constexpr int W_UNITS = 2 * WN;         // weight granules per slab
+  static constexpr int S_UNITS = 2 * WN;         // 256 B scale-dword rows per slab (one per n-tile)
+  static constexpr int A_PER_WAVE = A_UNITS / 4;
+  static constexpr int W_PER_WAVE = ceil_div(W_UNITS, 4);
+  static constexpr int S_PER_WAVE = ceil_div(S_UNITS, 4);
+  static constexpr int OPS = A_PER_WAVE + W_PER_WAVE + S_PER_WAVE;   // fills per wave per slab
+  // every wave issues the same number of fills; the surplus ones (past W_UNITS / S_UNITS, zero
+  // fills) land in padding slots of their own
+  static constexpr int W_OFF = A_UNITS * 1024;
+  static constexpr int S_OFF = W_OFF + 4 * W_PER_WAVE * 1024;
+  static constexpr int STAGE = S_OFF + 4 * S_PER_WAVE * 256;
+  static_assert(A_UNITS % 4 == 0, "tile");
 };
 
-template <int WM, int WN>
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// s_waitcnt vmcnt(n) with lgkmcnt and expcnt left open (gfx9 encoding)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// A workgroup barrier that orders the compiler's memory operations but emits no memory fence.
+__device__ __forceinline__ void bare_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <int WM, int WN, int NS>
 __global__ __launch_bounds__(kThreads) void gemm_tile(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
     const uint32_t* __restrict__ Sq, uint16_t* __restrict__ C, int M, int N, int K, int KTp,
     int KTe, int KG, int NTILES, int grid_m, int grid_n, int vec_out) {
   using S = TileShape<WM, WN>;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * S::STAGE];
+  static_assert(NS >= 2 && (NS - 2) * S::OPS < 64, "pipeline depth");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * S::STAGE];
 
   // ---- tile order: XCD-contiguous runs, grouped by 8 row blocks ----
   const int total = grid_m * grid_n;
@@ -57,54 +86,48 @@ __global__ __launch_bounds__(kThreads) void gemm_tile(
   const int bn = (t % per_group) / gm;
   const int m0 = bm * S::BM, nt_base = bn * (S::BN / 16);
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
 
-  // per-thread staging chunks
-  uint4 ra[S::A_CHUNKS];
-  v4i rw[S::W_CHUNKS];
-  uint32_t sv[WN], sv_next[WN];
+  // buffer resources: activations (all M x K), this tile's weight granules and scale dwords
+  const auto a_src = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, M * K, kBufferWord3);
+  const int ntiles_here = min(S::BN / 16, NTILES - nt_base);
+  const auto w_src = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(Wq + (size_t)nt_base * KTp * kGranuleBytes), 0, ntiles_here * KTp * kGranuleBytes,
+      kBufferWord3);
+  const auto s_src = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(Sq + (size_t)nt_base * KG * 64), 0, ntiles_here * KG * 256, kBufferWord3);
+  const int arow = lane & 15, ag = lane >> 4;
 
-  auto load_slab = [&](int kt) {
+  // Fill stage `st` with slab kt: every wave issues exactly S::OPS fills (out-of-range ones fill
+  // zeros), so the outstanding-fill count per slab is a compile-time constant.
+  auto fill = [&](int kt, int st) {
+    uint8_t* base = lds + st * S::STAGE;
+    const bool kin = kt < KTe;
 #pragma unroll
-    for (int c = 0; c < S::A_CHUNKS; ++c) {
-      const int ch = tid + c * kThreads;           // (row block, 16-byte column, row in block)
-      const int r16 = ch & 15, cc = (ch >> 4) & 7, rb = ch >> 7;
-      const int row = m0 + rb * 16 + r16;
-      const int kb = kt * kKTile + cc * 16;
-      ra[c] = (row < M && kb < K) ? *reinterpret_cast<const uint4*>(A + (size_t)row * K + kb)
-                                  : make_uint4(0, 0, 0, 0);
+    for (int u = 0; u < S::A_PER_WAVE; ++u) {
+      const int unit = wave * S::A_PER_WAVE + u;
+      const int row = m0 + (unit >> 1) * 16 + arow;
+      const int col = kt * kKTile + (unit & 1) * 64 + ag * 16;
+      const int off = (kin && col < K && row < M) ? row * K + col : kOut;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(a_src, (lds_ptr_t)(base + unit * 1024), 16, off, 0,
+                                               0, 0);
     }
 #pragma unroll
-    for (int c = 0; c < S::W_CHUNKS; ++c) {
-      const int ch = tid + c * kThreads;
-      const int nt = nt_base + (ch >> 6);
-      rw[c] = nt < NTILES ? load_v4i_stream(Wq + (((size_t)nt * KTp + kt) * 64 + (ch & 63)) * 16)
-                          : v4i{0, 0, 0, 0};
+    for (int u = 0; u < S::W_PER_WAVE; ++u) {
+      const int g = wave * S::W_PER_WAVE + u;
+      const int off = (kin && g < S::W_UNITS) ? (g * KTp + kt) * kGranuleBytes + lane * 16 : kOut;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(w_src, (lds_ptr_t)(base + S::W_OFF + g * 1024), 16,
+                                               off, 0, 0, kBufferNT);
     }
-  };
-  auto load_scales = [&](int kt, uint32_t* dst) {
 #pragma unroll
-    for (int j = 0; j < WN; ++j) {
-      const int nt = nt_base + wn * WN + j;
-      dst[j] = nt < NTILES ? Sq[((size_t)nt * KG + (kt >> 2)) * 64 + lane] >> (8 * (kt & 3))
-                           : 127u;
+    for (int u = 0; u < S::S_PER_WAVE; ++u) {
+      const int g = wave * S::S_PER_WAVE + u;
+      const int off = (kin && g < S::S_UNITS) ? ((g * KG + (kt >> 2)) * 64 + lane) * 4 : kOut;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(s_src, (lds_ptr_t)(base + S::S_OFF + g * 256), 4,
+                                               off, 0, 0, 0);
     }
-  };
-  auto store_slab = [&](int buf) {
-    uint8_t* sA = lds + buf * S::STAGE;
-#pragma unroll
-    for (int c = 0; c < S::A_CHUNKS; ++c) {
-      const int ch = tid + c * kThreads;
-      const int r16 = ch & 15, cc = (ch >> 4) & 7, rb = ch >> 7;
-      // 16-byte column cc (k = 16 cc ..) of row r16 is run cc >> 2 of fragment lane (cc & 3) * 16 + r16
-      *reinterpret_cast<uint4*>(sA + rb * 2048 + (cc >> 2) * 1024 + ((cc & 3) * 16 + r16) * 16) =
-          ra[c];
-    }
-    uint8_t* sW = sA + S::A_BYTES;
-#pragma unroll
-    for (int c = 0; c < S::W_CHUNKS; ++c)
-      *reinterpret_cast<v4i*>(sW + (tid + c * kThreads) * 16) = rw[c];
   };
 
   v4f acc[WM][WN];
@@ -113,58 +136,75 @@ __global__ __launch_bounds__(kThreads) void gemm_tile(
 #pragma unroll
     for (int j = 0; j < WN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  load_slab(0);
-  load_scales(0, sv);
-  store_slab(0);
-  __syncthreads();
-
-  for (int kt = 0; kt < KTe; ++kt) {
-    const int buf = kt & 1;
-    const bool more = kt + 1 < KTe;
-    if (more) {
-      load_slab(kt + 1);
-      load_scales(kt + 1, sv_next);
-    }
-    const uint8_t* sA = lds + buf * S::STAGE;
-    const uint8_t* sW = sA + S::A_BYTES;
+  auto compute = [&](int st, int kt) {
+    const uint8_t* base = lds + st * S::STAGE;
     v4i wf[WN];
+    uint32_t sc[WN];
+    const int sh = 8 * (kt & 3);
 #pragma unroll
-    for (int j = 0; j < WN; ++j)
-      wf[j] = *reinterpret_cast<const v4i*>(sW + (wn * WN + j) * kGranuleBytes + lane * 16);
+    for (int j = 0; j < WN; ++j) {
+      wf[j] = *reinterpret_cast<const v4i*>(base + S::W_OFF + (wn * WN + j) * 1024 + lane * 16);
+      sc[j] = *reinterpret_cast<const uint32_t*>(base + S::S_OFF + (wn * WN + j) * 256 + lane * 4) >>
+              sh;
+    }
+    // activation fragments double-buffered in registers: fragment i+1 is read while the MFMAs
+    // of fragment i issue, so the LDS latency hides behind them
+    const uint8_t* pa = base + (wm * WM * 2) * 1024 + lane * 16;
+    v4i lo = *reinterpret_cast<const v4i*>(pa), hi = *reinterpret_cast<const v4i*>(pa + 1024);
 #pragma unroll
     for (int i = 0; i < WM; ++i) {
-      const uint8_t* pa = sA + (wm * WM + i) * 2048 + lane * 16;
-      const v4i lo = *reinterpret_cast<const v4i*>(pa);
-      const v4i hi = *reinterpret_cast<const v4i*>(pa + 1024);
       const v8i xf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      if (i + 1 < WM) {
+        lo = *reinterpret_cast<const v4i*>(pa + (i + 1) * 2048);
+        hi = *reinterpret_cast<const v4i*>(pa + (i + 1) * 2048 + 1024);
+      }
 #pragma unroll
-      for (int j = 0; j < WN; ++j) acc[i][j] = mfma_w4a8(wf[j], xf, acc[i][j], sv[j]);
+      for (int j = 0; j < WN; ++j) acc[i][j] = mfma_w4a8(wf[j], xf, acc[i][j], sc[j]);
     }
-    if (more) {
-      store_slab(buf ^ 1);
-#pragma unroll
-      for (int j = 0; j < WN; ++j) sv[j] = sv_next[j];
-    }
-    __syncthreads();
-  }
+  };
 
+  // ---- NS-stage pipeline: slab kt+NS-1 is requested while slab kt is multiplied ----
+#pragma unroll
+  for (int p = 0; p < NS - 1; ++p) fill(p, p);
+  int st = 0;
+  for (int kt = 0; kt < KTe; ++kt) {
+    wait_vmcnt<(NS - 2) * S::OPS>();             // this wave's fills of slab kt have landed
+    bare_barrier();                              // ... and every wave's; slab kt-1 is consumed
+    const int nxt = st == 0 ? NS - 1 : st - 1;   // stage of slab kt+NS-1 == stage of slab kt-1
+    fill(kt + NS - 1, nxt);
+    compute(st, kt);
+    st = st + 1 == NS ? 0 : st + 1;
+  }
+  wait_vmcnt<0>();                               // no fill may outlive the workgroup's LDS
+
+  // per-token scales of this lane's WM tokens, all requested before the first is used
+  const auto as_src = __builtin_amdgcn_make_buffer_rsrc((void*)As, 0, M * 4, kBufferWord3);
+  float tsc[WM];
+#pragma unroll
+  for (int i = 0; i < WM; ++i) {
+    const int m = m0 + (wm * WM + i) * 16 + (lane & 15);
+    tsc[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                           as_src, m < M ? m * 4 : kOut, 0, 0));
+  }
   const bool vec = vec_out != 0;
 #pragma unroll
   for (int i = 0; i < WM; ++i) {
     const int m = m0 + (wm * WM + i) * 16 + (lane & 15);
     if (m >= M) continue;
-    const float sc = As[m];
 #pragma unroll
     for (int j = 0; j < WN; ++j) {
       const int n = (nt_base + wn * WN + j) * kNTile + 4 * (lane >> 4);
-      store_out4(C, N, m, n, N, acc[i][j], sc, vec);
+      store_out4(C, N, m, n, N, acc[i][j], tsc[i], vec);
     }
   }
 }
 
-#define W4A8_TILE_TABLE(X) X(2, 4) X(4, 4) X(8, 4) X(4, 8) X(8, 8)
+// (WM, WN, NS): wave tile 16 WM x 16 WN, NS-stage LDS pipeline (LDS = NS * STAGE <= 160 KiB)
+#define W4A8_TILE_TABLE(X)                                                                        \
+  X(2, 4, 4) X(4, 4, 3) X(4, 4, 4) X(8, 4, 3) X(4, 8, 3) X(8, 8, 3) X(8, 5, 3) X(4, 8, 4)          \
+  X(4, 2, 4)
 
-#define W4A8_TILE_CFG(wm, wn) TileCfg{wm, wn, TileShape<wm, wn>::BM, TileShape<wm, wn>::BN},
+#define W4A8_TILE_CFG(wm, wn, ns) TileCfg{wm, wn, TileShape<wm, wn>::BM, TileShape<wm, wn>::BN},
 constexpr TileCfg kTile[] = {W4A8_TILE_TABLE(W4A8_TILE_CFG)};
 #undef W4A8_TILE_CFG
 constexpr int kTileCount = sizeof(kTile) / sizeof(kTile[0]);
@@ -174,6 +214,12 @@ constexpr int kTileCount = sizeof(kTile) / sizeof(kTile[0]);
 int tile_variant_count() { return kTileCount; }
 TileCfg tile_variant(int v) { return kTile[v]; }
 
+bool tile_fits(int M, int N, int K) {
+  // 32-bit buffer offsets: the activations and one tile's weight stripe
+  return (long)M * K < (1L << 31) && (long)16 * padded_k(K) / 2 * 16 < (1L << 31) &&
+         (long)N < (1L << 24);
+}
+
 hipError_t launch_tile(const GemmArgs& g, int variant, hipStream_t stream) {
   const TileCfg c = kTile[variant];
   const int KTp = padded_k(g.K) / kKTile, KTe = ceil_div(g.K, kKTile), KG = KTp / kKGroup;
@@ -182,9 +228,10 @@ hipError_t launch_tile(const GemmArgs& g, int variant, hipStream_t stream) {
   const int vec_out = (g.N % 4 == 0 && ((uintptr_t)g.c % 8) == 0) ? 1 : 0;
   const dim3 grid(grid_m * grid_n), block(kThreads);
   int idx = 0;
-#define W4A8_TILE_LAUNCH(wm, wn)                                                                 \
+#define W4A8_TILE_LAUNCH(wm, wn, ns)                                                           \
   if (idx++ == variant) {                                                                        \
-    hipLaunchKernelGGL((gemm_tile<wm, wn>), grid, block, 0, stream, g.a, g.a_scale, g.wq, g.sq,  \
+    hipLaunchKernelGGL((gemm_tile<wm, wn, ns>), grid, block, 0, stream, g.a, g.a_scale, g.wq,  \
+                       g.sq,                                                                      \
                        g.c, g.M, g.N, g.K, KTp, KTe, KG, NTILES, grid_m, grid_n, vec_out);       \
     return hipGetLastError();                                                                    \
   }

@@ -129,6 +129,7 @@ hipError_t launch_stream(const GemmArgs& g, int variant, int cus, hipStream_t st
 struct TileCfg { int wm, wn, bm, bn; };
 int tile_variant_count();
 TileCfg tile_variant(int v);
+bool tile_fits(int M, int N, int K);
 hipError_t launch_tile(const GemmArgs& g, int variant, hipStream_t stream);
 
 // Register-resident MFMA throughput probe (shape 0: 16x16x128, 1: 32x32x64).
