@@ -158,11 +158,11 @@ void plan_impl(int M, int N, int K, int dev, int* kernel, int* variant, int* spl
     *split_k = ks;
     return;
   }
-  // Prefill band (measured on MI355X): 128 x 256 tiles for wide N, 256 x 160 where N divides into
+  // Prefill band (measured on MI355X): 256 x 256 tiles for wide N, 256 x 160 where N divides into
   // 160-column tiles that fill the CUs evenly (N = 5120: 512 tiles at M = 4096), 128 x 128 below.
   *kernel = W4A8_KERNEL_TILE;
   if (M >= 2048 && N % 160 == 0 && N <= 8192) *variant = find_tile(8, 5);
-  else if (M >= 2048) *variant = find_tile(4, 8);
+  else if (M >= 2048) *variant = find_tile(8, 8);
   else if (M >= 256) *variant = find_tile(4, 4);
   else *variant = find_tile(2, 4);
   *split_k = 1;

@@ -101,33 +101,34 @@ __global__ __launch_bounds__(kThreads) void gemm_tile(
   const int arow = lane & 15, ag = lane >> 4;
 
   // Fill stage `st` with slab kt: every wave issues exactly S::OPS fills (out-of-range ones fill
-  // zeros), so the outstanding-fill count per slab is a compile-time constant.
-  auto fill = [&](int kt, int st) {
-    uint8_t* base = lds + st * S::STAGE;
+  // zeros), so the outstanding-fill count per slab is a compile-time constant. Fill op o is an
+  // activation unit (o < A_PER_WAVE), then a weight granule, then a scale row; the ops are issued
+  // in WM shares between the MFMA groups, so the address unit streams them while the MFMAs run.
+  auto fill_op = [&](int kt, uint8_t* base, int o) {
     const bool kin = kt < KTe;
-#pragma unroll
-    for (int u = 0; u < S::A_PER_WAVE; ++u) {
-      const int unit = wave * S::A_PER_WAVE + u;
+    if (o < S::A_PER_WAVE) {
+      const int unit = wave * S::A_PER_WAVE + o;
       const int row = m0 + (unit >> 1) * 16 + arow;
       const int col = kt * kKTile + (unit & 1) * 64 + ag * 16;
       const int off = (kin && col < K && row < M) ? row * K + col : kOut;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(a_src, (lds_ptr_t)(base + unit * 1024), 16, off, 0,
                                                0, 0);
-    }
-#pragma unroll
-    for (int u = 0; u < S::W_PER_WAVE; ++u) {
-      const int g = wave * S::W_PER_WAVE + u;
+    } else if (o < S::A_PER_WAVE + S::W_PER_WAVE) {
+      const int g = wave * S::W_PER_WAVE + (o - S::A_PER_WAVE);
       const int off = (kin && g < S::W_UNITS) ? (g * KTp + kt) * kGranuleBytes + lane * 16 : kOut;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(w_src, (lds_ptr_t)(base + S::W_OFF + g * 1024), 16,
                                                off, 0, 0, kBufferNT);
-    }
-#pragma unroll
-    for (int u = 0; u < S::S_PER_WAVE; ++u) {
-      const int g = wave * S::S_PER_WAVE + u;
+    } else {
+      const int g = wave * S::S_PER_WAVE + (o - S::A_PER_WAVE - S::W_PER_WAVE);
       const int off = (kin && g < S::S_UNITS) ? ((g * KG + (kt >> 2)) * 64 + lane) * 4 : kOut;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(s_src, (lds_ptr_t)(base + S::S_OFF + g * 256), 4,
                                                off, 0, 0, 0);
     }
+  };
+  auto fill = [&](int kt, int st) {
+    uint8_t* base = lds + st * S::STAGE;
+#pragma unroll
+    for (int o = 0; o < S::OPS; ++o) fill_op(kt, base, o);
   };
 
   v4f acc[WM][WN];
@@ -136,8 +137,12 @@ __global__ __launch_bounds__(kThreads) void gemm_tile(
 #pragma unroll
     for (int j = 0; j < WN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](int st, int kt) {
+  // Multiply slab kt out of stage st while issuing the fills of slab fkt into stage fst: fragment
+  // i+1 is read and a share of the fills is issued before fragment i's MFMAs, and a scheduling
+  // barrier keeps the compiler from sinking them below the MFMAs.
+  auto compute = [&](int st, int kt, int fkt, int fst) {
     const uint8_t* base = lds + st * S::STAGE;
+    uint8_t* fbase = lds + fst * S::STAGE;
     v4i wf[WN];
     uint32_t sc[WN];
     const int sh = 8 * (kt & 3);
@@ -147,8 +152,6 @@ __global__ __launch_bounds__(kThreads) void gemm_tile(
       sc[j] = *reinterpret_cast<const uint32_t*>(base + S::S_OFF + (wn * WN + j) * 256 + lane * 4) >>
               sh;
     }
-    // activation fragments double-buffered in registers: fragment i+1 is read while the MFMAs
-    // of fragment i issue, so the LDS latency hides behind them
     const uint8_t* pa = base + (wm * WM * 2) * 1024 + lane * 16;
     v4i lo = *reinterpret_cast<const v4i*>(pa), hi = *reinterpret_cast<const v4i*>(pa + 1024);
 #pragma unroll
@@ -159,7 +162,11 @@ __global__ __launch_bounds__(kThreads) void gemm_tile(
         hi = *reinterpret_cast<const v4i*>(pa + (i + 1) * 2048 + 1024);
       }
 #pragma unroll
+      for (int o = i * S::OPS / WM; o < (i + 1) * S::OPS / WM; ++o) fill_op(fkt, fbase, o);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
       for (int j = 0; j < WN; ++j) acc[i][j] = mfma_w4a8(wf[j], xf, acc[i][j], sc[j]);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
@@ -171,8 +178,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tile(
     wait_vmcnt<(NS - 2) * S::OPS>();             // this wave's fills of slab kt have landed
     bare_barrier();                              // ... and every wave's; slab kt-1 is consumed
     const int nxt = st == 0 ? NS - 1 : st - 1;   // stage of slab kt+NS-1 == stage of slab kt-1
-    fill(kt + NS - 1, nxt);
-    compute(st, kt);
+    compute(st, kt, kt + NS - 1, nxt);           // issues slab kt+NS-1's fills in shares
     st = st + 1 == NS ? 0 : st + 1;
   }
   wait_vmcnt<0>();                               // no fill may outlive the workgroup's LDS
