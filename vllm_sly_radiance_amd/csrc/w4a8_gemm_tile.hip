@@ -6,17 +6,22 @@
 //  * 4 wave64 in a 2 x 2 arrangement; each wave owns WM x WN MFMA tiles of 16 tokens x 16
 //    columns (up to 128 x 128 per wave), so the workgroup tile is (32 WM) tokens x (32 WN) columns
 //    and a 128-k slab is 32 WM * 128 B of activations, 2 WN weight granules and their scale dwords.
-//  * Each slab is fragment-ordered in LDS: one load instruction moves one 1 KiB unit - a weight
-//    granule verbatim, or one run of a 16-token activation fragment (lane l = 16 g + row, k 16g..
-//    or 64 + 16g..) - and the LDS-direct form writes lane l's 16 bytes at unit + 16 l, so both the
-//    fills and the ds_read_b128 fragment reads are 1 KiB contiguous per wave and conflict-free.
+//  * One load instruction moves one 1 KiB unit of a slab straight into LDS: a weight granule
+//    verbatim (already in MFMA fragment order), or 8 tokens x 128 k of activations. For the latter,
+//    8 consecutive lanes read one token's 128-byte line: lanes that read scattered tokens instead
+//    (the fragment order) cut the L2-to-LDS rate by 3.5x on MI355X. The LDS-direct form writes
+//    lane l's 16 bytes at unit + 16 l, so each lane picks its chunk such that token R's chunk c
+//    sits at slot 8 (R % 8) + (c ^ ((R / 2) % 8)): the ds_read_b128 fragment reads then touch
+//    every bank once per 16 lanes.
 //  * The fills go straight from memory to LDS, so the pipeline depth costs LDS, not registers:
-//    NS stages, slab k+NS-1 requested while slab k is multiplied. One barrier per slab; the wait
-//    before it is explicit (every wave's own fills of slab k), and the barrier is a bare s_barrier
-//    - __syncthreads' release fence would wait for the younger slabs' fills too.
+//    NS stages, slab k+NS-1 requested while slab k is multiplied, its fills issued in shares
+//    between the MFMA groups. One barrier per slab; the wait before it is explicit (every wave's
+//    own fills of slab k), and the barrier is a bare s_barrier - __syncthreads' release fence
+//    would wait for the younger slabs' fills too.
 //  * Buffer resources bound every fill: the K tail, rows past M and n-tiles past N fill zeros.
-//  * The e8m0 scale dwords are filled the same way; the MFMA applies them, so no dequantisation
-//    happens anywhere.
+//  * The e8m0 scale dwords change every 4 slabs (one dword per lane per k-group), so they live in
+//    a ring of 3 k-groups outside the stages; each slab's fills carry a quarter of the next
+//    k-group's rows. The MFMA applies the scales, so no dequantisation happens anywhere.
 //  * Workgroups are renumbered so each XCD (hardware places workgroup b on XCD b % 8) gets a
 //    contiguous run of tiles, walked in groups of 8 row blocks, which keeps an XCD's activation
 //    and weight panels in its own L2.
@@ -34,18 +39,20 @@ template <int WM, int WN>
 struct TileShape {
   static constexpr int BM = 2 * WM * 16;
   static constexpr int BN = 2 * WN * 16;
-  static constexpr int A_UNITS = 2 * WM * 2;     // 1 KiB units per slab: 16-token blocks x 2 runs
+  static constexpr int A_UNITS = BM / 8;         // 1 KiB units per slab: 8 tokens x 128 k each
   static constexpr int W_UNITS = 2 * WN;         // weight granules per slab
-  static constexpr int S_UNITS = 2 * WN;         // 256 B scale-dword rows per slab (one per n-tile)
+  static constexpr int S_ROWS = 2 * WN;          // 256 B scale-dword rows per k-group (one per n-tile)
   static constexpr int A_PER_WAVE = A_UNITS / 4;
   static constexpr int W_PER_WAVE = ceil_div(W_UNITS, 4);
-  static constexpr int S_PER_WAVE = ceil_div(S_UNITS, 4);
+  static constexpr int S_QUARTER = ceil_div(S_ROWS, 4);        // rows filled per slab
+  static constexpr int S_PER_WAVE = ceil_div(S_QUARTER, 4);
   static constexpr int OPS = A_PER_WAVE + W_PER_WAVE + S_PER_WAVE;   // fills per wave per slab
-  // every wave issues the same number of fills; the surplus ones (past W_UNITS / S_UNITS, zero
-  // fills) land in padding slots of their own
+  // every wave issues the same number of fills; the surplus ones (past W_UNITS, or past a
+  // quarter's scale rows) are zero fills into padding slots of their own
   static constexpr int W_OFF = A_UNITS * 1024;
-  static constexpr int S_OFF = W_OFF + 4 * W_PER_WAVE * 1024;
-  static constexpr int STAGE = S_OFF + 4 * S_PER_WAVE * 256;
+  static constexpr int STAGE = W_OFF + 4 * W_PER_WAVE * 1024;
+  // scale ring: 3 k-groups of S_ROWS rows, plus one junk row
+  static constexpr int S_SLOT = (4 * S_QUARTER + 1) * 256;
   static_assert(A_UNITS % 4 == 0, "tile");
 };
 
@@ -71,8 +78,9 @@ __global__ __launch_bounds__(kThreads) void gemm_tile(
     const uint32_t* __restrict__ Sq, uint16_t* __restrict__ C, int M, int N, int K, int KTp,
     int KTe, int KG, int NTILES, int grid_m, int grid_n, int vec_out) {
   using S = TileShape<WM, WN>;
-  static_assert(NS >= 2 && (NS - 2) * S::OPS < 64, "pipeline depth");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * S::STAGE];
+  static_assert(NS >= 2 && NS <= 5 && (NS - 2) * S::OPS < 64, "pipeline depth");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * S::STAGE + 3 * S::S_SLOT];
+  uint8_t* const sring = lds + NS * S::STAGE;
 
   // ---- tile order: XCD-contiguous runs, grouped by 8 row blocks ----
   const int total = grid_m * grid_n;
@@ -98,31 +106,44 @@ __global__ __launch_bounds__(kThreads) void gemm_tile(
       kBufferWord3);
   const auto s_src = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(Sq + (size_t)nt_base * KG * 64), 0, ntiles_here * KG * 256, kBufferWord3);
-  const int arow = lane & 15, ag = lane >> 4;
 
-  // Fill stage `st` with slab kt: every wave issues exactly S::OPS fills (out-of-range ones fill
-  // zeros), so the outstanding-fill count per slab is a compile-time constant. Fill op o is an
-  // activation unit (o < A_PER_WAVE), then a weight granule, then a scale row; the ops are issued
-  // in WM shares between the MFMA groups, so the address unit streams them while the MFMAs run.
+  // Activation units: 8 consecutive lanes read one token's 128 k-bytes (one cache line), and the
+  // 16 B chunks land XOR-swizzled so the fragment reads below hit every LDS bank once. Token R of
+  // a 16-token block (unit 2b + R / 8) keeps chunk c at slot 8 (R % 8) + (c ^ ((R / 2) % 8)).
+  const int a_row = lane >> 3;                              // token within the 8-token unit
+  const int a_chunk = (lane & 7) ^ (a_row >> 1);            // chunk for even units; odd: ^ 4
+  // MFMA fragment of lane l: token l % 16, chunks l / 16 and 4 + l / 16 of the 16-token block
+  const int f_row = lane & 15;
+  const int f_lo = 1024 * (f_row >> 3) + 16 * (8 * (f_row & 7) + ((lane >> 4) ^ ((f_row >> 1) & 7)));
+  const int f_hi = f_lo ^ 64;                               // chunk + 4: slot bit 2 flips
+
+  // Fill op o of slab kt into stage base: an activation unit (o < A_PER_WAVE), a weight granule,
+  // or a scale row. Scale rows are per k-group of 4 slabs: the fills of slab kt carry quarter
+  // kt % 4 of the rows of k-group kt / 4 + 1, into ring slot (kt / 4 + 1) % 3.
   auto fill_op = [&](int kt, uint8_t* base, int o) {
     const bool kin = kt < KTe;
     if (o < S::A_PER_WAVE) {
       const int unit = wave * S::A_PER_WAVE + o;
-      const int row = m0 + (unit >> 1) * 16 + arow;
-      const int col = kt * kKTile + (unit & 1) * 64 + ag * 16;
-      const int off = (kin && col < K && row < M) ? row * K + col : kOut;
+      const int row = m0 + unit * 8 + a_row;
+      const int col = kt * kKTile + 16 * (a_chunk ^ ((unit & 1) << 2));
+      const int off = (kin & (col < K) & (row < M)) ? row * K + col : kOut;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(a_src, (lds_ptr_t)(base + unit * 1024), 16, off, 0,
                                                0, 0);
     } else if (o < S::A_PER_WAVE + S::W_PER_WAVE) {
       const int g = wave * S::W_PER_WAVE + (o - S::A_PER_WAVE);
-      const int off = (kin && g < S::W_UNITS) ? (g * KTp + kt) * kGranuleBytes + lane * 16 : kOut;
+      const int off = (kin & (g < S::W_UNITS)) ? (g * KTp + kt) * kGranuleBytes + lane * 16 : kOut;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(w_src, (lds_ptr_t)(base + S::W_OFF + g * 1024), 16,
                                                off, 0, 0, kBufferNT);
     } else {
-      const int g = wave * S::S_PER_WAVE + (o - S::A_PER_WAVE - S::W_PER_WAVE);
-      const int off = (kin && g < S::S_UNITS) ? ((g * KG + (kt >> 2)) * 64 + lane) * 4 : kOut;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(s_src, (lds_ptr_t)(base + S::S_OFF + g * 256), 4,
-                                               off, 0, 0, 0);
+      const int grp = (kt >> 2) + 1, q = kt & 3;
+      const int i = wave * S::S_PER_WAVE + (o - S::A_PER_WAVE - S::W_PER_WAVE);
+      const int r = q * S::S_QUARTER + i;
+      const bool real = (i < S::S_QUARTER) & (r < S::S_ROWS);
+      const int off = (real & (grp < KG)) ? ((r * KG + grp) * 64 + lane) * 4 : kOut;
+      const int slot = grp % 3;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          s_src, (lds_ptr_t)(sring + slot * S::S_SLOT + (real ? r : 4 * S::S_QUARTER) * 256), 4,
+          off, 0, 0, 0);
     }
   };
   auto fill = [&](int kt, int st) {
@@ -143,23 +164,23 @@ __global__ __launch_bounds__(kThreads) void gemm_tile(
   auto compute = [&](int st, int kt, int fkt, int fst) {
     const uint8_t* base = lds + st * S::STAGE;
     uint8_t* fbase = lds + fst * S::STAGE;
+    const uint8_t* srow = sring + ((kt >> 2) % 3) * S::S_SLOT + lane * 4;
     v4i wf[WN];
     uint32_t sc[WN];
     const int sh = 8 * (kt & 3);
 #pragma unroll
     for (int j = 0; j < WN; ++j) {
       wf[j] = *reinterpret_cast<const v4i*>(base + S::W_OFF + (wn * WN + j) * 1024 + lane * 16);
-      sc[j] = *reinterpret_cast<const uint32_t*>(base + S::S_OFF + (wn * WN + j) * 256 + lane * 4) >>
-              sh;
+      sc[j] = *reinterpret_cast<const uint32_t*>(srow + (wn * WN + j) * 256) >> sh;
     }
-    const uint8_t* pa = base + (wm * WM * 2) * 1024 + lane * 16;
-    v4i lo = *reinterpret_cast<const v4i*>(pa), hi = *reinterpret_cast<const v4i*>(pa + 1024);
+    const uint8_t* pa = base + wm * WM * 2048;
+    v4i lo = *reinterpret_cast<const v4i*>(pa + f_lo), hi = *reinterpret_cast<const v4i*>(pa + f_hi);
 #pragma unroll
     for (int i = 0; i < WM; ++i) {
       const v8i xf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       if (i + 1 < WM) {
-        lo = *reinterpret_cast<const v4i*>(pa + (i + 1) * 2048);
-        hi = *reinterpret_cast<const v4i*>(pa + (i + 1) * 2048 + 1024);
+        lo = *reinterpret_cast<const v4i*>(pa + (i + 1) * 2048 + f_lo);
+        hi = *reinterpret_cast<const v4i*>(pa + (i + 1) * 2048 + f_hi);
       }
 #pragma unroll
       for (int o = i * S::OPS / WM; o < (i + 1) * S::OPS / WM; ++o) fill_op(fkt, fbase, o);
@@ -171,6 +192,20 @@ __global__ __launch_bounds__(kThreads) void gemm_tile(
   };
 
   // ---- NS-stage pipeline: slab kt+NS-1 is requested while slab kt is multiplied ----
+  // k-group 0's scale rows first (4 quarters), so the wait for slab 0 covers them too
+  {
+    const int i = wave * S::S_PER_WAVE;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int e = 0; e < S::S_PER_WAVE; ++e) {
+        const int r = q * S::S_QUARTER + i + e;
+        const bool real = (i + e < S::S_QUARTER) & (r < S::S_ROWS);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            s_src, (lds_ptr_t)(sring + (real ? r : 4 * S::S_QUARTER) * 256), 4,
+            real ? (r * KG * 64 + lane) * 4 : kOut, 0, 0, 0);
+      }
+  }
 #pragma unroll
   for (int p = 0; p < NS - 1; ++p) fill(p, p);
   int st = 0;
