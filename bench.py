@@ -50,6 +50,12 @@ def parse():
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only-verify", action="store_true", help="skip prefill and M=1 legs")
+    ap.add_argument("--sweep", action="store_true",
+                    help="the 64-layer sweep instead of the headline: one-time repack cost per "
+                         "layer, linear ms per forward at M in {1, 8, 16, 64, 512, 4096}, and the "
+                         "M where the macro-tile GEMM overtakes the decode kernels; prints its own "
+                         "JSON line")
+    ap.add_argument("--sweep-layers", type=int, default=64)
     ap.add_argument("--profile", action="store_true",
                     help="counter-run workload: the verify-GEMM graph replay, 4 launches of each "
                          "prefill GEMM and one 256 MiB device copy (the counter calibration); "
@@ -225,6 +231,147 @@ def cpu_baseline():
                       f"{sec:.3f} s per GEMM"}
 
 
+SWEEP_M = [1, 8, 16, 64, 512, 4096]
+CROSSOVER_M = [8, 16, 17, 24, 32, 48, 64, 96, 128]
+
+
+def _timed_graph(fn, reps):
+    """Capture fn() into a HIP graph on a side stream, replay it once untimed and then `reps`
+    times between events on that stream; returns ms per replay."""
+    import torch
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        fn()
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        fn()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        graph.replay()
+        e0.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del graph
+    return ms
+
+
+def bench_sweep(n_layers):
+    """64 stacked Qwen3.8-27B-shaped layers (qkv, o_proj, gate_up, down), random-init MXFP4
+    checkpoint tensors generated on the device. Loads every linear through the plugin's
+    process_weights_after_loading (the one-time repack, timed per layer), then times the linear
+    part of a forward (per-token quant + GEMM per linear, through apply_weights as vLLM calls it)
+    at each M, one HIP graph per shape over all layers. The crossover compares the decode
+    kernels the plan uses up to M = 64 with the macro-tile kernel at the same M."""
+    import torch
+    from vllm_sly_radiance_amd import _native, radiance_mxfp4 as R, synthetic
+    dev = torch.device("cuda", 0)
+    R.ensure_scratch(dev)
+    kern = R.kernel_class()()
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20251)
+    layers = {name: [] for name, _, _ in LAYER_M1}
+    repack_ms = []
+    for _ in range(n_layers):
+        t = 0.0
+        for name, N, K in LAYER_M1:
+            lin = torch.nn.Module()
+            lin.weight = torch.nn.Parameter(
+                torch.randint(0, 256, (N, K // 2), dtype=torch.uint8, device=dev, generator=gen),
+                requires_grad=False)
+            lin.weight_scale = torch.nn.Parameter(
+                torch.randint(synthetic.SCALE_LO, synthetic.SCALE_HI + 1, (N, K // 32),
+                              dtype=torch.uint8, device=dev, generator=gen), requires_grad=False)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            kern.process_weights_after_loading(lin)
+            e1.record()
+            torch.cuda.synchronize()
+            t += e0.elapsed_time(e1)
+            layers[name].append(lin)
+        repack_ms.append(t)
+    weight_bytes = sum(N * K * 17 // 32 for _, N, K in LAYER_M1)
+    print(f"[bench] sweep: {n_layers} layers loaded, {weight_bytes * n_layers / 1e9:.2f} GB of "
+          f"repacked weights; repack {np.median(repack_ms):.3f} ms per layer (median)",
+          file=sys.stderr, flush=True)
+
+    xs = {}
+    for K in sorted({K for _, _, K in LAYER_M1}):
+        for M in SWEEP_M:
+            x = synthetic.activations(M, K, 100 + M)
+            xs[(M, K)] = torch.from_numpy(x.view(np.int16)).to(dev).view(torch.bfloat16)
+    forward = []
+    for M in SWEEP_M:
+        per_shape = {}
+        for name, N, K in LAYER_M1:
+            x = xs[(M, K)]
+
+            def fwd(x=x, name=name):
+                for lin in layers[name]:
+                    kern.apply_weights(lin, x)
+
+            reps = 3 if M >= 512 else 10
+            per_shape[name] = _timed_graph(fwd, reps)
+        ms = sum(per_shape.values())
+        flop = 2.0 * M * sum(N * K for _, N, K in LAYER_M1) * n_layers
+        nbytes = n_layers * sum(gemm_bytes(M, N, K) for _, N, K in LAYER_M1)
+        forward.append(dict(M=M, ms_per_forward=round(ms, 3),
+                            us_per_layer=round(ms * 1e3 / n_layers, 2),
+                            per_shape_us_per_layer={k: round(v * 1e3 / n_layers, 2)
+                                                    for k, v in per_shape.items()},
+                            tflops=round(flop / (ms * 1e-3) / 1e12, 1),
+                            gbs=round(nbytes / (ms * 1e-3) / 1e9, 1),
+                            plans={name: list(_native.plan(M, N, K)) for name, N, K in LAYER_M1}))
+        print(f"[bench] sweep M={M}: {ms:.3f} ms per forward of {n_layers} layers "
+              f"({forward[-1]['per_shape_us_per_layer']} us per layer)", file=sys.stderr,
+              flush=True)
+
+    # crossover: GEMM only (pre-quantized activations), 16 layers' weights rotating. The decode
+    # family is the streaming kernel where it serves (M <= 16), else the skinny kernel with the
+    # M-fragments covering M; the tile family is the macro-tile shape the plan picks at M.
+    skinny = _native.variants(_native.KERNEL_SKINNY)
+    cross = {}
+    for name, N, K in LAYER_M1:
+        rows = []
+        for M in CROSSOVER_M:
+            q, sc = R.quant_per_token(xs[(4096, K)][:M].contiguous())
+            out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+            lins = layers[name][:16]
+
+            def run(kernel, variant, split, q=q, sc=sc, out=out, lins=lins, M=M):
+                for lin in lins:
+                    _native.gemm(q.data_ptr(), sc.data_ptr(), lin.weight.data_ptr(),
+                                 lin.weight_scale.data_ptr(), out.data_ptr(), M, N, K,
+                                 torch.cuda.current_stream().cuda_stream, kernel, variant, split)
+
+            tile_v = _native.plan(max(M, 17), N, K)[1]
+            row = dict(M=M, tile_us=round(_timed_graph(
+                lambda: run(_native.KERNEL_TILE, tile_v, 1), 5) * 1e3 / 16, 2))
+            k, v, sp = _native.plan(M, N, K)
+            if k != _native.KERNEL_STREAM and M <= 64:
+                ntiles = -(-N // 16)
+                waves = 4 if ntiles >= 512 else 8 if ntiles >= 128 else 16
+                k, sp = _native.KERNEL_SKINNY, 1
+                v = next(i for i, c in enumerate(skinny)
+                         if c[0] == -(-M // 16) and c[1] == 1 and c[2] == waves)
+            if k != _native.KERNEL_TILE:
+                row["decode_us"] = round(_timed_graph(lambda: run(k, v, sp), 5) * 1e3 / 16, 2)
+                row["decode_kernel"] = "stream" if k == _native.KERNEL_STREAM else "skinny"
+            rows.append(row)
+        tile_wins = [r["M"] for r in rows if "decode_us" in r and r["tile_us"] <= r["decode_us"]]
+        cross[name] = dict(rows=rows, tile_wins_from_M=min(tile_wins) if tile_wins else None)
+        print(f"[bench] crossover {name}: {rows}", file=sys.stderr, flush=True)
+    return dict(layers=n_layers, weight_gb=round(weight_bytes * n_layers / 1e9, 3),
+                repack_ms_per_layer_median=round(float(np.median(repack_ms)), 4),
+                repack_ms_total=round(float(np.sum(repack_ms)), 2), forward=forward,
+                crossover=cross, plan_stream_max_M=16)
+
+
 CALIBRATION_BYTES = 256 * 2 ** 20
 
 
@@ -286,6 +433,14 @@ def main():
         profile_workload()
         return
     R.ensure_scratch(torch.device("cuda", 0))
+    if args.sweep:
+        sw = bench_sweep(args.sweep_layers)
+        print(json.dumps({"metric": "64-layer MXFP4 W4A8 linear sweep, ms per forward",
+                          "n_gpus": 1, "data": "synthetic, random-init layers",
+                          "config": {"workload": "Qwen3.8-27B-shaped linear set x "
+                                                 f"{args.sweep_layers} layers",
+                                     "M": SWEEP_M}, "sweep": sw}), flush=True)
+        return
     v = bench_verify(args)
     print(f"[bench] verify M=8: {v['kernel_us']:.2f} us/launch in the graph-timed region, "
           f"event pairs {v['event_pair_us_median']:.2f} us median, plan {v['plan']}",

@@ -106,16 +106,30 @@ def test_split_k_without_scratch_is_refused(lib):
 
 def test_plan_bands(lib):
     k, v, s = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
-    # M <= 16: the streaming family when a wave's run and the LDS staging fit; then skinny to 64;
-    # then macro-tile. N=17408 K=8704 would need 43-granule runs, past the largest stream variant;
-    # K=640 has fewer k-tiles per n-tile than the smallest run.
+    # M <= 16: the streaming family when a wave's run and the LDS staging fit, else skinny; above
+    # M = 16 the macro-tile family. N=17408 K=8704 would need 43-granule runs, past the largest
+    # stream variant; K=640 has fewer k-tiles per n-tile than the smallest run.
     for M, N, K, kernel in [(1, 17408, 5120, 3), (8, 17408, 5120, 3), (16, 17408, 5120, 3),
                             (8, 5120, 8704, 3), (8, 17408, 8704, 1), (8, 33, 640, 1),
-                            (17, 17408, 5120, 1), (64, 17408, 5120, 1), (65, 17408, 5120, 2),
+                            (17, 17408, 5120, 2), (64, 17408, 5120, 2), (65, 17408, 5120, 2),
                             (4096, 17408, 5120, 2)]:
         assert lib.w4a8_plan(M, N, K, ctypes.byref(k), ctypes.byref(v), ctypes.byref(s)) == 0
         assert (M, N, K, k.value) == (M, N, K, kernel) and v.value >= 0 and s.value >= 1
     assert lib.w4a8_plan(8, 17408, 5000, ctypes.byref(k), ctypes.byref(v), ctypes.byref(s)) == 1
+
+
+@pytest.mark.parametrize("M,N,K,wave_tile", [
+    # small M: the smallest tile whose workgroup count stays within 5/8 of 256 CUs
+    (32, 10240, 5120, (1, 2)), (32, 17408, 5120, (1, 4)), (64, 17408, 5120, (2, 4)),
+    (64, 5120, 8704, (1, 2)), (128, 5120, 6144, (1, 4)), (128, 17408, 5120, (4, 4)),
+    (256, 17408, 5120, (4, 4)),
+    # prefill: 256 x 256 for wide N, 256 x 160 when N splits into 160-column tiles
+    (1024, 17408, 5120, (4, 4)), (4096, 17408, 5120, (8, 8)), (4096, 5120, 8704, (8, 5))])
+def test_plan_tile_shapes(lib, M, N, K, wave_tile):
+    k, v, s = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    assert lib.w4a8_plan(M, N, K, ctypes.byref(k), ctypes.byref(v), ctypes.byref(s)) == 0
+    assert k.value == 2
+    assert _native.variants(2)[v.value][:2] == wave_tile
 
 
 def test_variant_tables(lib):

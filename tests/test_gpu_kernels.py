@@ -269,7 +269,7 @@ def test_mfma_model_matches_device_on_random_granules(gpu_lib):
 DECODE_SHAPES = [(5120, 5120), (17408, 5120), (5120, 8704), (48, 5120), (33, 640), (10240, 96)]
 
 
-@pytest.mark.parametrize("M", [1, 2, 8, 16, 17, 33, 64])
+@pytest.mark.parametrize("M", [1, 2, 8, 16, 17, 24, 33, 48, 64])
 @pytest.mark.parametrize("N,K", DECODE_SHAPES)
 def test_gemm_decode_band_auto_plan(gpu_lib, scratch, M, N, K):
     x = synthetic.activations(M, K, seed=11 * M + K)

@@ -128,10 +128,23 @@ int find_stream(int M, int N, int K, int dev) {
   return best;
 }
 
-// Decode / verify band: M <= 64 streams the weights once. M <= 16 takes the streaming family
-// when a variant fits (whole-K workgroups, every weight load in flight at once); otherwise the
-// skinny family, whose workgroup count should cover the 256 CUs several times over; for small N
-// the K dimension is split across workgroups too.
+// Smallest-area macro tile, in the order 32x64, 32x128, 64x128, 128x128, whose workgroup count
+// stays within 5/8 of the CUs: at M <= 256 the tile GEMM streams the weights once per row block,
+// and on MI355X fewer, longer workgroups beat one workgroup per CU (measured on the Qwen3.8-27B
+// linear shapes at M = 24..256).
+int small_m_tile(int M, int N, int cus) {
+  static const int cand[][2] = {{1, 2}, {1, 4}, {2, 4}, {4, 4}};
+  for (const auto& c : cand) {
+    const int bm = 32 * c[0], bn = 32 * c[1];
+    if ((long)ceil_div(M, bm) * ceil_div(N, bn) <= (long)cus * 5 / 8) return find_tile(c[0], c[1]);
+  }
+  return find_tile(4, 4);
+}
+
+// Decode / verify band: M <= 16 takes the streaming family when a variant fits (whole-K
+// workgroups, every weight load in flight at once), else the skinny family, whose workgroup count
+// should cover the 256 CUs several times over (for small N the K dimension is split across
+// workgroups too). Above M = 16 the macro-tile family wins from M = 24 on every Qwen3.8-27B shape.
 void plan_impl(int M, int N, int K, int dev, int* kernel, int* variant, int* split_k) {
   if (M <= 16) {
     const int v = find_stream(M, N, K, dev);
@@ -141,30 +154,28 @@ void plan_impl(int M, int N, int K, int dev, int* kernel, int* variant, int* spl
       *split_k = 1;
       return;
     }
-  }
-  if (M <= 64) {
-    const int mt = M <= 16 ? 1 : ceil_div(M, 16);
     const int ntiles = padded_n(N) / kNTile;
     int waves = ntiles >= 512 ? 4 : ntiles >= 128 ? 8 : 16;
-    int v = find_skinny(mt, 1, waves);
+    int v2 = find_skinny(1, 1, waves);
     int ks = 1;
     const int kte = ceil_div(K, kKTile);
     if (ntiles < 128) {
       for (int c = 2; c <= 16 && ntiles * ks < 256; c *= 2)
-        if (c <= kte / 2 && scratch_fits(dev, v, N, c)) ks = c;
+        if (c <= kte / 2 && scratch_fits(dev, v2, N, c)) ks = c;
     }
     *kernel = W4A8_KERNEL_SKINNY;
-    *variant = v;
+    *variant = v2;
     *split_k = ks;
     return;
   }
   // Prefill band (measured on MI355X): 256 x 256 tiles for wide N, 256 x 160 where N divides into
-  // 160-column tiles that fill the CUs evenly (N = 5120: 512 tiles at M = 4096), 128 x 128 below.
+  // 160-column tiles that fill the CUs evenly (N = 5120: 512 tiles at M = 4096), 128 x 128 from
+  // M = 512, and below that the small-M rule.
   *kernel = W4A8_KERNEL_TILE;
   if (M >= 2048 && N % 160 == 0 && N <= 8192) *variant = find_tile(8, 5);
   else if (M >= 2048) *variant = find_tile(8, 8);
-  else if (M >= 256) *variant = find_tile(4, 4);
-  else *variant = find_tile(2, 4);
+  else if (M > 256) *variant = find_tile(4, 4);
+  else *variant = small_m_tile(M, N, device_info(dev).cus);
   *split_k = 1;
 }
 

@@ -243,7 +243,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tile(
 // (WM, WN, NS): wave tile 16 WM x 16 WN, NS-stage LDS pipeline (LDS = NS * STAGE <= 160 KiB)
 #define W4A8_TILE_TABLE(X)                                                                        \
   X(2, 4, 4) X(4, 4, 3) X(4, 4, 4) X(8, 4, 3) X(4, 8, 3) X(8, 8, 3) X(8, 5, 3) X(4, 8, 4)          \
-  X(4, 2, 4)
+  X(4, 2, 4) X(1, 2, 4) X(2, 2, 4) X(1, 4, 4) X(2, 2, 5)
 
 #define W4A8_TILE_CFG(wm, wn, ns) TileCfg{wm, wn, TileShape<wm, wn>::BM, TileShape<wm, wn>::BN},
 constexpr TileCfg kTile[] = {W4A8_TILE_TABLE(W4A8_TILE_CFG)};
