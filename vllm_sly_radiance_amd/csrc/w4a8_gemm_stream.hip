@@ -8,7 +8,8 @@
 // of that size is fastest with one workgroup per CU whose waves each issue one contiguous
 // ~20 KiB run of 128-bit loads before using any; a second round of workgroups, grid-stride loops
 // or per-granule branching all cost 10-60 %. So:
-//  * The grid is min(n-tiles, CUs). Workgroup b owns the n-tile range
+//  * The grid is at most one workgroup per CU, sized so every workgroup owns the same number of
+//    n-tiles (NTMAX = ceil(n-tiles / CUs)). Workgroup b owns the n-tile range
 //    [b * NTILES / G, (b + 1) * NTILES / G) (at most NTMAX n-tiles); its W = NTMAX * S waves each
 //    own one (n-tile, K split) pair, a contiguous run of whole 4-granule groups in the granule
 //    layout ([n-tile][k-tile][lane][16 B]) - so no run crosses an n-tile and one scale dword
@@ -16,9 +17,10 @@
 //  * Every global load goes through a buffer resource; granules past the run load as zero without
 //    a memory access, so the MFMA loop has no branches and the compiler counts outstanding loads
 //    exactly. All of a wave's weight loads and scale dwords are issued before it waits.
-//  * The activations (M rows x K, L2-resident, shared by every workgroup) are loaded first and
-//    staged in LDS, row-major with a 16-byte row pad so the 16 lanes of a fragment read hit
-//    distinct banks, plus one zero row for the fragment lanes of tokens past the staged rows.
+//  * The activations (M rows x K, L2-resident, shared by every workgroup) are loaded after the
+//    weights and staged in LDS, row-major with a 16-byte row pad so the 16 lanes of a fragment
+//    read hit distinct banks, plus one zero row for the fragment lanes of tokens past the staged
+//    rows.
 //  * Run bounds and offsets are wave-uniform scalar arithmetic (the wave index comes through
 //    readfirstlane), so the per-granule code is a load, a shift, two LDS reads and an MFMA.
 //  * The S partial sums of an n-tile meet in LDS and are added in split order (deterministic),
@@ -27,6 +29,12 @@
 
 namespace w4a8 {
 namespace {
+
+// Byte offset of the split-reduction buffer: past the RP + 1 staged rows, 16-byte aligned.
+template <int RP>
+__host__ __device__ constexpr size_t red_offset_rp(int K) {
+  return ((size_t)(RP + 1) * (K + 16) + 15) / 16 * 16;
+}
 
 // U: granules per wave at most (a multiple of 4); W: waves per workgroup; RP: activation rows
 // staged (8 or 16, M <= RP); AM: 16-byte activation chunks per thread, so K <= AM * (64 W / RP) * 16.
@@ -55,20 +63,7 @@ __global__ __launch_bounds__(W * 64) void gemm_stream(
   const float tok_scale = __builtin_bit_cast(
       float, __builtin_amdgcn_raw_buffer_load_b32(as_src, (lane & 15) * 4, 0, 0));
 
-  // ---- 1. activation loads (L2), before the weights: a load issued after them would retire
-  //         behind the whole weight stream. Thread t stages row t / TPR, 16-byte chunks
-  //         t % TPR + TPR * c; rows at or past M read as zero ----
-  const int srow = tid / TPR, scol = tid % TPR;
-  const auto ra_src = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, M * K, kBufferWord3);
-  v4i ra[AM];
-#pragma unroll
-  for (int c = 0; c < AM; ++c) {
-    const int col = scol + c * TPR;
-    ra[c] = __builtin_amdgcn_raw_buffer_load_b128(
-        ra_src, col * 16 < K ? srow * K + col * 16 : kOut, 0, 0);
-  }
-
-  // ---- 2. this wave's granules: n-tile ntb0 + j, k-tiles [kr0, kr1), at most U of them ----
+  // ---- 1. this wave's granules: n-tile ntb0 + j, k-tiles [kr0, kr1), at most U of them ----
   const int nt = ntb0 + j;
   const auto w_src = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(Wq + (size_t)nt * KT * kGranuleBytes), 0, active ? kr1 * kGranuleBytes : 0,
@@ -86,6 +81,21 @@ __global__ __launch_bounds__(W * 64) void gemm_stream(
                                                        0);
   }
 
+  // ---- 2. activation loads (L2), after the weights: they retire behind this wave's weight
+  //         stream, so the MFMAs below run once every granule has landed - measured on MI355X,
+  //         that beats putting ~40 KiB of L2 reads ahead of every workgroup's weight stream.
+  //         Thread t stages row t / TPR, 16-byte chunks t % TPR + TPR * c; rows at or past M read
+  //         as zero ----
+  const int srow = tid / TPR, scol = tid % TPR;
+  const auto ra_src = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, M * K, kBufferWord3);
+  v4i ra[AM];
+#pragma unroll
+  for (int c = 0; c < AM; ++c) {
+    const int col = scol + c * TPR;
+    ra[c] = __builtin_amdgcn_raw_buffer_load_b128(
+        ra_src, col * 16 < K ? srow * K + col * 16 : kOut, 0, 0);
+  }
+
   // ---- 3. stage the activations in LDS: rows 0..RP-1 (zero past M) plus a zero row RP that
   //         the fragment lanes of tokens >= RP read ----
 #pragma unroll
@@ -98,30 +108,35 @@ __global__ __launch_bounds__(W * 64) void gemm_stream(
   __syncthreads();
 
   // ---- 4. MFMAs, branch-free: granules past the run are zero and add nothing. Fragment lane
-  //         (token l % 16, g = l / 16) reads k 16g.. and 64 + 16g..; two accumulator chains ----
-  constexpr int CH = 2;
+  //         (token l % 16, g = l / 16) reads k 16g.. and 64 + 16g..; the fragment of granule
+  //         u + 1 is read before granule u's MFMA, and four accumulator chains keep the MFMAs
+  //         independent once the last granules land together ----
+  constexpr int CH = 4;
   v4f acc[CH];
 #pragma unroll
   for (int c = 0; c < CH; ++c) acc[c] = v4f{0.f, 0.f, 0.f, 0.f};
   const int m = lane & 15;
   const uint8_t* xrow = lds + (m < RP ? m : RP) * ldr + (lane >> 4) * 16;
   if (active) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int kt = kr0 + u < KT ? kr0 + u : KT - 1;      // stays inside the staged row
+    auto frag = [&](int u) {
+      const int kt = kr0 + u < KT ? kr0 + u : KT - 1;    // stays inside the staged row
       const v4i lo = *reinterpret_cast<const v4i*>(xrow + kt * kKTile);
       const v4i hi = *reinterpret_cast<const v4i*>(xrow + kt * kKTile + 64);
-      const v8i xf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      acc[u % CH] = mfma_w4a8(wv[u], xf, acc[u % CH], sv[u / 4] >> (8 * (u & 3)));
+      return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
+    v8i xf = frag(0);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const v8i cur = xf;
+      if (u + 1 < U) xf = frag(u + 1);
+      acc[u % CH] = mfma_w4a8(wv[u], cur, acc[u % CH], sv[u / 4] >> (8 * (u & 3)));
     }
   }
-  v4f sum = acc[0];
-#pragma unroll
-  for (int c = 1; c < CH; ++c) sum += acc[c];
+  v4f sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
 
-  // ---- 5. the S partial sums of each n-tile meet in LDS and are added in split order ----
-  __syncthreads();                               // the activation buffer becomes the reduce buffer
-  v4f* red = reinterpret_cast<v4f*>(lds);
+  // ---- 5. the S partial sums of each n-tile meet in LDS (a region of their own, past the
+  //         staged rows) and are added in split order ----
+  v4f* red = reinterpret_cast<v4f*>(lds + red_offset_rp<RP>(K));
   red[wave * 64 + lane] = sum;
   __syncthreads();
   const bool vec = vec_out != 0;
@@ -152,17 +167,21 @@ constexpr int kStreamCount = sizeof(kStream) / sizeof(kStream[0]);
 int stream_variant_count() { return kStreamCount; }
 StreamCfg stream_variant(int v) { return kStream[v]; }
 
+// The fewest workgroups that keep the largest n-tile share of min(n-tiles, CUs) workgroups: every
+// workgroup then carries the same share (N = 17408: 218 workgroups of 5 n-tiles rather than 256
+// of 4 or 5), which measured 5 % faster on MI355X than one workgroup per CU.
 int stream_grid(int N, int cus) {
   const int ntiles = padded_n(N) / kNTile;
-  return ntiles < cus ? ntiles : cus;
+  const int g = ntiles < cus ? ntiles : cus;
+  return ceil_div(ntiles, ceil_div(ntiles, g));
 }
 
 size_t stream_lds_bytes(int variant, int M, int K) {
   (void)M;
   const StreamCfg c = kStream[variant];
-  const size_t act = (size_t)(c.mt + 1) * (K + 16);      // RP rows + the zero row
-  const size_t red = (size_t)c.waves * 64 * sizeof(v4f);
-  return act > red ? act : red;
+  // RP rows + the zero row, then the split-reduction buffer
+  const size_t act = c.mt == 8 ? red_offset_rp<8>(K) : red_offset_rp<16>(K);
+  return act + (size_t)c.waves * 64 * sizeof(v4f);
 }
 
 // K splits per n-tile for a variant on this shape (0: the variant cannot serve it).

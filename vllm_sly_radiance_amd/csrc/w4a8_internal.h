@@ -112,7 +112,7 @@ int skinny_counter_count(int variant, int N);
 hipError_t launch_skinny(const GemmArgs& g, int variant, int split_k, float* partial,
                          int* counters, hipStream_t stream);
 
-// Streaming family (M <= 16, K % 512 == 0): grid = min(n-tiles, CUs), waves = (n-tile, K split)
+// Streaming family (M <= 16, K % 512 == 0): grid = at most one workgroup per CU, each with the same number of n-tiles; waves = (n-tile, K split)
 // pairs holding at most t granules each, activations staged in LDS. variant indexes the
 // instantiated table; mt = staged activation rows (8 or 16, M <= mt), am = activation chunks per
 // thread.
