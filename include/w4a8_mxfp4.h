@@ -96,9 +96,10 @@ int w4a8_gemm_planned(const void* a, const float* a_scale, const void* wq, const
 /* Number of instantiated variants of a kernel family, and their parameters:
  * skinny: p = {MT (16-token fragments), NT (n-tiles per workgroup), waves, unroll};
  * tile:   p = {WM, WN (MFMA tiles per wave), BM, BN (workgroup tile)};
- * stream: p = {MT, U (granules per wave at most), waves, activation chunks per thread}. A stream
- *         variant serves (M, N, K) only when a wave's run fits U and the activations fit its LDS
- *         and register staging; forcing one that does not returns W4A8_EINVAL. */
+ * stream: p = {NT (n-tiles per workgroup at most), KPW (k-tiles per wave at most), waves,
+ *         NT * KPW (granules per wave at most)}. A stream variant serves (M, N, K) only when
+ *         M <= 16, K % 512 == 0 and the shape's n-tiles per workgroup and k-tiles per wave fit it;
+ *         forcing one that does not returns W4A8_EINVAL. */
 int w4a8_variant_count(int kernel);
 int w4a8_variant_info(int kernel, int variant, int* p0, int* p1, int* p2, int* p3);
 

@@ -117,14 +117,17 @@ bool scratch_fits(int dev, int variant, int N, int split_k) {
          (size_t)skinny_counter_count(variant, N) * sizeof(int) <= s.counter_bytes;
 }
 
-// The smallest stream variant that serves (M, N, K): fewest registers held per wave.
+// The stream variant that serves (M, N, K) with the fewest granules on its busiest wave, then the
+// fewest n-tile slots, then the fewest waves.
 int find_stream(int M, int N, int K, int dev) {
   const DeviceInfo d = device_info(dev);
-  int best = -1;
-  for (int v = 0; v < stream_variant_count(); ++v)
-    if (stream_fits(v, M, N, K, d.cus, d.lds) &&
-        (best < 0 || stream_variant(v).t < stream_variant(best).t))
-      best = v;
+  int best = -1, best_key = 0;
+  for (int v = 0; v < stream_variant_count(); ++v) {
+    if (!stream_fits(v, M, N, K, d.cus, d.lds)) continue;
+    const StreamCfg c = stream_variant(v);
+    const int key = (stream_granules(v, N, K, d.cus) * 64 + c.nt) * 64 + c.waves;
+    if (best < 0 || key < best_key) best = v, best_key = key;
+  }
   return best;
 }
 
@@ -324,7 +327,7 @@ W4A8_API int w4a8_variant_info(int kernel, int variant, int* p0, int* p1, int* p
     v[0] = c.wm; v[1] = c.wn; v[2] = c.bm; v[3] = c.bn;
   } else if (kernel == W4A8_KERNEL_STREAM && variant >= 0 && variant < stream_variant_count()) {
     const StreamCfg c = stream_variant(variant);
-    v[0] = c.mt; v[1] = c.t; v[2] = c.waves; v[3] = c.am;
+    v[0] = c.nt; v[1] = c.kpw; v[2] = c.waves; v[3] = c.u;
   } else {
     return fail(W4A8_EINVAL, "w4a8_variant_info: no variant %d of kernel %d", variant, kernel);
   }

@@ -1,163 +1,139 @@
-// Streaming W4A8 GEMM for decode M (1..16) on gfx950: one workgroup per CU, every weight byte of a
-// wave requested before the wave waits on anything.
+// Streaming W4A8 GEMM for decode M (1..16) on gfx950: one workgroup per CU at most, every weight
+// byte of a wave requested before the wave waits on anything.
 //
 // Counterpart of the reference's decode kernel (sly/mxfp4/radiance_mxfp4_fp8.hip:981-1228) for the
 // M <= 16 band, redesigned around the MI355X memory system. At M <= 16 the GEMM is a weight stream
 // (47 MB for the 17408 x 5120 gate/up), bounded by how early and how evenly the whole matrix is
-// requested and by how little instruction work sits between the loads. Measured on MI355X, a read
-// of that size is fastest with one workgroup per CU whose waves each issue one contiguous
-// ~20 KiB run of 128-bit loads before using any; a second round of workgroups, grid-stride loops
-// or per-granule branching all cost 10-60 %. So:
+// requested and by how little work is left once the last bytes land. Measured on MI355X:
+//  * a read of that size is fastest with one workgroup per CU whose waves each hold ~20 KiB of
+//    128-bit loads in flight, all issued before any is used;
+//  * a per-wave timeline (s_memrealtime) of a design that staged the activations in LDS and gave
+//    each wave one n-tile showed the stream done at ~7.5 us and then 1.6 us of MFMA work bound by
+//    LDS reads (every wave re-read its 16-row activation fragments for every granule).
+// So:
 //  * The grid is at most one workgroup per CU, sized so every workgroup owns the same number of
-//    n-tiles (NTMAX = ceil(n-tiles / CUs)). Workgroup b owns the n-tile range
-//    [b * NTILES / G, (b + 1) * NTILES / G) (at most NTMAX n-tiles); its W = NTMAX * S waves each
-//    own one (n-tile, K split) pair, a contiguous run of whole 4-granule groups in the granule
-//    layout ([n-tile][k-tile][lane][16 B]) - so no run crosses an n-tile and one scale dword
-//    serves four granules.
-//  * Every global load goes through a buffer resource; granules past the run load as zero without
-//    a memory access, so the MFMA loop has no branches and the compiler counts outstanding loads
-//    exactly. All of a wave's weight loads and scale dwords are issued before it waits.
-//  * The activations (M rows x K, L2-resident, shared by every workgroup) are loaded after the
-//    weights and staged in LDS, row-major with a 16-byte row pad so the 16 lanes of a fragment
-//    read hit distinct banks, plus one zero row for the fragment lanes of tokens past the staged
-//    rows.
-//  * Run bounds and offsets are wave-uniform scalar arithmetic (the wave index comes through
-//    readfirstlane), so the per-granule code is a load, a shift, two LDS reads and an MFMA.
-//  * The S partial sums of an n-tile meet in LDS and are added in split order (deterministic),
-//    scaled by the per-token fp32 scale and stored as bf16. Nothing crosses workgroups.
+//    n-tiles: workgroup b owns [b * NTILES / G, (b + 1) * NTILES / G), at most NT of them.
+//  * Wave w owns the k-groups [KG w / W, KG (w + 1) / W) (4 k-tiles each, so one scale dword per
+//    n-tile) of every n-tile of the workgroup. It loads its activation fragments for those
+//    k-tiles straight into registers (lane l: token l % 16, k 16 (l / 16).. and 64 + 16 (l / 16)..;
+//    tokens past M read as zero), then the scale dwords, then the granules k-tile by k-tile, and
+//    multiplies each fragment into all NT n-tiles as their granules land: no LDS staging, no
+//    barrier before the MFMAs, NT independent accumulator chains.
+//  * Every global load goes through a buffer resource; loads past the workgroup's n-tiles or the
+//    wave's k-range return zero without a memory access, so the code has no branches around loads
+//    and the compiler counts outstanding loads exactly.
+//  * The W partial sums of each n-tile meet once in LDS and are added in wave order
+//    (deterministic), scaled by the per-token fp32 scale and stored as bf16. Nothing crosses
+//    workgroups.
 #include "w4a8_internal.h"
 
 namespace w4a8 {
 namespace {
 
-// Byte offset of the split-reduction buffer: past the RP + 1 staged rows, 16-byte aligned.
-template <int RP>
-__host__ __device__ constexpr size_t red_offset_rp(int K) {
-  return ((size_t)(RP + 1) * (K + 16) + 15) / 16 * 16;
-}
-
-// U: granules per wave at most (a multiple of 4); W: waves per workgroup; RP: activation rows
-// staged (8 or 16, M <= RP); AM: 16-byte activation chunks per thread, so K <= AM * (64 W / RP) * 16.
-// The host requires K % 512 == 0: whole k-tiles, whole 4-k-tile scale groups, no K padding.
-template <int U, int W, int RP, int AM>
+// NT: n-tiles per workgroup at most; KPW: k-tiles per wave at most (a multiple of 4); W: waves.
+// The host requires K % 512 == 0 (whole k-groups), M <= 16, 4 * ceil(KG / W) <= KPW.
+template <int NT, int KPW, int W>
 __global__ __launch_bounds__(W * 64) void gemm_stream(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
     const uint32_t* __restrict__ Sq, uint16_t* __restrict__ C, int M, int N, int K, int KT,
-    int KG, int NTILES, int S, int vec_out) {
-  static_assert(U % 4 == 0 && (RP == 8 || RP == 16) && (W * 64) % RP == 0, "stream variant");
-  constexpr int TPR = W * 64 / RP;               // staging threads per activation row
+    int KG, int NTILES, int vec_out) {
+  static_assert(KPW % 4 == 0 && NT >= 1 && W >= 1 && W <= 16, "stream variant");
   constexpr int kOut = 0x7FFFFFF0;               // an offset past every buffer resource here
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   // Wave-uniform work selection in scalar registers; 32-bit products only (the host bounds them).
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = gridDim.x, b = blockIdx.x;
-  const int ntb0 = b * NTILES / G, ntb1 = (b + 1) * NTILES / G;
-  const int j = wave / S, split = wave - j * S;            // this wave's n-tile (local), K split
-  const bool active = j < ntb1 - ntb0;
-  const int kr0 = 4 * ((KT >> 2) * split / S), kr1 = 4 * ((KT >> 2) * (split + 1) / S);
-  const int ldr = K + 16;
+  const int ntb0 = b * NTILES / G, nth = (b + 1) * NTILES / G - ntb0;
+  const int kr0 = 4 * (KG * wave / W), kr1 = 4 * (KG * (wave + 1) / W);
 
-  // the epilogue's per-token scale (token lane % 16), fetched first so it never waits at the end
+  // ---- 1. activation fragments of k-tiles kr0.. (L2): token lane % 16, two 16-byte runs.
+  //         Tokens past M fall outside the buffer and read as zero; a k-tile past the wave's
+  //         range re-reads the row's last k-tile (clamped in scalar arithmetic), which only ever
+  //         meets zero weights ----
+  const int m = lane & 15, g = lane >> 4;
+  const auto a_src = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, M * K, kBufferWord3);
+  v4i xlo[KPW], xhi[KPW];
+#pragma unroll
+  for (int u = 0; u < KPW; ++u) {
+    const int kt = min(kr0 + u, KT - 1);
+    const int off = m * K + kt * kKTile + 16 * g;
+    xlo[u] = __builtin_amdgcn_raw_buffer_load_b128(a_src, off, 0, 0);
+    xhi[u] = __builtin_amdgcn_raw_buffer_load_b128(a_src, off + 64, 0, 0);
+  }
+
+  // ---- 2. scale dwords (one per n-tile and k-group), then the granules k-tile by k-tile.
+  //         One buffer resource per n-tile, sized to end at the wave's k-range: loads past it,
+  //         or of n-tile slots past the workgroup's share, return zero ----
+  uint32_t sv[NT][KPW / 4];
+  v4i wv[KPW][NT];
+  {
+    __amdgpu_buffer_rsrc_t w_src[NT], s_src[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const bool have = t < nth;
+      w_src[t] = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(Wq + (size_t)(ntb0 + t) * KT * kGranuleBytes), 0,
+          have ? kr1 * kGranuleBytes : 0, kBufferWord3);
+      s_src[t] = __builtin_amdgcn_make_buffer_rsrc((void*)(Sq + (size_t)(ntb0 + t) * KG * 64), 0,
+                                                   have ? (kr1 >> 2) * 256 : 0, kBufferWord3);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int q = 0; q < KPW / 4; ++q)
+        sv[t][q] = __builtin_amdgcn_raw_buffer_load_b32(
+            s_src[t], (((kr0 >> 2) + q) * 64 + lane) * 4, 0, 0);
+#pragma unroll
+    for (int u = 0; u < KPW; ++u)
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        wv[u][t] = __builtin_amdgcn_raw_buffer_load_b128(
+            w_src[t], (kr0 + u) * kGranuleBytes + lane * 16, 0, kBufferNT);
+  }
+  // the epilogue's per-token scale, last: it is needed last
   const auto as_src = __builtin_amdgcn_make_buffer_rsrc((void*)As, 0, M * 4, kBufferWord3);
   const float tok_scale = __builtin_bit_cast(
       float, __builtin_amdgcn_raw_buffer_load_b32(as_src, (lane & 15) * 4, 0, 0));
+  __builtin_amdgcn_sched_barrier(0);             // every load above is issued before any MFMA
 
-  // ---- 1. this wave's granules: n-tile ntb0 + j, k-tiles [kr0, kr1), at most U of them ----
-  const int nt = ntb0 + j;
-  const auto w_src = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(Wq + (size_t)nt * KT * kGranuleBytes), 0, active ? kr1 * kGranuleBytes : 0,
-      kBufferWord3);
-  const auto s_src = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(Sq + (size_t)nt * KG * 64), 0, active ? (kr1 >> 2) * 256 : 0, kBufferWord3);
-  v4i wv[U];
-  uint32_t sv[U / 4];
+  // ---- 3. MFMAs, branch-free: loads past the k-range or the n-tiles are zero and add nothing ----
+  v4f acc[NT];
 #pragma unroll
-  for (int u = 0; u < U; ++u) {                  // granule u (and, every 4th, its scale dword)
-    wv[u] = __builtin_amdgcn_raw_buffer_load_b128(w_src, (kr0 + u) * kGranuleBytes + lane * 16, 0,
-                                                  kBufferNT);
-    if (u % 4 == 0)
-      sv[u / 4] = __builtin_amdgcn_raw_buffer_load_b32(s_src, ((kr0 + u) >> 2) * 256 + lane * 4, 0,
-                                                       0);
+  for (int t = 0; t < NT; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < KPW; ++u) {
+    const v8i xf = {xlo[u][0], xlo[u][1], xlo[u][2], xlo[u][3],
+                    xhi[u][0], xhi[u][1], xhi[u][2], xhi[u][3]};
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      acc[t] = mfma_w4a8(wv[u][t], xf, acc[t], sv[t][u / 4] >> (8 * (u & 3)));
   }
 
-  // ---- 2. activation loads (L2), after the weights: they retire behind this wave's weight
-  //         stream, so the MFMAs below run once every granule has landed - measured on MI355X,
-  //         that beats putting ~40 KiB of L2 reads ahead of every workgroup's weight stream.
-  //         Thread t stages row t / TPR, 16-byte chunks t % TPR + TPR * c; rows at or past M read
-  //         as zero ----
-  const int srow = tid / TPR, scol = tid % TPR;
-  const auto ra_src = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, M * K, kBufferWord3);
-  v4i ra[AM];
+  // ---- 4. the W partial sums of each n-tile meet in LDS and are added in wave order ----
+  v4f* red = reinterpret_cast<v4f*>(lds);
 #pragma unroll
-  for (int c = 0; c < AM; ++c) {
-    const int col = scol + c * TPR;
-    ra[c] = __builtin_amdgcn_raw_buffer_load_b128(
-        ra_src, col * 16 < K ? srow * K + col * 16 : kOut, 0, 0);
-  }
-
-  // ---- 3. stage the activations in LDS: rows 0..RP-1 (zero past M) plus a zero row RP that
-  //         the fragment lanes of tokens >= RP read ----
-#pragma unroll
-  for (int c = 0; c < AM; ++c) {
-    const int col = scol + c * TPR;
-    if (col * 16 < K) *reinterpret_cast<v4i*>(lds + srow * ldr + col * 16) = ra[c];
-  }
-  for (int col = tid; col * 16 < K; col += W * 64)
-    *reinterpret_cast<v4i*>(lds + RP * ldr + col * 16) = v4i{0, 0, 0, 0};
-  __syncthreads();
-
-  // ---- 4. MFMAs, branch-free: granules past the run are zero and add nothing. Fragment lane
-  //         (token l % 16, g = l / 16) reads k 16g.. and 64 + 16g..; the fragment of granule
-  //         u + 1 is read before granule u's MFMA, and four accumulator chains keep the MFMAs
-  //         independent once the last granules land together ----
-  constexpr int CH = 4;
-  v4f acc[CH];
-#pragma unroll
-  for (int c = 0; c < CH; ++c) acc[c] = v4f{0.f, 0.f, 0.f, 0.f};
-  const int m = lane & 15;
-  const uint8_t* xrow = lds + (m < RP ? m : RP) * ldr + (lane >> 4) * 16;
-  if (active) {
-    auto frag = [&](int u) {
-      const int kt = kr0 + u < KT ? kr0 + u : KT - 1;    // stays inside the staged row
-      const v4i lo = *reinterpret_cast<const v4i*>(xrow + kt * kKTile);
-      const v4i hi = *reinterpret_cast<const v4i*>(xrow + kt * kKTile + 64);
-      return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    };
-    v8i xf = frag(0);
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const v8i cur = xf;
-      if (u + 1 < U) xf = frag(u + 1);
-      acc[u % CH] = mfma_w4a8(wv[u], cur, acc[u % CH], sv[u / 4] >> (8 * (u & 3)));
-    }
-  }
-  v4f sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-
-  // ---- 5. the S partial sums of each n-tile meet in LDS (a region of their own, past the
-  //         staged rows) and are added in split order ----
-  v4f* red = reinterpret_cast<v4f*>(lds + red_offset_rp<RP>(K));
-  red[wave * 64 + lane] = sum;
+  for (int t = 0; t < NT; ++t) red[(wave * NT + t) * 64 + lane] = acc[t];
   __syncthreads();
   const bool vec = vec_out != 0;
-  for (int slot = tid; slot < (ntb1 - ntb0) * 64; slot += W * 64) {
-    const int jj = slot >> 6;
-    v4f v = red[(jj * S) * 64 + lane];
-    for (int q = 1; q < S; ++q) v += red[(jj * S + q) * 64 + lane];
-    const int mm = lane & 15;                    // slot lane == this thread's lane
-    const int n = (ntb0 + jj) * kNTile + 4 * (lane >> 4);
-    if (mm < M) store_out4(C, N, mm, n, N, v, tok_scale, vec);
+  for (int slot = tid; slot < nth * 64; slot += W * 64) {
+    const int t = slot >> 6;                     // slot lane == this thread's lane
+    v4f v = red[t * 64 + lane];
+#pragma unroll 4
+    for (int w = 1; w < W; ++w) v += red[(w * NT + t) * 64 + lane];
+    const int n = (ntb0 + t) * kNTile + 4 * (lane >> 4);
+    if (m < M) store_out4(C, N, m, n, N, v, tok_scale, vec);
   }
 }
 
-// (U, W, RP, AM). S = W / (n-tiles per workgroup) K splits per n-tile; a split holds at most U
-// granules; M <= RP; K <= AM * (64 W / RP) * 16.
+// (NT, KPW, W): NT * KPW granules and 2 KPW activation runs per wave in registers; W waves at
+// most 4 per SIMD. Chosen per shape by the host: the fewest granules per wave, then the fewest
+// n-tile slots, then the fewest waves.
 #define W4A8_STREAM_TABLE(X)                                                                      \
-  X(20, 10, 8, 7) X(24, 10, 8, 7) X(12, 8, 8, 9) X(16, 8, 8, 9) X(20, 8, 8, 9) X(24, 8, 8, 9)     \
-  X(12, 12, 8, 6) X(20, 6, 8, 12) X(8, 16, 8, 5) X(20, 10, 16, 14) X(12, 8, 16, 17)              \
-  X(20, 8, 16, 17) X(12, 12, 16, 12)
+  X(1, 4, 16) X(1, 8, 16) X(2, 4, 10) X(2, 4, 12) X(2, 4, 16) X(2, 8, 9) X(3, 4, 10)              \
+  X(3, 4, 12) X(4, 4, 10) X(5, 4, 10) X(6, 4, 8) X(8, 4, 8)
 
-#define W4A8_STREAM_CFG(u, w, rp, am) StreamCfg{rp, u, w, am},
+#define W4A8_STREAM_CFG(nt, kpw, w) StreamCfg{nt, kpw, w, nt * kpw},
 constexpr StreamCfg kStream[] = {W4A8_STREAM_TABLE(W4A8_STREAM_CFG)};
 #undef W4A8_STREAM_CFG
 constexpr int kStreamCount = sizeof(kStream) / sizeof(kStream[0]);
@@ -178,53 +154,48 @@ int stream_grid(int N, int cus) {
 
 size_t stream_lds_bytes(int variant, int M, int K) {
   (void)M;
+  (void)K;
   const StreamCfg c = kStream[variant];
-  // RP rows + the zero row, then the split-reduction buffer
-  const size_t act = c.mt == 8 ? red_offset_rp<8>(K) : red_offset_rp<16>(K);
-  return act + (size_t)c.waves * 64 * sizeof(v4f);
+  return (size_t)c.waves * c.nt * 64 * sizeof(v4f);
 }
 
-// K splits per n-tile for a variant on this shape (0: the variant cannot serve it).
-int stream_splits(int variant, int N, int K, int cus) {
+// Granules the busiest wave of a variant streams for this shape (0: the variant cannot serve it).
+int stream_granules(int variant, int N, int K, int cus) {
   const StreamCfg c = kStream[variant];
-  const int G = stream_grid(N, cus);
-  const int ntmax = ceil_div(padded_n(N) / kNTile, G);
-  const int S = c.waves / ntmax;
-  if (S < 1 || K % 512) return 0;
-  const int KT = K / kKTile;
-  return 4 * ceil_div(KT / 4, S) <= c.t ? S : 0;
+  if (K % 512) return 0;
+  const int ntiles = padded_n(N) / kNTile;
+  const int ntmax = ceil_div(ntiles, stream_grid(N, cus));
+  const int kpw = 4 * ceil_div(K / kKAlign, c.waves);
+  if (ntmax > c.nt || kpw > c.kpw) return 0;
+  return ntmax * kpw;
 }
 
 bool stream_fits(int variant, int M, int N, int K, int cus, size_t lds_limit) {
+  if (M < 1 || M > 16 || stream_granules(variant, N, K, cus) == 0) return false;
   const StreamCfg c = kStream[variant];
-  if (K % 512 || M < 1 || M > c.mt || (long)K > (long)c.am * (64 * c.waves / c.mt) * 16) return false;
-  const int ntiles = padded_n(N) / kNTile;
-  const int G = stream_grid(N, cus);
-  // every index the kernel forms stays in 32 bits
-  const bool small = (long)(G + 1) * ntiles < (1L << 31) && (long)M * K < (1L << 31) &&
-                     (long)(K / kKTile) * kGranuleBytes < (1L << 31);
-  return small && G >= 1 && stream_splits(variant, N, K, cus) > 0 &&
-         stream_lds_bytes(variant, M, K) <= lds_limit;
+  // every offset the kernel forms stays in 32 bits
+  const bool small = (long)M * K < (1L << 31) && (long)c.nt * (K / kKTile) * kGranuleBytes <
+                     (1L << 31) && (long)padded_n(N) < (1L << 24);
+  return small && stream_lds_bytes(variant, M, K) <= lds_limit;
 }
 
 hipError_t launch_stream(const GemmArgs& g, int variant, int cus, hipStream_t stream) {
   const int KT = g.K / kKTile, KG = KT / kKGroup;
   const int NTILES = padded_n(g.N) / kNTile;
-  const int S = stream_splits(variant, g.N, g.K, cus);
   const int vec_out = (g.N % 4 == 0 && ((uintptr_t)g.c % 8) == 0) ? 1 : 0;
   const dim3 grid(stream_grid(g.N, cus)), block(kStream[variant].waves * 64);
   const size_t lds = stream_lds_bytes(variant, g.M, g.K);
   int idx = 0;
-#define W4A8_STREAM_LAUNCH(u, w, rp, am)                                                         \
+#define W4A8_STREAM_LAUNCH(nt, kpw, w)                                                           \
   if (idx++ == variant) {                                                                        \
     if (lds > 64 * 1024) {                                                                       \
-      const hipError_t e = hipFuncSetAttribute((const void*)gemm_stream<u, w, rp, am>,           \
+      const hipError_t e = hipFuncSetAttribute((const void*)gemm_stream<nt, kpw, w>,             \
                                                hipFuncAttributeMaxDynamicSharedMemorySize,       \
                                                (int)lds);                                        \
       if (e != hipSuccess) return e;                                                             \
     }                                                                                            \
-    hipLaunchKernelGGL((gemm_stream<u, w, rp, am>), grid, block, lds, stream, g.a, g.a_scale,    \
-                       g.wq, g.sq, g.c, g.M, g.N, g.K, KT, KG, NTILES, S, vec_out);              \
+    hipLaunchKernelGGL((gemm_stream<nt, kpw, w>), grid, block, lds, stream, g.a, g.a_scale, g.wq, \
+                       g.sq, g.c, g.M, g.N, g.K, KT, KG, NTILES, vec_out);                       \
     return hipGetLastError();                                                                    \
   }
   W4A8_STREAM_TABLE(W4A8_STREAM_LAUNCH)

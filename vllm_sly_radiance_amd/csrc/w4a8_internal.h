@@ -112,16 +112,16 @@ int skinny_counter_count(int variant, int N);
 hipError_t launch_skinny(const GemmArgs& g, int variant, int split_k, float* partial,
                          int* counters, hipStream_t stream);
 
-// Streaming family (M <= 16, K % 512 == 0): grid = at most one workgroup per CU, each with the same number of n-tiles; waves = (n-tile, K split)
-// pairs holding at most t granules each, activations staged in LDS. variant indexes the
-// instantiated table; mt = staged activation rows (8 or 16, M <= mt), am = activation chunks per
-// thread.
-struct StreamCfg { int mt, t, waves, am; };
+// Streaming family (M <= 16, K % 512 == 0): grid = at most one workgroup per CU, each with the
+// same number of n-tiles (at most nt); each of the `waves` waves owns a k-range of at most kpw
+// k-tiles across all of them (u = nt * kpw granules in registers). variant indexes the
+// instantiated table.
+struct StreamCfg { int nt, kpw, waves, u; };
 int stream_variant_count();
 StreamCfg stream_variant(int v);
 int stream_grid(int N, int cus);
 size_t stream_lds_bytes(int variant, int M, int K);
-int stream_splits(int variant, int N, int K, int cus);
+int stream_granules(int variant, int N, int K, int cus);
 bool stream_fits(int variant, int M, int N, int K, int cus, size_t lds_limit);
 hipError_t launch_stream(const GemmArgs& g, int variant, int cus, hipStream_t stream);
 
