@@ -104,10 +104,16 @@ def per_launch_us(g, n, stream_obj):
     return float(np.median(t)), float(np.mean(t))
 
 
-def graph_timed(g, steps, warmup):
+WARM_SECONDS = 1.0
+
+
+def graph_timed(g, steps, warmup, warm_seconds=WARM_SECONDS):
     """Capture one launch per weight copy into a HIP graph on a side stream, replay it on that same
     stream (warmup, then the timed region) and return (steps run, warmup run, seconds, per-launch
-    event median/mean). The events bracket the timed replays on the stream the kernels run on."""
+    event median/mean). The events bracket the timed replays on the stream the kernels run on.
+    Warmup runs at least `warmup` launches and at least `warm_seconds` of replays: MI355X raises
+    its clocks over the first few hundred milliseconds of load, and a cold GEMM reads up to 20 %
+    slow."""
     import torch
     stream = torch.cuda.Stream()
     n = len(g.w)
@@ -124,9 +130,13 @@ def graph_timed(g, steps, warmup):
     wreps = max(1, -(-warmup // n))
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
-        for _ in range(wreps):
-            graph.replay()
-        torch.cuda.synchronize()
+        done, t_end = 0, time.perf_counter() + warm_seconds
+        while done < wreps or time.perf_counter() < t_end:
+            for _ in range(max(1, wreps)):
+                graph.replay()
+            done += max(1, wreps)
+            torch.cuda.synchronize()
+        wreps = done
         e0.record(stream)
         for _ in range(reps):
             graph.replay()
@@ -235,9 +245,10 @@ SWEEP_M = [1, 8, 16, 64, 512, 4096]
 CROSSOVER_M = [8, 16, 17, 24, 32, 48, 64, 96, 128]
 
 
-def _timed_graph(fn, reps):
-    """Capture fn() into a HIP graph on a side stream, replay it once untimed and then `reps`
-    times between events on that stream; returns ms per replay."""
+def _timed_graph(fn, reps, warm_seconds=0.2):
+    """Capture fn() into a HIP graph on a side stream, replay it untimed for at least
+    `warm_seconds` (and at least once), then `reps` times between events on that stream; returns
+    ms per replay."""
     import torch
     stream = torch.cuda.Stream()
     torch.cuda.synchronize()
@@ -249,7 +260,12 @@ def _timed_graph(fn, reps):
         fn()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
-        graph.replay()
+        t_end = time.perf_counter() + warm_seconds
+        while True:
+            graph.replay()
+            torch.cuda.synchronize()
+            if time.perf_counter() >= t_end:
+                break
         e0.record(stream)
         for _ in range(reps):
             graph.replay()

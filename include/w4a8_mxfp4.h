@@ -84,7 +84,10 @@ int w4a8_gemm(const void* a, const float* a_scale, const void* wq, const void* s
 
 /* The plan w4a8_gemm would use: kernel (W4A8_KERNEL_*), variant index and K split. Counterpart of
  * the reference's band/split policy (sly/mxfp4/radiance_mxfp4_fp8.hip:1252-1343, :1390-1500) and
- * its Python replica band_map (sly/mxfp4/band_map.py:31-95). */
+ * its Python replica band_map (sly/mxfp4/band_map.py:31-95). For a macro-tile plan whose
+ * workgroups fill a CU each, w4a8_gemm may run the variant on the leading columns that fill whole
+ * rounds of workgroups and a 128 x 128 tile variant on the rest (two launches on the stream);
+ * w4a8_gemm_planned with the returned triple always makes one launch. */
 int w4a8_plan(int M, int N, int K, int* kernel, int* variant, int* split_k);
 
 /* w4a8_gemm with an explicit plan, for sweeps and tests (the reference forces cells through the

@@ -118,18 +118,19 @@ def test_plan_bands(lib):
     assert lib.w4a8_plan(8, 17408, 5000, ctypes.byref(k), ctypes.byref(v), ctypes.byref(s)) == 1
 
 
-@pytest.mark.parametrize("M,N,K,wave_tile", [
+@pytest.mark.parametrize("M,N,K,tile", [
     # small M: the smallest tile whose workgroup count stays within 5/8 of 256 CUs
-    (32, 10240, 5120, (1, 2)), (32, 17408, 5120, (1, 4)), (64, 17408, 5120, (2, 4)),
-    (64, 5120, 8704, (1, 2)), (128, 5120, 6144, (1, 4)), (128, 17408, 5120, (4, 4)),
-    (256, 17408, 5120, (4, 4)),
-    # prefill: 256 x 256 for wide N, 256 x 160 when N splits into 160-column tiles
-    (1024, 17408, 5120, (4, 4)), (4096, 17408, 5120, (8, 8)), (4096, 5120, 8704, (8, 5))])
-def test_plan_tile_shapes(lib, M, N, K, wave_tile):
+    (32, 10240, 5120, (32, 64)), (32, 17408, 5120, (32, 128)), (64, 17408, 5120, (64, 128)),
+    (64, 5120, 8704, (32, 64)), (128, 5120, 6144, (32, 128)), (128, 17408, 5120, (128, 128)),
+    (256, 17408, 5120, (128, 128)), (512, 17408, 5120, (128, 128)),
+    # prefill: 256 x 256 (8 waves) for wide N, 256 x 160 when N splits into 160-column tiles
+    (1024, 17408, 5120, (256, 256)), (4096, 17408, 5120, (256, 256)),
+    (4096, 5120, 8704, (256, 160))])
+def test_plan_tile_shapes(lib, M, N, K, tile):
     k, v, s = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     assert lib.w4a8_plan(M, N, K, ctypes.byref(k), ctypes.byref(v), ctypes.byref(s)) == 0
     assert k.value == 2
-    assert _native.variants(2)[v.value][:2] == wave_tile
+    assert _native.variants(2)[v.value][2:] == tile
 
 
 def test_variant_tables(lib):
@@ -139,7 +140,7 @@ def test_variant_tables(lib):
     a = [ctypes.c_int() for _ in range(4)]
     assert lib.w4a8_variant_info(2, 0, *[ctypes.byref(x) for x in a]) == 0
     wm, wn, bm, bn = (x.value for x in a)
-    assert bm == 32 * wm and bn == 32 * wn
+    assert bn == 32 * wn and bm % (32 * wm) == 0
 
 
 def test_quant_and_repack_validate(lib):

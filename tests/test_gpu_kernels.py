@@ -329,6 +329,31 @@ def test_gemm_every_tile_variant(gpu_lib, M, N, K):
         assert_gemm_close(out, q, s, w, ws, f"M={M} N={N} K={K} tile variant {v} {cfg}")
 
 
+@pytest.mark.parametrize("M,N,K", [(4000, 5104, 1024), (2100, 4800, 2048)])
+def test_gemm_tile_variants_agree_bitwise(gpu_lib, M, N, K):
+    """More tiles than CUs, so the persistent variants walk several tiles per workgroup (with a
+    ragged last row block and, for N=5104, a ragged last column block; 270 tiles is not a multiple
+    of the 8-XCD interleave). Every tile variant accumulates each output's k-tiles in the same
+    order into one fp32 chain, so all of them must agree bit for bit; the first is checked against
+    the oracle."""
+    x = synthetic.activations(M, K, seed=M + 1)
+    w, ws = synthetic.weights(N, K, seed=N + 1)
+    q, s = O.quant_per_token(x)
+    wq, sq = gpu_repack(w, ws)
+    cfgs = _native.variants(TILE)
+    first = None
+    for v, cfg in enumerate(cfgs):
+        print(f"[tile] M={M} N={N} K={K} variant {v} {cfg}", flush=True)
+        out = gpu_gemm(q, s, wq, sq, N, K, TILE, v)
+        if first is None:
+            assert_gemm_close(out, q, s, w, ws, f"M={M} N={N} K={K} tile variant {v} {cfg}")
+            first = out
+        else:
+            bad = np.argwhere(out != first)
+            assert bad.size == 0, \
+                f"tile variant {v} {cfg}: {len(bad)} outputs differ from variant 0, first {bad[:3]}"
+
+
 @pytest.mark.parametrize("N,K", [(17408, 5120), (5120, 8704)])
 def test_gemm_prefill_4096_sampled_rows(gpu_lib, N, K):
     """M=4096 prefill GEMMs (gate_up, down): every output column, 192 sampled token rows checked

@@ -100,10 +100,10 @@ int find_skinny(int mt, int nt, int waves) {
   return -1;
 }
 
-int find_tile(int wm, int wn) {
+int find_tile(int wm, int wn, int nw = 4, int pers = 0) {
   for (int v = 0; v < tile_variant_count(); ++v) {
     const TileCfg c = tile_variant(v);
-    if (c.wm == wm && c.wn == wn) return v;
+    if (c.wm == wm && c.wn == wn && c.nw == nw && c.pers == pers) return v;
   }
   return -1;
 }
@@ -171,21 +171,53 @@ void plan_impl(int M, int N, int K, int dev, int* kernel, int* variant, int* spl
     *split_k = ks;
     return;
   }
-  // Prefill band (measured on MI355X): 256 x 256 tiles for wide N, 256 x 160 where N divides into
-  // 160-column tiles that fill the CUs evenly (N = 5120: 512 tiles at M = 4096), 128 x 128 from
-  // M = 512, and below that the small-M rule.
+  // Prefill band (measured on MI355X): 8-wave 256 x 256 tiles for wide N (the automatic path
+  // splits N so the last round of these one-per-CU workgroups is not mostly idle, see
+  // tile_split), 256 x 160 where N divides into 160-column tiles that fill the CUs evenly
+  // (N = 5120: 512 tiles at M = 4096), 128 x 128 below M = 1024, and the small-M rule below that.
   *kernel = W4A8_KERNEL_TILE;
-  if (M >= 2048 && N % 160 == 0 && N <= 8192) *variant = find_tile(8, 5);
-  else if (M >= 2048) *variant = find_tile(8, 8);
+  if (M >= 1024 && N % 160 == 0 && N <= 8192) *variant = find_tile(4, 5, 8);
+  else if (M >= 1024) *variant = find_tile(4, 8, 8);
   else if (M > 256) *variant = find_tile(4, 4);
   else *variant = small_m_tile(M, N, device_info(dev).cus);
   *split_k = 1;
 }
 
+// A tile variant whose workgroup fills a CU's LDS runs in rounds of one workgroup per CU. When the
+// last round would run at under half occupancy (gate/up at M = 4096 on 256 x 256 tiles: 1088
+// tiles = 4.25 rounds), the automatic path gives the variant the columns [0, n_main) that fill
+// whole rounds (16384 of 17408) and the rest to 128 x 128 tiles, which fill one more, shorter
+// round. Returns n_main, or 0 for no split.
+int tile_split(int M, int N, int variant, int dev, int* tail_variant) {
+  const TileCfg c = tile_variant(variant);
+  const DeviceInfo d = device_info(dev);
+  if ((size_t)2 * c.lds <= d.lds) return 0;       // two or more workgroups per CU
+  const int mb = ceil_div(M, c.bm), nb = ceil_div(N, c.bn), slots = d.cus;
+  const long total = (long)mb * nb;
+  if (total < slots || total % slots == 0 || 2 * (total % slots) >= slots) return 0;
+  int nbm = nb - 1;
+  while (nbm > 0 && ((long)mb * nbm) % slots) --nbm;
+  const int tv = find_tile(4, 4);
+  if (nbm <= 0 || tv < 0) return 0;
+  *tail_variant = tv;
+  return nbm * c.bn;
+}
+
+// Output columns [n0, n0 + n) of an M x N GEMM on one tile variant: the weights, scales and
+// output are offset by n0 / 16 n-tiles; the output keeps its row stride N.
+int tile_columns(const void* a, const float* as, const void* wq, const void* sq, void* c, int M,
+                 int N, int K, int n0, int n, int variant, hipStream_t st) {
+  const size_t kt = padded_k(K) / kKTile, nt0 = n0 / kNTile;
+  const GemmArgs g{(const uint8_t*)a, as, (const uint8_t*)wq + nt0 * kt * kGranuleBytes,
+                   (const uint32_t*)sq + nt0 * (kt / kKGroup) * 64, (uint16_t*)c + n0, M, n, K,
+                   N};
+  return hip_status(launch_tile(g, variant, device_info(current_device()).cus, st), "w4a8_gemm");
+}
+
 int gemm_dispatch(const void* a, const float* as, const void* wq, const void* sq, void* c, int M,
                   int N, int K, int kernel, int variant, int split_k, void* stream) {
   const GemmArgs g{(const uint8_t*)a, as, (const uint8_t*)wq, (const uint32_t*)sq, (uint16_t*)c,
-                   M, N, K};
+                   M, N, K, N};
   const hipStream_t st = (hipStream_t)stream;
   if (kernel == W4A8_KERNEL_SKINNY) {
     if (variant < 0 || variant >= skinny_variant_count())
@@ -217,7 +249,7 @@ int gemm_dispatch(const void* a, const float* as, const void* wq, const void* sq
     if (!tile_fits(M, N, K))
       return fail(W4A8_EINVAL, "w4a8_gemm: M=%d K=%d exceeds the tile kernel's 32-bit offsets", M,
                   K);
-    return hip_status(launch_tile(g, variant, st), "w4a8_gemm");
+    return hip_status(launch_tile(g, variant, device_info(current_device()).cus, st), "w4a8_gemm");
   }
   if (kernel == W4A8_KERNEL_STREAM) {
     if (variant < 0 || variant >= stream_variant_count())
@@ -300,7 +332,19 @@ W4A8_API int w4a8_gemm_planned(const void* a, const float* a_scale, const void* 
   if (int e = check_gemm_shape("w4a8_gemm", M, N, K)) return e;
   if (M == 0) return W4A8_OK;
   if (int e = check_gemm_ptrs("w4a8_gemm", a, a_scale, wq, sq, c)) return e;
-  if (kernel == W4A8_KERNEL_AUTO) plan_impl(M, N, K, current_device(), &kernel, &variant, &split_k);
+  if (kernel == W4A8_KERNEL_AUTO) {
+    const int dev = current_device();
+    plan_impl(M, N, K, dev, &kernel, &variant, &split_k);
+    int tail = -1;
+    const int n_main = kernel == W4A8_KERNEL_TILE && tile_fits(M, N, K)
+                           ? tile_split(M, N, variant, dev, &tail)
+                           : 0;
+    if (n_main > 0 && n_main < N && n_main % kNTile == 0) {
+      const hipStream_t st = (hipStream_t)stream;
+      if (int e = tile_columns(a, a_scale, wq, sq, c, M, N, K, 0, n_main, variant, st)) return e;
+      return tile_columns(a, a_scale, wq, sq, c, M, N, K, n_main, N - n_main, tail, st);
+    }
+  }
   return gemm_dispatch(a, a_scale, wq, sq, c, M, N, K, kernel, variant, split_k, stream);
 }
 

@@ -27,36 +27,42 @@
 //    and weight panels in its own L2.
 //  * Epilogue: a lane holds 4 consecutive columns of one token; scaled by the per-token fp32 scale,
 //    rounded to bf16 and stored 8 bytes at a time.
+#include <type_traits>
+
 #include "w4a8_internal.h"
 
 namespace w4a8 {
 namespace {
 
-constexpr int kThreads = 256;
 constexpr int kOut = 0x7FFFFFF0;                 // an offset past every buffer resource here
 
-template <int WM, int WN>
+// NW waves in an (NW / 2) x 2 arrangement, each owning WM x WN MFMA tiles of 16 x 16.
+template <int WM, int WN, int NW>
 struct TileShape {
-  static constexpr int BM = 2 * WM * 16;
-  static constexpr int BN = 2 * WN * 16;
+  static constexpr int WVM = NW / 2, WVN = 2;
+  static constexpr int BM = WVM * WM * 16;
+  static constexpr int BN = WVN * WN * 16;
   static constexpr int A_UNITS = BM / 8;         // 1 KiB units per slab: 8 tokens x 128 k each
-  static constexpr int W_UNITS = 2 * WN;         // weight granules per slab
-  static constexpr int S_ROWS = 2 * WN;          // 256 B scale-dword rows per k-group (one per n-tile)
-  static constexpr int A_PER_WAVE = A_UNITS / 4;
-  static constexpr int W_PER_WAVE = ceil_div(W_UNITS, 4);
+  static constexpr int W_UNITS = BN / 16;        // weight granules per slab
+  static constexpr int S_ROWS = BN / 16;         // 256 B scale-dword rows per k-group (one per n-tile)
+  static constexpr int A_PER_WAVE = A_UNITS / NW;
+  static constexpr int W_PER_WAVE = ceil_div(W_UNITS, NW);
   static constexpr int S_QUARTER = ceil_div(S_ROWS, 4);        // rows filled per slab
-  static constexpr int S_PER_WAVE = ceil_div(S_QUARTER, 4);
+  static constexpr int S_PER_WAVE = ceil_div(S_QUARTER, NW);
   static constexpr int OPS = A_PER_WAVE + W_PER_WAVE + S_PER_WAVE;   // fills per wave per slab
   // every wave issues the same number of fills; the surplus ones (past W_UNITS, or past a
   // quarter's scale rows) are zero fills into padding slots of their own
   static constexpr int W_OFF = A_UNITS * 1024;
-  static constexpr int STAGE = W_OFF + 4 * W_PER_WAVE * 1024;
+  static constexpr int STAGE = W_OFF + NW * W_PER_WAVE * 1024;
   // scale ring: 3 k-groups of S_ROWS rows, plus one junk row
   static constexpr int S_SLOT = (4 * S_QUARTER + 1) * 256;
-  static_assert(A_UNITS % 4 == 0, "tile");
+  // the tile's per-token fp32 scales, one 256-byte row per 64 tokens
+  static constexpr int TSCALE = 256 * ceil_div(BM, 64);
+  static_assert(NW % 2 == 0 && A_UNITS % NW == 0, "tile");
 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 
 // s_waitcnt vmcnt(n) with lgkmcnt and expcnt left open (gfx9 encoding)
 template <int N>
@@ -72,15 +78,17 @@ __device__ __forceinline__ void bare_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <int WM, int WN, int NS>
-__global__ __launch_bounds__(kThreads) void gemm_tile(
+template <int WM, int WN, int NS, int NW>
+__global__ __launch_bounds__(NW * 64) void gemm_tile(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
     const uint32_t* __restrict__ Sq, uint16_t* __restrict__ C, int M, int N, int K, int KTp,
-    int KTe, int KG, int NTILES, int grid_m, int grid_n, int vec_out) {
-  using S = TileShape<WM, WN>;
+    int KTe, int KG, int NTILES, int grid_m, int grid_n, int ldc, int vec_out) {
+  using S = TileShape<WM, WN, NW>;
   static_assert(NS >= 2 && NS <= 5 && (NS - 2) * S::OPS < 64, "pipeline depth");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * S::STAGE + 3 * S::S_SLOT];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * S::STAGE + 3 * S::S_SLOT +
+                                                         S::TSCALE];
   uint8_t* const sring = lds + NS * S::STAGE;
+  uint8_t* const tscale = sring + 3 * S::S_SLOT;   // the tile's per-token fp32 scales
 
   // ---- tile order: XCD-contiguous runs, grouped by 8 row blocks ----
   const int total = grid_m * grid_n;
@@ -96,7 +104,7 @@ __global__ __launch_bounds__(kThreads) void gemm_tile(
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave >> 1, wn = wave & 1;      // (NW / 2) x 2 waves
 
   // buffer resources: activations (all M x K), this tile's weight granules and scale dwords
   const auto a_src = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, M * K, kBufferWord3);
@@ -158,41 +166,37 @@ __global__ __launch_bounds__(kThreads) void gemm_tile(
 #pragma unroll
     for (int j = 0; j < WN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  // Multiply slab kt out of stage st while issuing the fills of slab fkt into stage fst: fragment
-  // i+1 is read and a share of the fills is issued before fragment i's MFMAs, and a scheduling
-  // barrier keeps the compiler from sinking them below the MFMAs.
-  auto compute = [&](int st, int kt, int fkt, int fst) {
+  // Fragment reads: this wave's weight fragments and scale dwords of slab kt from stage st (the
+  // MFMA takes the dword's byte kt % 4: shift it by 8 (kt % 4) where it is used), and its
+  // activation fragment i (tokens 16 (wm WM + i) ..) of the same stage.
+  auto read_w = [&](int st, int kt, v4i* wf, uint32_t* sc) {
     const uint8_t* base = lds + st * S::STAGE;
-    uint8_t* fbase = lds + fst * S::STAGE;
     const uint8_t* srow = sring + ((kt >> 2) % 3) * S::S_SLOT + lane * 4;
-    v4i wf[WN];
-    uint32_t sc[WN];
-    const int sh = 8 * (kt & 3);
 #pragma unroll
     for (int j = 0; j < WN; ++j) {
       wf[j] = *reinterpret_cast<const v4i*>(base + S::W_OFF + (wn * WN + j) * 1024 + lane * 16);
-      sc[j] = *reinterpret_cast<const uint32_t*>(srow + (wn * WN + j) * 256) >> sh;
-    }
-    const uint8_t* pa = base + wm * WM * 2048;
-    v4i lo = *reinterpret_cast<const v4i*>(pa + f_lo), hi = *reinterpret_cast<const v4i*>(pa + f_hi);
-#pragma unroll
-    for (int i = 0; i < WM; ++i) {
-      const v8i xf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      if (i + 1 < WM) {
-        lo = *reinterpret_cast<const v4i*>(pa + (i + 1) * 2048 + f_lo);
-        hi = *reinterpret_cast<const v4i*>(pa + (i + 1) * 2048 + f_hi);
-      }
-#pragma unroll
-      for (int o = i * S::OPS / WM; o < (i + 1) * S::OPS / WM; ++o) fill_op(fkt, fbase, o);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int j = 0; j < WN; ++j) acc[i][j] = mfma_w4a8(wf[j], xf, acc[i][j], sc[j]);
-      __builtin_amdgcn_sched_barrier(0);
+      sc[j] = *reinterpret_cast<const uint32_t*>(srow + (wn * WN + j) * 256);
     }
   };
+  auto read_a = [&](int st, int i, v4i& lo, v4i& hi) {
+    const uint8_t* pa = lds + st * S::STAGE + (wm * WM + i) * 2048;
+    lo = *reinterpret_cast<const v4i*>(pa + f_lo);
+    hi = *reinterpret_cast<const v4i*>(pa + f_hi);
+  };
 
-  // ---- NS-stage pipeline: slab kt+NS-1 is requested while slab kt is multiplied ----
-  // k-group 0's scale rows first (4 quarters), so the wait for slab 0 covers them too
+  // The epilogue's per-token scales (the tile's BM tokens) go straight to LDS before anything
+  // else: they are older than every fill, so the first fill wait and barrier cover them, and their
+  // latency hides under the main loop at no register cost.
+  {
+    const auto as_src = __builtin_amdgcn_make_buffer_rsrc((void*)As, 0, M * 4, kBufferWord3);
+    const int r = wave * 64 + lane;
+    if (wave * 64 < S::BM)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(as_src, (lds_ptr_t)(tscale + wave * 256), 4,
+                                               (r < S::BM && m0 + r < M) ? (m0 + r) * 4 : kOut,
+                                               0, 0, 0);
+  }
+
+  // k-group 0's scale rows go out first (4 quarters), so the wait for slab 0 covers them too
   {
     const int i = wave * S::S_PER_WAVE;
 #pragma unroll
@@ -206,26 +210,126 @@ __global__ __launch_bounds__(kThreads) void gemm_tile(
             real ? (r * KG * 64 + lane) * 4 : kOut, 0, 0, 0);
       }
   }
+
+  if constexpr (WM >= 3) {
+    // ---- NS-stage pipeline, barrier two MFMA groups before the end of each slab. At the
+    //      barrier of slab kt every wave has its own fills of slab kt+1 landed and has finished
+    //      every read of slab kt; past it, the wave reads slab kt+1's weight fragments, scales
+    //      and first activation fragment, and refills slab kt's stage with slab kt+NS, while the
+    //      last two groups of slab kt's MFMAs run. A slab is requested NS-1 slabs before its
+    //      barrier, and no wave idles at a barrier with an empty MFMA queue behind it. ----
+    constexpr int P = WM - 2;
 #pragma unroll
-  for (int p = 0; p < NS - 1; ++p) fill(p, p);
-  int st = 0;
-  for (int kt = 0; kt < KTe; ++kt) {
-    wait_vmcnt<(NS - 2) * S::OPS>();             // this wave's fills of slab kt have landed
-    bare_barrier();                              // ... and every wave's; slab kt-1 is consumed
-    const int nxt = st == 0 ? NS - 1 : st - 1;   // stage of slab kt+NS-1 == stage of slab kt-1
-    compute(st, kt, kt + NS - 1, nxt);           // issues slab kt+NS-1's fills in shares
-    st = st + 1 == NS ? 0 : st + 1;
+    for (int p = 0; p < NS; ++p) fill(p, p);
+    wait_vmcnt<(NS - 1) * S::OPS>();             // slab 0 (and k-group 0's scales) have landed
+    bare_barrier();
+    v4i wf[WN], lo, hi;
+    uint32_t sc[WN];
+    read_w(0, 0, wf, sc);
+    read_a(0, 0, lo, hi);
+    int st = 0;
+    for (int kt = 0; kt < KTe; ++kt) {
+      const int nst = st + 1 == NS ? 0 : st + 1;
+      uint8_t* fbase = lds + st * S::STAGE;      // slab kt's stage, refilled with slab kt+NS
+      v4i wfn[WN], lon, hin;
+      uint32_t scn[WN];
+#pragma unroll
+      for (int i = 0; i < WM; ++i) {
+        const v8i xf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        if (i + 1 < WM) read_a(st, i + 1, lo, hi);
+        if (i == P) {
+          wait_vmcnt<(NS - 2) * S::OPS>();       // this wave's fills of slab kt+1 have landed
+          __builtin_amdgcn_s_waitcnt(0xC07F);    // lgkmcnt(0): this wave's reads of slab kt done
+          bare_barrier();
+          read_w(nst, kt + 1, wfn, scn);
+          read_a(nst, 0, lon, hin);
+        }
+        if (i >= P) {
+#pragma unroll
+          for (int o = (i - P) * S::OPS / 2; o < (i - P + 1) * S::OPS / 2; ++o)
+            fill_op(kt + NS, fbase, o);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+          acc[i][j] = mfma_w4a8(wf[j], xf, acc[i][j], sc[j] >> (8 * (kt & 3)));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int j = 0; j < WN; ++j) wf[j] = wfn[j], sc[j] = scn[j];
+      lo = lon;
+      hi = hin;
+      st = nst;
+    }
+  } else {
+    // ---- NS-stage pipeline, barrier at the head of each slab: slab kt+NS-1 is requested in
+    //      shares between the MFMA groups of slab kt; fragment i+1 is read before fragment i's
+    //      MFMAs, and scheduling barriers keep the compiler from sinking either below them ----
+#pragma unroll
+    for (int p = 0; p < NS - 1; ++p) fill(p, p);
+    int st = 0;
+    for (int kt = 0; kt < KTe; ++kt) {
+      wait_vmcnt<(NS - 2) * S::OPS>();           // this wave's fills of slab kt have landed
+      bare_barrier();                            // ... and every wave's; slab kt-1 is consumed
+      const int fst = st == 0 ? NS - 1 : st - 1; // stage of slab kt+NS-1 == stage of slab kt-1
+      uint8_t* fbase = lds + fst * S::STAGE;
+      v4i wf[WN], lo, hi;
+      uint32_t sc[WN];
+      read_w(st, kt, wf, sc);
+      read_a(st, 0, lo, hi);
+#pragma unroll
+      for (int i = 0; i < WM; ++i) {
+        const v8i xf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        if (i + 1 < WM) read_a(st, i + 1, lo, hi);
+#pragma unroll
+        for (int o = i * S::OPS / WM; o < (i + 1) * S::OPS / WM; ++o)
+          fill_op(kt + NS - 1, fbase, o);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+          acc[i][j] = mfma_w4a8(wf[j], xf, acc[i][j], sc[j] >> (8 * (kt & 3)));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      st = st + 1 == NS ? 0 : st + 1;
+    }
   }
   wait_vmcnt<0>();                               // no fill may outlive the workgroup's LDS
 
-  // per-token scales of this lane's WM tokens, all requested before the first is used
-  const auto as_src = __builtin_amdgcn_make_buffer_rsrc((void*)As, 0, M * 4, kBufferWord3);
   float tsc[WM];
 #pragma unroll
-  for (int i = 0; i < WM; ++i) {
-    const int m = m0 + (wm * WM + i) * 16 + (lane & 15);
-    tsc[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                           as_src, m < M ? m * 4 : kOut, 0, 0));
+  for (int i = 0; i < WM; ++i)
+    tsc[i] = reinterpret_cast<const float*>(tscale)[(wm * WM + i) * 16 + (lane & 15)];
+
+  // Epilogue. A lane holds 4 consecutive columns of one token per MFMA tile, so direct stores
+  // touch 16 rows per instruction (measured: ~7.5 us per 256 x 256 tile on MI355X). A full tile
+  // is therefore staged through the freed pipeline stages, row-major with a 16-byte row pad, and
+  // written out as 16-byte row-contiguous stores; edge tiles store directly.
+  constexpr int OROW = S::BN * 2 + 16;
+  constexpr bool kStaged = S::BM * OROW <= NS * S::STAGE;
+  if (kStaged && vec_out == 2 && m0 + S::BM <= M && nt_base * kNTile + S::BN <= N) {
+    bare_barrier();                              // every wave is done with the stages
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+      const int r = (wm * WM + i) * 16 + (lane & 15);
+#pragma unroll
+      for (int j = 0; j < WN; ++j) {
+        const int col = (wn * WN + j) * kNTile + 4 * (lane >> 4);
+        const v4f v = acc[i][j];
+        const uint32_t b0 = f32_to_bf16(v[0] * tsc[i]), b1 = f32_to_bf16(v[1] * tsc[i]);
+        const uint32_t b2 = f32_to_bf16(v[2] * tsc[i]), b3 = f32_to_bf16(v[3] * tsc[i]);
+        *reinterpret_cast<uint2*>(lds + r * OROW + col * 2) =
+            make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
+      }
+    }
+    __syncthreads();
+    constexpr int CH = S::BN * 2 / 16;           // 16-byte chunks per row
+    uint16_t* const crow = C + (size_t)m0 * ldc + nt_base * kNTile;
+    for (int idx = tid; idx < S::BM * CH; idx += NW * 64) {
+      const int r = idx / CH, c = idx - r * CH;
+      *reinterpret_cast<v4i*>(crow + (size_t)r * ldc + c * 8) =
+          *reinterpret_cast<const v4i*>(lds + r * OROW + c * 16);
+    }
+    return;
   }
   const bool vec = vec_out != 0;
 #pragma unroll
@@ -235,17 +339,280 @@ __global__ __launch_bounds__(kThreads) void gemm_tile(
 #pragma unroll
     for (int j = 0; j < WN; ++j) {
       const int n = (nt_base + wn * WN + j) * kNTile + 4 * (lane >> 4);
-      store_out4(C, N, m, n, N, acc[i][j], tsc[i], vec);
+      store_out4(C, ldc, m, n, N, acc[i][j], tsc[i], vec);
     }
   }
 }
 
-// (WM, WN, NS): wave tile 16 WM x 16 WN, NS-stage LDS pipeline (LDS = NS * STAGE <= 160 KiB)
-#define W4A8_TILE_TABLE(X)                                                                        \
-  X(2, 4, 4) X(4, 4, 3) X(4, 4, 4) X(8, 4, 3) X(4, 8, 3) X(8, 8, 3) X(8, 5, 3) X(4, 8, 4)          \
-  X(4, 2, 4) X(1, 2, 4) X(2, 2, 4) X(1, 4, 4) X(2, 2, 5)
+// Persistent form of the mid-slab-barrier pipeline, for K % 512 == 0: the grid is one workgroup
+// per CU, workgroup b walks the tiles b, b + G, b + 2G, ... (XCD-contiguous order, as above), and
+// the fill stream runs across tile boundaries - slab kt+NS of the stream may be the next tile's
+// first slab - so a tile's first slabs land while the previous tile finishes and stores, instead
+// of behind a per-tile prologue (measured ~4 us per 256 x 256 tile on MI355X). The scale ring
+// counts k-groups along the stream; each slab's fills also carry one token-scale op (real for a
+// tile's first slab: the tile's BM scales into one of two LDS buffers; a zero fill otherwise).
+template <int WM, int WN, int NS, int NW>
+__global__ __launch_bounds__(NW * 64) void gemm_tile_pers(
+    const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
+    const uint32_t* __restrict__ Sq, uint16_t* __restrict__ C, int M, int N, int K, int KTp,
+    int KTe, int KG, int NTILES, int grid_m, int grid_n, int ldc, int vec_out) {
+  using S = TileShape<WM, WN, NW>;
+  constexpr int OPS = S::OPS + 1;                // fills per wave per slab, + the token-scale op
+  constexpr int P = WM - 2;
+  static_assert(WM >= 3 && NS >= 2 && NS <= 5, "pipeline depth");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * S::STAGE + 3 * S::S_SLOT +
+                                                         2 * S::TSCALE + 256];
+  uint8_t* const sring = lds + NS * S::STAGE;
+  uint8_t* const tscale = sring + 3 * S::S_SLOT;     // [2][BM] fp32, by tile parity
+  uint8_t* const junk = tscale + 2 * S::TSCALE;      // sink of the zero token-scale fills
 
-#define W4A8_TILE_CFG(wm, wn, ns) TileCfg{wm, wn, TileShape<wm, wn>::BM, TileShape<wm, wn>::BN},
+  const int total = grid_m * grid_n, G = gridDim.x, b = blockIdx.x;
+  const int ntl = (total - b + G - 1) / G;           // tiles of this workgroup (b < total)
+  const int KQ = KTe >> 2;                           // k-groups per tile
+
+  // tile i of this workgroup -> (first token, first n-tile); past the last tile: tile 0's.
+  // Branch-free (selects only), so the k-loop that advances the fill cursor stays one block.
+  auto tile_at = [&](int i, int& m0, int& ntb) {
+    int t = i < ntl ? b + i * G : b;
+    t = total % 8 == 0 ? (t % 8) * (total / 8) + t / 8 : t;
+    constexpr int GROUP = 8;
+    const int per_group = GROUP * grid_n;
+    const int first_m = (t / per_group) * GROUP;
+    const int gm = min(grid_m - first_m, GROUP);
+    m0 = (first_m + (t % per_group) % gm) * S::BM;
+    ntb = ((t % per_group) / gm) * (S::BN / 16);
+  };
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;           // (NW / 2) x 2 waves
+  const auto a_src = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, M * K, kBufferWord3);
+  const auto as_src = __builtin_amdgcn_make_buffer_rsrc((void*)As, 0, M * 4, kBufferWord3);
+  const int a_row = lane >> 3;
+  const int a_chunk = (lane & 7) ^ (a_row >> 1);
+  const int f_row = lane & 15;
+  const int f_lo = 1024 * (f_row >> 3) + 16 * (8 * (f_row & 7) + ((lane >> 4) ^ ((f_row >> 1) & 7)));
+  const int f_hi = f_lo ^ 64;
+
+  // Fill ops [o0, o1) of one stream slab into stage base. The slab is k-tile fkt of the tile at
+  // (fm0, fntb) (kin: that tile exists); it also carries quarter fg % 4 of the scale rows of the
+  // next stream k-group: group sgrp of the tile at sntb (sin: that tile exists); and, when fkt is
+  // 0, the tile's token scales (parity tpar). Op o: an activation unit, a weight granule, a scale
+  // row, or the token-scale op. All arguments are scalar and every choice below is a select.
+  auto fill_ops = [&](int fg, int fkt, int fm0, int fntb, bool kin, int sntb, int sgrp, bool sin,
+                      int tpar, uint8_t* base, int o0, int o1) {
+    const int nth = kin ? min(S::BN / 16, NTILES - fntb) : 0;
+    const auto w_src = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(Wq + (size_t)fntb * KTp * kGranuleBytes), 0, nth * KTp * kGranuleBytes,
+        kBufferWord3);
+    const int snth = sin ? min(S::BN / 16, NTILES - sntb) : 0;
+    const auto s_src = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(Sq + (size_t)sntb * KG * 64), 0, snth * KG * 256, kBufferWord3);
+#pragma unroll
+    for (int o = 0; o < OPS; ++o) {
+      if (o < o0 || o >= o1) continue;
+      if (o < S::A_PER_WAVE) {
+        const int unit = wave * S::A_PER_WAVE + o;
+        const int row = fm0 + unit * 8 + a_row;
+        const int col = fkt * kKTile + 16 * (a_chunk ^ ((unit & 1) << 2));
+        const int off = (kin & (col < K) & (row < M)) ? row * K + col : kOut;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(a_src, (lds_ptr_t)(base + unit * 1024), 16, off,
+                                                 0, 0, 0);
+      } else if (o < S::A_PER_WAVE + S::W_PER_WAVE) {
+        const int g = wave * S::W_PER_WAVE + (o - S::A_PER_WAVE);
+        const int off =
+            (kin & (g < S::W_UNITS)) ? (g * KTp + fkt) * kGranuleBytes + lane * 16 : kOut;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(w_src, (lds_ptr_t)(base + S::W_OFF + g * 1024),
+                                                 16, off, 0, 0, kBufferNT);
+      } else if (o < S::OPS) {
+        const int q = fg & 3;
+        const int i = wave * S::S_PER_WAVE + (o - S::A_PER_WAVE - S::W_PER_WAVE);
+        const int r = q * S::S_QUARTER + i;
+        const bool real = (i < S::S_QUARTER) & (r < S::S_ROWS);
+        const int off = (real & sin) ? ((r * KG + sgrp) * 64 + lane) * 4 : kOut;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            s_src,
+            (lds_ptr_t)(sring + (((fg >> 2) + 1) % 3) * S::S_SLOT +
+                        (real ? r : 4 * S::S_QUARTER) * 256),
+            4, off, 0, 0, 0);
+      } else {
+        const int r = wave * 64 + lane;
+        const bool real = kin & (fkt == 0) & (wave * 64 < S::BM);
+        const int off = (real & (r < S::BM) & (fm0 + r < M)) ? (fm0 + r) * 4 : kOut;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            as_src, (lds_ptr_t)(real ? tscale + tpar * S::TSCALE + wave * 256 : junk), 4, off, 0,
+            0, 0);
+      }
+    }
+  };
+  auto read_w = [&](int st, int g, v4i* wf, uint32_t* sc) {
+    const uint8_t* base = lds + st * S::STAGE;
+    const uint8_t* srow = sring + ((g >> 2) % 3) * S::S_SLOT + lane * 4;
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      wf[j] = *reinterpret_cast<const v4i*>(base + S::W_OFF + (wn * WN + j) * 1024 + lane * 16);
+      sc[j] = *reinterpret_cast<const uint32_t*>(srow + (wn * WN + j) * 256);
+    }
+  };
+  auto read_a = [&](int st, int i, v4i& lo, v4i& hi) {
+    const uint8_t* pa = lds + st * S::STAGE + (wm * WM + i) * 2048;
+    lo = *reinterpret_cast<const v4i*>(pa + f_lo);
+    hi = *reinterpret_cast<const v4i*>(pa + f_hi);
+  };
+
+  // stream k-group 0's scale rows (tile 0), then slabs 0..NS-1 (all of tile 0: KTe >= 2 NS)
+  int c_m0, c_ntb, n1_m0, n1_ntb, n2_m0, n2_ntb;
+  tile_at(0, c_m0, c_ntb);
+  tile_at(1, n1_m0, n1_ntb);
+  {
+    const int nth = min(S::BN / 16, NTILES - c_ntb);
+    const auto s_src = __builtin_amdgcn_make_buffer_rsrc((void*)(Sq + (size_t)c_ntb * KG * 64),
+                                                         0, nth * KG * 256, kBufferWord3);
+    const int i = wave * S::S_PER_WAVE;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int e = 0; e < S::S_PER_WAVE; ++e) {
+        const int r = q * S::S_QUARTER + i + e;
+        const bool real = (i + e < S::S_QUARTER) & (r < S::S_ROWS);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            s_src, (lds_ptr_t)(sring + (real ? r : 4 * S::S_QUARTER) * 256), 4,
+            real ? (r * KG * 64 + lane) * 4 : kOut, 0, 0, 0);
+      }
+  }
+#pragma unroll
+  for (int p = 0; p < NS; ++p) {
+    const bool sn = (p >> 2) + 1 == KQ;
+    fill_ops(p, p, c_m0, c_ntb, true, sn ? n1_ntb : c_ntb, sn ? 0 : (p >> 2) + 1, !sn || 1 < ntl,
+             0, lds + p * S::STAGE, 0, OPS);
+  }
+  wait_vmcnt<(NS - 1) * OPS>();                  // slab 0 (and everything older) has landed
+  bare_barrier();
+  v4i wf[WN], lo, hi;
+  uint32_t sc[WN];
+  read_w(0, 0, wf, sc);
+  read_a(0, 0, lo, hi);
+  // Output: a tile's results leave as ST = WM * WN 8-byte stores per wave right after its last
+  // slab. Stores count in vmcnt like the fills, so the first NS-1 slab waits of the next tile
+  // (whose awaited fills are older than the stores) allow ST more outstanding ops; from slab NS-1
+  // on, the awaited fills are younger than the stores, which have had NS-1 slabs to drain.
+  constexpr int ST = WM * WN;
+  static_assert((NS - 2) * OPS + ST < 64, "vmcnt range");
+  int st = 0, g = 0;
+  int c_m0_ = 0, c_ntb_ = 0, n1_m0_ = 0, n1_ntb_ = 0, n2_m0_ = 0, n2_ntb_ = 0;
+  bool v1_ = false, v2_ = false;
+  int tile = 0;
+  v4f acc[WM][WN];
+  auto set_tile = [&](int t) {
+    tile = t;
+    tile_at(t, c_m0_, c_ntb_);
+    tile_at(t + 1, n1_m0_, n1_ntb_);
+    tile_at(t + 2, n2_m0_, n2_ntb_);
+    v1_ = t + 1 < ntl;
+    v2_ = t + 2 < ntl;
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int j = 0; j < WN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+  };
+  // one slab of the current tile: k-tile kt; EXTRA: stores outstanding beyond the fills
+  auto kstep = [&](int kt, auto extra) {
+    constexpr int EXTRA = decltype(extra)::value;
+    const int nst = st + 1 == NS ? 0 : st + 1;
+    uint8_t* fbase = lds + st * S::STAGE;        // slab g's stage, refilled with slab g+NS
+    // slab g+NS: k-tile fkt of this tile or the next; its scale rows: the next k-group
+    const bool fw = kt + NS >= KTe;
+    const int fkt = fw ? kt + NS - KTe : kt + NS;
+    const int fm0 = fw ? n1_m0_ : c_m0_, fntb = fw ? n1_ntb_ : c_ntb_;
+    const bool kin = fw ? v1_ : true;
+    const bool sn = (fkt >> 2) + 1 == KQ;
+    const int sgrp = sn ? 0 : (fkt >> 2) + 1;
+    const int sntb = (fw & sn) ? n2_ntb_ : (fw | sn) ? n1_ntb_ : c_ntb_;
+    const bool sin = (fw & sn) ? v2_ : (fw | sn) ? v1_ : true;
+    const int tpar = (tile + fw) & 1;
+    v4i wfn[WN], lon, hin;
+    uint32_t scn[WN];
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+      const v8i xf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      if (i + 1 < WM) read_a(st, i + 1, lo, hi);
+      if (i == P) {
+        wait_vmcnt<(NS - 2) * OPS + EXTRA>();    // this wave's fills of slab g+1 have landed
+        __builtin_amdgcn_s_waitcnt(0xC07F);      // lgkmcnt(0): this wave's reads of slab g done
+        bare_barrier();
+        read_w(nst, g + 1, wfn, scn);
+        read_a(nst, 0, lon, hin);
+      }
+      if (i >= P)
+        fill_ops(g + NS, fkt, fm0, fntb, kin, sntb, sgrp, sin, tpar, fbase, (i - P) * OPS / 2,
+                 (i - P + 1) * OPS / 2);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < WN; ++j)
+        acc[i][j] = mfma_w4a8(wf[j], xf, acc[i][j], sc[j] >> (8 * (g & 3)));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int j = 0; j < WN; ++j) wf[j] = wfn[j], sc[j] = scn[j];
+    lo = lon;
+    hi = hin;
+    st = nst;
+    ++g;
+  };
+  using no_stores = std::integral_constant<int, 0>;
+  using after_stores = std::integral_constant<int, ST>;
+  // The stores go through a buffer resource with every lane active (an out-of-range element gets
+  // an offset past the resource), so each wave issues exactly ST of them whatever the tile edge.
+  const auto c_dst = __builtin_amdgcn_make_buffer_rsrc((void*)C, 0, M * ldc * 2, kBufferWord3);
+  auto epilogue = [&]() {
+    const float* ts = reinterpret_cast<const float*>(tscale + (tile & 1) * S::TSCALE);
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+      const int m = c_m0_ + (wm * WM + i) * 16 + (lane & 15);
+      const float tsc = ts[(wm * WM + i) * 16 + (lane & 15)];
+#pragma unroll
+      for (int j = 0; j < WN; ++j) {
+        const int n = (c_ntb_ + wn * WN + j) * kNTile + 4 * (lane >> 4);
+        const v4f v = acc[i][j];
+        const uint32_t b0 = f32_to_bf16(v[0] * tsc), b1 = f32_to_bf16(v[1] * tsc);
+        const uint32_t b2 = f32_to_bf16(v[2] * tsc), b3 = f32_to_bf16(v[3] * tsc);
+        const int off = ((m < M) & (n < N)) ? (m * ldc + n) * 2 : kOut;
+        __builtin_amdgcn_raw_buffer_store_b64(v2u{b0 | (b1 << 16), b2 | (b3 << 16)}, c_dst, off, 0,
+                                              0);
+      }
+    }
+  };
+
+  // the first NS-1 slabs of a tile wait on fills issued before the previous tile's stores
+  set_tile(0);
+#pragma unroll
+  for (int kt = 0; kt + 1 < NS; ++kt) kstep(kt, no_stores{});
+  for (int t = 0; t < ntl; ++t) {
+    for (int kt = NS - 1; kt < KTe; ++kt) kstep(kt, no_stores{});
+    epilogue();
+    if (t + 1 < ntl) {
+      set_tile(t + 1);
+#pragma unroll
+      for (int kt = 0; kt + 1 < NS; ++kt) kstep(kt, after_stores{});
+    }
+  }
+  wait_vmcnt<0>();                               // no fill may outlive the workgroup's LDS
+}
+
+// (WM, WN, NS, NW, PERS): NW waves of 16 WM x 16 WN in an (NW / 2) x 2 arrangement, NS-stage LDS
+// pipeline (LDS = NS * STAGE + 3 scale slots + token scales <= 160 KiB); PERS: the persistent form
+// (one workgroup per CU; needs K % 512 == 0 and at least 2 NS k-tiles, else the plain form runs)
+#define W4A8_TILE_TABLE(X)                                                                        \
+  X(2, 4, 4, 4, 0) X(4, 4, 3, 4, 0) X(4, 4, 4, 4, 0) X(8, 4, 3, 4, 0) X(4, 8, 3, 4, 0)            \
+  X(8, 8, 3, 4, 0) X(8, 5, 3, 4, 0) X(4, 8, 4, 4, 0) X(4, 2, 4, 4, 0) X(1, 2, 4, 4, 0)            \
+  X(2, 2, 4, 4, 0) X(1, 4, 4, 4, 0) X(2, 2, 5, 4, 0) X(4, 8, 3, 8, 0) X(4, 5, 3, 8, 0)            \
+  X(4, 5, 3, 8, 1)
+
+#define W4A8_TILE_CFG(wm, wn, ns, nw, pers)                                                       \
+  TileCfg{wm, wn, TileShape<wm, wn, nw>::BM, TileShape<wm, wn, nw>::BN, nw,                        \
+          ns * TileShape<wm, wn, nw>::STAGE + 3 * TileShape<wm, wn, nw>::S_SLOT +                \
+              (pers ? 2 : 1) * TileShape<wm, wn, nw>::TSCALE + (pers ? 256 : 0),                 \
+          pers},
 constexpr TileCfg kTile[] = {W4A8_TILE_TABLE(W4A8_TILE_CFG)};
 #undef W4A8_TILE_CFG
 constexpr int kTileCount = sizeof(kTile) / sizeof(kTile[0]);
@@ -261,19 +628,34 @@ bool tile_fits(int M, int N, int K) {
          (long)N < (1L << 24);
 }
 
-hipError_t launch_tile(const GemmArgs& g, int variant, hipStream_t stream) {
+hipError_t launch_tile(const GemmArgs& g, int variant, int cus, hipStream_t stream) {
   const TileCfg c = kTile[variant];
   const int KTp = padded_k(g.K) / kKTile, KTe = ceil_div(g.K, kKTile), KG = KTp / kKGroup;
   const int NTILES = padded_n(g.N) / kNTile;
   const int grid_m = ceil_div(g.M, c.bm), grid_n = ceil_div(g.N, c.bn);
-  const int vec_out = (g.N % 4 == 0 && ((uintptr_t)g.c % 8) == 0) ? 1 : 0;
-  const dim3 grid(grid_m * grid_n), block(kThreads);
+  // 2: 16-byte row stores possible (staged epilogue), 1: 8-byte stores, 0: scalar stores
+  const int vec_out = (g.N % 8 == 0 && g.ldc % 8 == 0 && ((uintptr_t)g.c % 16) == 0)  ? 2
+                      : (g.N % 4 == 0 && g.ldc % 4 == 0 && ((uintptr_t)g.c % 8) == 0) ? 1
+                                                                                         : 0;
+  const dim3 grid(grid_m * grid_n), block(c.nw * 64);
   int idx = 0;
-#define W4A8_TILE_LAUNCH(wm, wn, ns)                                                           \
+#define W4A8_TILE_LAUNCH(wm, wn, ns, nw, pers)                                                 \
   if (idx++ == variant) {                                                                        \
-    hipLaunchKernelGGL((gemm_tile<wm, wn, ns>), grid, block, 0, stream, g.a, g.a_scale, g.wq,  \
-                       g.sq,                                                                      \
-                       g.c, g.M, g.N, g.K, KTp, KTe, KG, NTILES, grid_m, grid_n, vec_out);       \
+    if constexpr (pers) {                                                                         \
+      if (KTe % 4 == 0 && KTe >= 2 * ns && vec_out >= 1 &&                                       \
+          (long)g.M * g.ldc * 2 < (1L << 31)) {                                                   \
+        const int G = grid_m * grid_n < cus ? grid_m * grid_n : cus;                             \
+        hipLaunchKernelGGL((gemm_tile_pers<wm, wn, ns, nw>), dim3(G), block, 0, stream, g.a,     \
+                           g.a_scale, g.wq, g.sq, g.c, g.M, g.N, g.K, KTp, KTe, KG, NTILES,      \
+                           grid_m, grid_n, g.ldc, vec_out);                                      \
+        return hipGetLastError();                                                                \
+      }                                                                                          \
+    }                                                                                            \
+    {                                                                                            \
+      hipLaunchKernelGGL((gemm_tile<wm, wn, ns, nw>), grid, block, 0, stream, g.a, g.a_scale,    \
+                         g.wq, g.sq, g.c, g.M, g.N, g.K, KTp, KTe, KG, NTILES, grid_m, grid_n,   \
+                         g.ldc, vec_out);                                                        \
+    }                                                                                            \
     return hipGetLastError();                                                                    \
   }
   W4A8_TILE_TABLE(W4A8_TILE_LAUNCH)

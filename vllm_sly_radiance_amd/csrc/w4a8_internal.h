@@ -94,8 +94,9 @@ struct GemmArgs {
   const float* a_scale;  // [M]
   const uint8_t* wq;     // granules
   const uint32_t* sq;    // scale dwords
-  uint16_t* c;           // bf16 [M, N] row-major
+  uint16_t* c;           // bf16 [M, N] with row stride ldc (elements)
   int M, N, K;
+  int ldc;               // N, except for a column slice of a wider output (macro-tile family)
 };
 
 hipError_t launch_quant(const uint16_t* x, long ldx, uint8_t* q, float* s, int M, int K,
@@ -125,12 +126,13 @@ int stream_granules(int variant, int N, int K, int cus);
 bool stream_fits(int variant, int M, int N, int K, int cus, size_t lds_limit);
 hipError_t launch_stream(const GemmArgs& g, int variant, int cus, hipStream_t stream);
 
-// Macro-tile family (large M). variant indexes the instantiated (WM, WN) table.
-struct TileCfg { int wm, wn, bm, bn; };
+// Macro-tile family (M > 16). variant indexes the instantiated (WM, WN, NS, NW) table: nw waves of
+// wm x wn 16 x 16 MFMA tiles, a bm x bn workgroup tile.
+struct TileCfg { int wm, wn, bm, bn, nw, lds, pers; };
 int tile_variant_count();
 TileCfg tile_variant(int v);
 bool tile_fits(int M, int N, int K);
-hipError_t launch_tile(const GemmArgs& g, int variant, hipStream_t stream);
+hipError_t launch_tile(const GemmArgs& g, int variant, int cus, hipStream_t stream);
 
 // Register-resident MFMA throughput probe (shape 0: 16x16x128, 1: 32x32x64).
 hipError_t launch_mfma_probe(int shape, float* out, int blocks, int iters, double* flop,
