@@ -218,7 +218,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile(
     //      and first activation fragment, and refills slab kt's stage with slab kt+NS, while the
     //      last two groups of slab kt's MFMAs run. A slab is requested NS-1 slabs before its
     //      barrier, and no wave idles at a barrier with an empty MFMA queue behind it. ----
-    constexpr int P = WM - 2;
+    constexpr int R = WM >= 4 ? 3 : 2;             // MFMA groups past the barrier
+    constexpr int P = WM - R;
 #pragma unroll
     for (int p = 0; p < NS; ++p) fill(p, p);
     wait_vmcnt<(NS - 1) * S::OPS>();             // slab 0 (and k-group 0's scales) have landed
@@ -227,27 +228,26 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile(
     uint32_t sc[WN];
     read_w(0, 0, wf, sc);
     read_a(0, 0, lo, hi);
+    __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0): the loop starts with nothing pending
     int st = 0;
     for (int kt = 0; kt < KTe; ++kt) {
       const int nst = st + 1 == NS ? 0 : st + 1;
       uint8_t* fbase = lds + st * S::STAGE;      // slab kt's stage, refilled with slab kt+NS
       v4i wfn[WN], lon, hin;
       uint32_t scn[WN];
+      v8i xr[R];                                 // fragments of groups P.., read before the barrier
 #pragma unroll
-      for (int i = 0; i < WM; ++i) {
+      for (int i = 0; i < P; ++i) {
         const v8i xf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        if (i + 1 < WM) read_a(st, i + 1, lo, hi);
-        if (i == P) {
-          wait_vmcnt<(NS - 2) * S::OPS>();       // this wave's fills of slab kt+1 have landed
-          __builtin_amdgcn_s_waitcnt(0xC07F);    // lgkmcnt(0): this wave's reads of slab kt done
-          bare_barrier();
-          read_w(nst, kt + 1, wfn, scn);
-          read_a(nst, 0, lon, hin);
-        }
-        if (i >= P) {
+        if (i + 1 < P) {
+          read_a(st, i + 1, lo, hi);
+        } else {
 #pragma unroll
-          for (int o = (i - P) * S::OPS / 2; o < (i - P + 1) * S::OPS / 2; ++o)
-            fill_op(kt + NS, fbase, o);
+          for (int r = 0; r < R; ++r) {
+            v4i l, h;
+            read_a(st, P + r, l, h);
+            xr[r] = v8i{l[0], l[1], l[2], l[3], h[0], h[1], h[2], h[3]};
+          }
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -255,6 +255,36 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile(
           acc[i][j] = mfma_w4a8(wf[j], xf, acc[i][j], sc[j] >> (8 * (kt & 3)));
         __builtin_amdgcn_sched_barrier(0);
       }
+      {
+        // the last R groups: their fragments are read before the barrier; past it, the next
+        // slab's fragment reads and this slab's refill go out one or two per MFMA, so the MFMA
+        // queue never waits behind a run of memory instructions
+        wait_vmcnt<(NS - 2) * S::OPS>();         // this wave's fills of slab kt+1 have landed
+        __builtin_amdgcn_s_waitcnt(0xC07F);      // lgkmcnt(0): this wave's reads of slab kt done
+        bare_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t* nbase = lds + nst * S::STAGE;
+        const uint8_t* srow = sring + (((kt + 1) >> 2) % 3) * S::S_SLOT + lane * 4;
+#pragma unroll
+        for (int m = 0; m < R * WN; ++m) {
+          const int r = m / WN, j = m % WN;
+          acc[P + r][j] = mfma_w4a8(wf[j], xr[r], acc[P + r][j], sc[j] >> (8 * (kt & 3)));
+          __builtin_amdgcn_sched_barrier(0);
+          if (m < WN) {
+            wfn[m] = *reinterpret_cast<const v4i*>(nbase + S::W_OFF + (wn * WN + m) * 1024 +
+                                                   lane * 16);
+            scn[m] = *reinterpret_cast<const uint32_t*>(srow + (wn * WN + m) * 256);
+          }
+          if (m == WN) read_a(nst, 0, lon, hin);
+#pragma unroll
+          for (int o = m * S::OPS / (R * WN); o < (m + 1) * S::OPS / (R * WN); ++o)
+            fill_op(kt + NS, fbase, o);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      // slab kt+1's fragments (read right after the barrier, a group of MFMAs ago) are in: said
+      // here, the compiler does not make the next slab's first MFMAs wait on every LDS read
+      __builtin_amdgcn_s_waitcnt(0xC07F);
 #pragma unroll
       for (int j = 0; j < WN; ++j) wf[j] = wfn[j], sc[j] = scn[j];
       lo = lon;
@@ -492,6 +522,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile_pers(
   uint32_t sc[WN];
   read_w(0, 0, wf, sc);
   read_a(0, 0, lo, hi);
+  __builtin_amdgcn_s_waitcnt(0xC07F);            // lgkmcnt(0): the k-steps start with nothing pending
   // Output: a tile's results leave as ST = WM * WN 8-byte stores per wave right after its last
   // slab. Stores count in vmcnt like the fills, so the first NS-1 slab waits of the next tile
   // (whose awaited fills are older than the stores) allow ST more outstanding ops; from slab NS-1
@@ -533,25 +564,47 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile_pers(
     v4i wfn[WN], lon, hin;
     uint32_t scn[WN];
 #pragma unroll
-    for (int i = 0; i < WM; ++i) {
+    for (int i = 0; i < P; ++i) {
       const v8i xf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      if (i + 1 < WM) read_a(st, i + 1, lo, hi);
-      if (i == P) {
-        wait_vmcnt<(NS - 2) * OPS + EXTRA>();    // this wave's fills of slab g+1 have landed
-        __builtin_amdgcn_s_waitcnt(0xC07F);      // lgkmcnt(0): this wave's reads of slab g done
-        bare_barrier();
-        read_w(nst, g + 1, wfn, scn);
-        read_a(nst, 0, lon, hin);
-      }
-      if (i >= P)
-        fill_ops(g + NS, fkt, fm0, fntb, kin, sntb, sgrp, sin, tpar, fbase, (i - P) * OPS / 2,
-                 (i - P + 1) * OPS / 2);
+      read_a(st, i + 1, lo, hi);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int j = 0; j < WN; ++j)
         acc[i][j] = mfma_w4a8(wf[j], xf, acc[i][j], sc[j] >> (8 * (g & 3)));
       __builtin_amdgcn_sched_barrier(0);
     }
+    {
+      // the last two groups, as in the plain form: reads and refills one or two per MFMA
+      const v8i xp = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      read_a(st, P + 1, lo, hi);
+      wait_vmcnt<(NS - 2) * OPS + EXTRA>();      // this wave's fills of slab g+1 have landed
+      __builtin_amdgcn_s_waitcnt(0xC07F);        // lgkmcnt(0): this wave's reads of slab g done
+      bare_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      const v8i xq = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      const uint8_t* nbase = lds + nst * S::STAGE;
+      const uint8_t* srow = sring + (((g + 1) >> 2) % 3) * S::S_SLOT + lane * 4;
+#pragma unroll
+      for (int m = 0; m < 2 * WN; ++m) {
+        const int j = m % WN;
+        if (m < WN)
+          acc[P][j] = mfma_w4a8(wf[j], xp, acc[P][j], sc[j] >> (8 * (g & 3)));
+        else
+          acc[P + 1][j] = mfma_w4a8(wf[j], xq, acc[P + 1][j], sc[j] >> (8 * (g & 3)));
+        __builtin_amdgcn_sched_barrier(0);
+        if (m < WN) {
+          wfn[m] =
+              *reinterpret_cast<const v4i*>(nbase + S::W_OFF + (wn * WN + m) * 1024 + lane * 16);
+          scn[m] = *reinterpret_cast<const uint32_t*>(srow + (wn * WN + m) * 256);
+        }
+        if (m == WN) read_a(nst, 0, lon, hin);
+        if (m < OPS)
+          fill_ops(g + NS, fkt, fm0, fntb, kin, sntb, sgrp, sin, tpar, fbase, m,
+                   m == 2 * WN - 1 ? OPS : m + 1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0): slab g+1's fragments are in
 #pragma unroll
     for (int j = 0; j < WN; ++j) wf[j] = wfn[j], sc[j] = scn[j];
     lo = lon;
