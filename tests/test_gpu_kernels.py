@@ -331,11 +331,10 @@ def test_gemm_every_tile_variant(gpu_lib, M, N, K):
 
 @pytest.mark.parametrize("M,N,K", [(4000, 5104, 1024), (2100, 4800, 2048)])
 def test_gemm_tile_variants_agree_bitwise(gpu_lib, M, N, K):
-    """More tiles than CUs, so the persistent variants walk several tiles per workgroup (with a
-    ragged last row block and, for N=5104, a ragged last column block; 270 tiles is not a multiple
-    of the 8-XCD interleave). Every tile variant accumulates each output's k-tiles in the same
-    order into one fp32 chain, so all of them must agree bit for bit; the first is checked against
-    the oracle."""
+    """More tiles than CUs (several rounds of workgroups), with a ragged last row block and, for
+    N=5104, a ragged last column block; 270 tiles is not a multiple of the 8-XCD interleave. Every
+    tile variant accumulates each output's k-tiles in the same order into one fp32 chain, so all
+    of them must agree bit for bit; the first is checked against the oracle."""
     x = synthetic.activations(M, K, seed=M + 1)
     w, ws = synthetic.weights(N, K, seed=N + 1)
     q, s = O.quant_per_token(x)

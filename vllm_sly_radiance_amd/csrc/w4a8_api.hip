@@ -100,10 +100,10 @@ int find_skinny(int mt, int nt, int waves) {
   return -1;
 }
 
-int find_tile(int wm, int wn, int nw = 4, int pers = 0) {
+int find_tile(int wm, int wn, int nw = 4) {
   for (int v = 0; v < tile_variant_count(); ++v) {
     const TileCfg c = tile_variant(v);
-    if (c.wm == wm && c.wn == wn && c.nw == nw && c.pers == pers) return v;
+    if (c.wm == wm && c.wn == wn && c.nw == nw) return v;
   }
   return -1;
 }
@@ -211,7 +211,7 @@ int tile_columns(const void* a, const float* as, const void* wq, const void* sq,
   const GemmArgs g{(const uint8_t*)a, as, (const uint8_t*)wq + nt0 * kt * kGranuleBytes,
                    (const uint32_t*)sq + nt0 * (kt / kKGroup) * 64, (uint16_t*)c + n0, M, n, K,
                    N};
-  return hip_status(launch_tile(g, variant, device_info(current_device()).cus, st), "w4a8_gemm");
+  return hip_status(launch_tile(g, variant, st), "w4a8_gemm");
 }
 
 int gemm_dispatch(const void* a, const float* as, const void* wq, const void* sq, void* c, int M,
@@ -249,7 +249,7 @@ int gemm_dispatch(const void* a, const float* as, const void* wq, const void* sq
     if (!tile_fits(M, N, K))
       return fail(W4A8_EINVAL, "w4a8_gemm: M=%d K=%d exceeds the tile kernel's 32-bit offsets", M,
                   K);
-    return hip_status(launch_tile(g, variant, device_info(current_device()).cus, st), "w4a8_gemm");
+    return hip_status(launch_tile(g, variant, st), "w4a8_gemm");
   }
   if (kernel == W4A8_KERNEL_STREAM) {
     if (variant < 0 || variant >= stream_variant_count())

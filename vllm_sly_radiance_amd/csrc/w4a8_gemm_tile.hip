@@ -27,8 +27,6 @@
 //    and weight panels in its own L2.
 //  * Epilogue: a lane holds 4 consecutive columns of one token; scaled by the per-token fp32 scale,
 //    rounded to bf16 and stored 8 bytes at a time.
-#include <type_traits>
-
 #include "w4a8_internal.h"
 
 namespace w4a8 {
@@ -62,7 +60,6 @@ struct TileShape {
 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
-typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 
 // s_waitcnt vmcnt(n) with lgkmcnt and expcnt left open (gfx9 encoding)
 template <int N>
@@ -374,298 +371,17 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile(
   }
 }
 
-// Persistent form of the mid-slab-barrier pipeline, for K % 512 == 0: the grid is one workgroup
-// per CU, workgroup b walks the tiles b, b + G, b + 2G, ... (XCD-contiguous order, as above), and
-// the fill stream runs across tile boundaries - slab kt+NS of the stream may be the next tile's
-// first slab - so a tile's first slabs land while the previous tile finishes and stores, instead
-// of behind a per-tile prologue (measured ~4 us per 256 x 256 tile on MI355X). The scale ring
-// counts k-groups along the stream; each slab's fills also carry one token-scale op (real for a
-// tile's first slab: the tile's BM scales into one of two LDS buffers; a zero fill otherwise).
-template <int WM, int WN, int NS, int NW>
-__global__ __launch_bounds__(NW * 64) void gemm_tile_pers(
-    const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
-    const uint32_t* __restrict__ Sq, uint16_t* __restrict__ C, int M, int N, int K, int KTp,
-    int KTe, int KG, int NTILES, int grid_m, int grid_n, int ldc, int vec_out) {
-  using S = TileShape<WM, WN, NW>;
-  constexpr int OPS = S::OPS + 1;                // fills per wave per slab, + the token-scale op
-  constexpr int P = WM - 2;
-  static_assert(WM >= 3 && NS >= 2 && NS <= 5, "pipeline depth");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * S::STAGE + 3 * S::S_SLOT +
-                                                         2 * S::TSCALE + 256];
-  uint8_t* const sring = lds + NS * S::STAGE;
-  uint8_t* const tscale = sring + 3 * S::S_SLOT;     // [2][BM] fp32, by tile parity
-  uint8_t* const junk = tscale + 2 * S::TSCALE;      // sink of the zero token-scale fills
-
-  const int total = grid_m * grid_n, G = gridDim.x, b = blockIdx.x;
-  const int ntl = (total - b + G - 1) / G;           // tiles of this workgroup (b < total)
-  const int KQ = KTe >> 2;                           // k-groups per tile
-
-  // tile i of this workgroup -> (first token, first n-tile); past the last tile: tile 0's.
-  // Branch-free (selects only), so the k-loop that advances the fill cursor stays one block.
-  auto tile_at = [&](int i, int& m0, int& ntb) {
-    int t = i < ntl ? b + i * G : b;
-    t = total % 8 == 0 ? (t % 8) * (total / 8) + t / 8 : t;
-    constexpr int GROUP = 8;
-    const int per_group = GROUP * grid_n;
-    const int first_m = (t / per_group) * GROUP;
-    const int gm = min(grid_m - first_m, GROUP);
-    m0 = (first_m + (t % per_group) % gm) * S::BM;
-    ntb = ((t % per_group) / gm) * (S::BN / 16);
-  };
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;           // (NW / 2) x 2 waves
-  const auto a_src = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, M * K, kBufferWord3);
-  const auto as_src = __builtin_amdgcn_make_buffer_rsrc((void*)As, 0, M * 4, kBufferWord3);
-  const int a_row = lane >> 3;
-  const int a_chunk = (lane & 7) ^ (a_row >> 1);
-  const int f_row = lane & 15;
-  const int f_lo = 1024 * (f_row >> 3) + 16 * (8 * (f_row & 7) + ((lane >> 4) ^ ((f_row >> 1) & 7)));
-  const int f_hi = f_lo ^ 64;
-
-  // Fill ops [o0, o1) of one stream slab into stage base. The slab is k-tile fkt of the tile at
-  // (fm0, fntb) (kin: that tile exists); it also carries quarter fg % 4 of the scale rows of the
-  // next stream k-group: group sgrp of the tile at sntb (sin: that tile exists); and, when fkt is
-  // 0, the tile's token scales (parity tpar). Op o: an activation unit, a weight granule, a scale
-  // row, or the token-scale op. All arguments are scalar and every choice below is a select.
-  auto fill_ops = [&](int fg, int fkt, int fm0, int fntb, bool kin, int sntb, int sgrp, bool sin,
-                      int tpar, uint8_t* base, int o0, int o1) {
-    const int nth = kin ? min(S::BN / 16, NTILES - fntb) : 0;
-    const auto w_src = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(Wq + (size_t)fntb * KTp * kGranuleBytes), 0, nth * KTp * kGranuleBytes,
-        kBufferWord3);
-    const int snth = sin ? min(S::BN / 16, NTILES - sntb) : 0;
-    const auto s_src = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(Sq + (size_t)sntb * KG * 64), 0, snth * KG * 256, kBufferWord3);
-#pragma unroll
-    for (int o = 0; o < OPS; ++o) {
-      if (o < o0 || o >= o1) continue;
-      if (o < S::A_PER_WAVE) {
-        const int unit = wave * S::A_PER_WAVE + o;
-        const int row = fm0 + unit * 8 + a_row;
-        const int col = fkt * kKTile + 16 * (a_chunk ^ ((unit & 1) << 2));
-        const int off = (kin & (col < K) & (row < M)) ? row * K + col : kOut;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(a_src, (lds_ptr_t)(base + unit * 1024), 16, off,
-                                                 0, 0, 0);
-      } else if (o < S::A_PER_WAVE + S::W_PER_WAVE) {
-        const int g = wave * S::W_PER_WAVE + (o - S::A_PER_WAVE);
-        const int off =
-            (kin & (g < S::W_UNITS)) ? (g * KTp + fkt) * kGranuleBytes + lane * 16 : kOut;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(w_src, (lds_ptr_t)(base + S::W_OFF + g * 1024),
-                                                 16, off, 0, 0, kBufferNT);
-      } else if (o < S::OPS) {
-        const int q = fg & 3;
-        const int i = wave * S::S_PER_WAVE + (o - S::A_PER_WAVE - S::W_PER_WAVE);
-        const int r = q * S::S_QUARTER + i;
-        const bool real = (i < S::S_QUARTER) & (r < S::S_ROWS);
-        const int off = (real & sin) ? ((r * KG + sgrp) * 64 + lane) * 4 : kOut;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            s_src,
-            (lds_ptr_t)(sring + (((fg >> 2) + 1) % 3) * S::S_SLOT +
-                        (real ? r : 4 * S::S_QUARTER) * 256),
-            4, off, 0, 0, 0);
-      } else {
-        const int r = wave * 64 + lane;
-        const bool real = kin & (fkt == 0) & (wave * 64 < S::BM);
-        const int off = (real & (r < S::BM) & (fm0 + r < M)) ? (fm0 + r) * 4 : kOut;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            as_src, (lds_ptr_t)(real ? tscale + tpar * S::TSCALE + wave * 256 : junk), 4, off, 0,
-            0, 0);
-      }
-    }
-  };
-  auto read_w = [&](int st, int g, v4i* wf, uint32_t* sc) {
-    const uint8_t* base = lds + st * S::STAGE;
-    const uint8_t* srow = sring + ((g >> 2) % 3) * S::S_SLOT + lane * 4;
-#pragma unroll
-    for (int j = 0; j < WN; ++j) {
-      wf[j] = *reinterpret_cast<const v4i*>(base + S::W_OFF + (wn * WN + j) * 1024 + lane * 16);
-      sc[j] = *reinterpret_cast<const uint32_t*>(srow + (wn * WN + j) * 256);
-    }
-  };
-  auto read_a = [&](int st, int i, v4i& lo, v4i& hi) {
-    const uint8_t* pa = lds + st * S::STAGE + (wm * WM + i) * 2048;
-    lo = *reinterpret_cast<const v4i*>(pa + f_lo);
-    hi = *reinterpret_cast<const v4i*>(pa + f_hi);
-  };
-
-  // stream k-group 0's scale rows (tile 0), then slabs 0..NS-1 (all of tile 0: KTe >= 2 NS)
-  int c_m0, c_ntb, n1_m0, n1_ntb, n2_m0, n2_ntb;
-  tile_at(0, c_m0, c_ntb);
-  tile_at(1, n1_m0, n1_ntb);
-  {
-    const int nth = min(S::BN / 16, NTILES - c_ntb);
-    const auto s_src = __builtin_amdgcn_make_buffer_rsrc((void*)(Sq + (size_t)c_ntb * KG * 64),
-                                                         0, nth * KG * 256, kBufferWord3);
-    const int i = wave * S::S_PER_WAVE;
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-#pragma unroll
-      for (int e = 0; e < S::S_PER_WAVE; ++e) {
-        const int r = q * S::S_QUARTER + i + e;
-        const bool real = (i + e < S::S_QUARTER) & (r < S::S_ROWS);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            s_src, (lds_ptr_t)(sring + (real ? r : 4 * S::S_QUARTER) * 256), 4,
-            real ? (r * KG * 64 + lane) * 4 : kOut, 0, 0, 0);
-      }
-  }
-#pragma unroll
-  for (int p = 0; p < NS; ++p) {
-    const bool sn = (p >> 2) + 1 == KQ;
-    fill_ops(p, p, c_m0, c_ntb, true, sn ? n1_ntb : c_ntb, sn ? 0 : (p >> 2) + 1, !sn || 1 < ntl,
-             0, lds + p * S::STAGE, 0, OPS);
-  }
-  wait_vmcnt<(NS - 1) * OPS>();                  // slab 0 (and everything older) has landed
-  bare_barrier();
-  v4i wf[WN], lo, hi;
-  uint32_t sc[WN];
-  read_w(0, 0, wf, sc);
-  read_a(0, 0, lo, hi);
-  __builtin_amdgcn_s_waitcnt(0xC07F);            // lgkmcnt(0): the k-steps start with nothing pending
-  // Output: a tile's results leave as ST = WM * WN 8-byte stores per wave right after its last
-  // slab. Stores count in vmcnt like the fills, so the first NS-1 slab waits of the next tile
-  // (whose awaited fills are older than the stores) allow ST more outstanding ops; from slab NS-1
-  // on, the awaited fills are younger than the stores, which have had NS-1 slabs to drain.
-  constexpr int ST = WM * WN;
-  static_assert((NS - 2) * OPS + ST < 64, "vmcnt range");
-  int st = 0, g = 0;
-  int c_m0_ = 0, c_ntb_ = 0, n1_m0_ = 0, n1_ntb_ = 0, n2_m0_ = 0, n2_ntb_ = 0;
-  bool v1_ = false, v2_ = false;
-  int tile = 0;
-  v4f acc[WM][WN];
-  auto set_tile = [&](int t) {
-    tile = t;
-    tile_at(t, c_m0_, c_ntb_);
-    tile_at(t + 1, n1_m0_, n1_ntb_);
-    tile_at(t + 2, n2_m0_, n2_ntb_);
-    v1_ = t + 1 < ntl;
-    v2_ = t + 2 < ntl;
-#pragma unroll
-    for (int i = 0; i < WM; ++i)
-#pragma unroll
-      for (int j = 0; j < WN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-  };
-  // one slab of the current tile: k-tile kt; EXTRA: stores outstanding beyond the fills
-  auto kstep = [&](int kt, auto extra) {
-    constexpr int EXTRA = decltype(extra)::value;
-    const int nst = st + 1 == NS ? 0 : st + 1;
-    uint8_t* fbase = lds + st * S::STAGE;        // slab g's stage, refilled with slab g+NS
-    // slab g+NS: k-tile fkt of this tile or the next; its scale rows: the next k-group
-    const bool fw = kt + NS >= KTe;
-    const int fkt = fw ? kt + NS - KTe : kt + NS;
-    const int fm0 = fw ? n1_m0_ : c_m0_, fntb = fw ? n1_ntb_ : c_ntb_;
-    const bool kin = fw ? v1_ : true;
-    const bool sn = (fkt >> 2) + 1 == KQ;
-    const int sgrp = sn ? 0 : (fkt >> 2) + 1;
-    const int sntb = (fw & sn) ? n2_ntb_ : (fw | sn) ? n1_ntb_ : c_ntb_;
-    const bool sin = (fw & sn) ? v2_ : (fw | sn) ? v1_ : true;
-    const int tpar = (tile + fw) & 1;
-    v4i wfn[WN], lon, hin;
-    uint32_t scn[WN];
-#pragma unroll
-    for (int i = 0; i < P; ++i) {
-      const v8i xf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      read_a(st, i + 1, lo, hi);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int j = 0; j < WN; ++j)
-        acc[i][j] = mfma_w4a8(wf[j], xf, acc[i][j], sc[j] >> (8 * (g & 3)));
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    {
-      // the last two groups, as in the plain form: reads and refills one or two per MFMA
-      const v8i xp = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      read_a(st, P + 1, lo, hi);
-      wait_vmcnt<(NS - 2) * OPS + EXTRA>();      // this wave's fills of slab g+1 have landed
-      __builtin_amdgcn_s_waitcnt(0xC07F);        // lgkmcnt(0): this wave's reads of slab g done
-      bare_barrier();
-      __builtin_amdgcn_sched_barrier(0);
-      const v8i xq = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      const uint8_t* nbase = lds + nst * S::STAGE;
-      const uint8_t* srow = sring + (((g + 1) >> 2) % 3) * S::S_SLOT + lane * 4;
-#pragma unroll
-      for (int m = 0; m < 2 * WN; ++m) {
-        const int j = m % WN;
-        if (m < WN)
-          acc[P][j] = mfma_w4a8(wf[j], xp, acc[P][j], sc[j] >> (8 * (g & 3)));
-        else
-          acc[P + 1][j] = mfma_w4a8(wf[j], xq, acc[P + 1][j], sc[j] >> (8 * (g & 3)));
-        __builtin_amdgcn_sched_barrier(0);
-        if (m < WN) {
-          wfn[m] =
-              *reinterpret_cast<const v4i*>(nbase + S::W_OFF + (wn * WN + m) * 1024 + lane * 16);
-          scn[m] = *reinterpret_cast<const uint32_t*>(srow + (wn * WN + m) * 256);
-        }
-        if (m == WN) read_a(nst, 0, lon, hin);
-        if (m < OPS)
-          fill_ops(g + NS, fkt, fm0, fntb, kin, sntb, sgrp, sin, tpar, fbase, m,
-                   m == 2 * WN - 1 ? OPS : m + 1);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-    __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0): slab g+1's fragments are in
-#pragma unroll
-    for (int j = 0; j < WN; ++j) wf[j] = wfn[j], sc[j] = scn[j];
-    lo = lon;
-    hi = hin;
-    st = nst;
-    ++g;
-  };
-  using no_stores = std::integral_constant<int, 0>;
-  using after_stores = std::integral_constant<int, ST>;
-  // The stores go through a buffer resource with every lane active (an out-of-range element gets
-  // an offset past the resource), so each wave issues exactly ST of them whatever the tile edge.
-  const auto c_dst = __builtin_amdgcn_make_buffer_rsrc((void*)C, 0, M * ldc * 2, kBufferWord3);
-  auto epilogue = [&]() {
-    const float* ts = reinterpret_cast<const float*>(tscale + (tile & 1) * S::TSCALE);
-#pragma unroll
-    for (int i = 0; i < WM; ++i) {
-      const int m = c_m0_ + (wm * WM + i) * 16 + (lane & 15);
-      const float tsc = ts[(wm * WM + i) * 16 + (lane & 15)];
-#pragma unroll
-      for (int j = 0; j < WN; ++j) {
-        const int n = (c_ntb_ + wn * WN + j) * kNTile + 4 * (lane >> 4);
-        const v4f v = acc[i][j];
-        const uint32_t b0 = f32_to_bf16(v[0] * tsc), b1 = f32_to_bf16(v[1] * tsc);
-        const uint32_t b2 = f32_to_bf16(v[2] * tsc), b3 = f32_to_bf16(v[3] * tsc);
-        const int off = ((m < M) & (n < N)) ? (m * ldc + n) * 2 : kOut;
-        __builtin_amdgcn_raw_buffer_store_b64(v2u{b0 | (b1 << 16), b2 | (b3 << 16)}, c_dst, off, 0,
-                                              0);
-      }
-    }
-  };
-
-  // the first NS-1 slabs of a tile wait on fills issued before the previous tile's stores
-  set_tile(0);
-#pragma unroll
-  for (int kt = 0; kt + 1 < NS; ++kt) kstep(kt, no_stores{});
-  for (int t = 0; t < ntl; ++t) {
-    for (int kt = NS - 1; kt < KTe; ++kt) kstep(kt, no_stores{});
-    epilogue();
-    if (t + 1 < ntl) {
-      set_tile(t + 1);
-#pragma unroll
-      for (int kt = 0; kt + 1 < NS; ++kt) kstep(kt, after_stores{});
-    }
-  }
-  wait_vmcnt<0>();                               // no fill may outlive the workgroup's LDS
-}
-
-// (WM, WN, NS, NW, PERS): NW waves of 16 WM x 16 WN in an (NW / 2) x 2 arrangement, NS-stage LDS
-// pipeline (LDS = NS * STAGE + 3 scale slots + token scales <= 160 KiB); PERS: the persistent form
-// (one workgroup per CU; needs K % 512 == 0 and at least 2 NS k-tiles, else the plain form runs)
+// (WM, WN, NS, NW): NW waves of 16 WM x 16 WN in an (NW / 2) x 2 arrangement, NS-stage LDS
+// pipeline (LDS = NS * STAGE + 3 scale slots + token scales <= 160 KiB)
 #define W4A8_TILE_TABLE(X)                                                                        \
-  X(2, 4, 4, 4, 0) X(4, 4, 3, 4, 0) X(4, 4, 4, 4, 0) X(8, 4, 3, 4, 0) X(4, 8, 3, 4, 0)            \
-  X(8, 8, 3, 4, 0) X(8, 5, 3, 4, 0) X(4, 8, 4, 4, 0) X(4, 2, 4, 4, 0) X(1, 2, 4, 4, 0)            \
-  X(2, 2, 4, 4, 0) X(1, 4, 4, 4, 0) X(2, 2, 5, 4, 0) X(4, 8, 3, 8, 0) X(4, 5, 3, 8, 0)            \
-  X(4, 5, 3, 8, 1)
+  X(2, 4, 4, 4) X(4, 4, 3, 4) X(4, 4, 4, 4) X(8, 4, 3, 4) X(4, 8, 3, 4) X(8, 8, 3, 4)            \
+  X(8, 5, 3, 4) X(4, 8, 4, 4) X(4, 2, 4, 4) X(1, 2, 4, 4) X(2, 2, 4, 4) X(1, 4, 4, 4)            \
+  X(2, 2, 5, 4) X(4, 8, 3, 8) X(4, 5, 3, 8)
 
-#define W4A8_TILE_CFG(wm, wn, ns, nw, pers)                                                       \
+#define W4A8_TILE_CFG(wm, wn, ns, nw)                                                             \
   TileCfg{wm, wn, TileShape<wm, wn, nw>::BM, TileShape<wm, wn, nw>::BN, nw,                        \
           ns * TileShape<wm, wn, nw>::STAGE + 3 * TileShape<wm, wn, nw>::S_SLOT +                \
-              (pers ? 2 : 1) * TileShape<wm, wn, nw>::TSCALE + (pers ? 256 : 0),                 \
-          pers},
+              TileShape<wm, wn, nw>::TSCALE},
 constexpr TileCfg kTile[] = {W4A8_TILE_TABLE(W4A8_TILE_CFG)};
 #undef W4A8_TILE_CFG
 constexpr int kTileCount = sizeof(kTile) / sizeof(kTile[0]);
@@ -681,7 +397,7 @@ bool tile_fits(int M, int N, int K) {
          (long)N < (1L << 24);
 }
 
-hipError_t launch_tile(const GemmArgs& g, int variant, int cus, hipStream_t stream) {
+hipError_t launch_tile(const GemmArgs& g, int variant, hipStream_t stream) {
   const TileCfg c = kTile[variant];
   const int KTp = padded_k(g.K) / kKTile, KTe = ceil_div(g.K, kKTile), KG = KTp / kKGroup;
   const int NTILES = padded_n(g.N) / kNTile;
@@ -692,23 +408,11 @@ hipError_t launch_tile(const GemmArgs& g, int variant, int cus, hipStream_t stre
                                                                                          : 0;
   const dim3 grid(grid_m * grid_n), block(c.nw * 64);
   int idx = 0;
-#define W4A8_TILE_LAUNCH(wm, wn, ns, nw, pers)                                                 \
+#define W4A8_TILE_LAUNCH(wm, wn, ns, nw)                                                       \
   if (idx++ == variant) {                                                                        \
-    if constexpr (pers) {                                                                         \
-      if (KTe % 4 == 0 && KTe >= 2 * ns && vec_out >= 1 &&                                       \
-          (long)g.M * g.ldc * 2 < (1L << 31)) {                                                   \
-        const int G = grid_m * grid_n < cus ? grid_m * grid_n : cus;                             \
-        hipLaunchKernelGGL((gemm_tile_pers<wm, wn, ns, nw>), dim3(G), block, 0, stream, g.a,     \
-                           g.a_scale, g.wq, g.sq, g.c, g.M, g.N, g.K, KTp, KTe, KG, NTILES,      \
-                           grid_m, grid_n, g.ldc, vec_out);                                      \
-        return hipGetLastError();                                                                \
-      }                                                                                          \
-    }                                                                                            \
-    {                                                                                            \
-      hipLaunchKernelGGL((gemm_tile<wm, wn, ns, nw>), grid, block, 0, stream, g.a, g.a_scale,    \
-                         g.wq, g.sq, g.c, g.M, g.N, g.K, KTp, KTe, KG, NTILES, grid_m, grid_n,   \
-                         g.ldc, vec_out);                                                        \
-    }                                                                                            \
+    hipLaunchKernelGGL((gemm_tile<wm, wn, ns, nw>), grid, block, 0, stream, g.a, g.a_scale, g.wq, \
+                       g.sq, g.c, g.M, g.N, g.K, KTp, KTe, KG, NTILES, grid_m, grid_n, g.ldc,     \
+                       vec_out);                                                                 \
     return hipGetLastError();                                                                    \
   }
   W4A8_TILE_TABLE(W4A8_TILE_LAUNCH)

@@ -128,11 +128,11 @@ hipError_t launch_stream(const GemmArgs& g, int variant, int cus, hipStream_t st
 
 // Macro-tile family (M > 16). variant indexes the instantiated (WM, WN, NS, NW) table: nw waves of
 // wm x wn 16 x 16 MFMA tiles, a bm x bn workgroup tile.
-struct TileCfg { int wm, wn, bm, bn, nw, lds, pers; };
+struct TileCfg { int wm, wn, bm, bn, nw, lds; };
 int tile_variant_count();
 TileCfg tile_variant(int v);
 bool tile_fits(int M, int N, int K);
-hipError_t launch_tile(const GemmArgs& g, int variant, int cus, hipStream_t stream);
+hipError_t launch_tile(const GemmArgs& g, int variant, hipStream_t stream);
 
 // Register-resident MFMA throughput probe (shape 0: 16x16x128, 1: 32x32x64).
 hipError_t launch_mfma_probe(int shape, float* out, int blocks, int iters, double* flop,
