@@ -116,6 +116,35 @@ int w4a8_scratch_bytes(int variant, int N, int split_k, size_t* partial_bytes,
 int w4a8_linear(const void* x, long ldx, void* q, float* scale, const void* wq, const void* sq,
                 void* c, int M, int N, int K, void* stream);
 
+/* (4) Fused fp8 activation producers. Each writes the (q [M, K] e4m3fn, scale [M] fp32) pair of
+ * entry point (1) for its bf16 result, so the pair can feed w4a8_gemm directly (the tuple branch of
+ * apply_weights, radiance::mxfp4_linear_pq). One workgroup per row; every floating-point step is
+ * fixed (no fused multiply-add, fixed summation order, correctly rounded 1/sqrt, a self-contained
+ * exp), so the results are reproducible bit for bit. Rows are contiguous and 16-byte aligned. */
+
+/* Gemma RMSNorm with residual, then quant: v = y + residual (fp32), residual_out = bf16(v),
+ * x = bf16(v * rsqrt(mean(v^2) + eps) * (weight + 1)). y, residual, residual_out bf16 [M, K],
+ * weight bf16 [K]; K % 8 == 0, K <= 10240. Replaces launch_add_rms_quant
+ * (sly/mxfp4/radiance_mxfp4_fp8.hip:2196-2234; kernel :1834-1933), behind the reference's
+ * radiance::add_rms_quant op (sly/mxfp4/radiance_fused_norm.py:132-160). */
+int w4a8_add_rms_quant(const void* y, const void* residual, const void* weight, void* q,
+                       float* scale, void* residual_out, int M, int K, float eps, void* stream);
+
+/* SiLU-and-mul, then quant: gate_up bf16 [M, 2N] (gate = columns 0..N-1, up = N..2N-1) ->
+ * x = bf16(bf16(silu(gate)) * up), q [M, N]; N % 8 == 0, N <= 18432. Replaces
+ * launch_silu_mul_quant (sly/mxfp4/radiance_mxfp4_fp8.hip:2019-2066; kernel :1935-2010), behind
+ * radiance::silu_mul_quant (sly/mxfp4/radiance_fused_norm.py:163-187). */
+int w4a8_silu_mul_quant(const void* gate_up, void* q, float* scale, int M, int N, void* stream);
+
+/* Per-head gated RMSNorm (heads of 128, norm before the gate, silu gate, weight without +1), then
+ * quant: x = bf16(x * rsqrt(mean_head(x^2) + eps) * weight * silu(z)). x bf16 [M, N] contiguous,
+ * z bf16 [M, N] with row stride z_stride elements (a column slice of a wider projection; a
+ * multiple of 8), weight bf16 [128] shared by the heads; N % 128 == 0, N <= 10240. Replaces
+ * launch_gdn_norm_quant (sly/mxfp4/radiance_mxfp4_fp8.hip:2159-2195; kernel :2068-2156), behind
+ * radiance::gdn_norm_quant (sly/mxfp4/radiance_fused_norm.py:189-220). */
+int w4a8_gdn_norm_quant(const void* x, const void* z, long z_stride, const void* weight, void* q,
+                        float* scale, int M, int N, float eps, void* stream);
+
 /* Diagnostic: register-resident throughput probe of the scaled MFMA (fp4 A x fp8 B) the GEMMs
  * issue; shape 0 = 16x16x128, 1 = 32x32x64. Launches `blocks` workgroups of 4 waves that write
  * blocks*4 checksums to out; *flop receives the FLOP performed, the caller times the launch. The

@@ -148,3 +148,28 @@ def test_quant_and_repack_validate(lib):
     assert lib.w4a8_quant_per_token(None, 8, None, None, 0, 8, None) == 0
     assert lib.w4a8_quant_per_token(4096, 4, 4096, 4096, 4, 8, None) == 1   # ldx < K
     assert lib.w4a8_repack(None, None, None, None, 16, 100, None) == 1
+
+
+@pytest.mark.parametrize("K,msg", [(12, b"8-aligned"), (10248, b"<= 10240"), (0, b"8-aligned")])
+def test_add_rms_quant_validates_before_launch(lib, K, msg):
+    p = 4096
+    assert lib.w4a8_add_rms_quant(p, p, p, p, p, p, 4, K, 1e-6, None) == 1
+    assert msg in lib.w4a8_last_error()
+
+
+def test_producers_validate_before_launch(lib):
+    p = 4096
+    assert lib.w4a8_add_rms_quant(None, None, None, None, None, None, 0, 8, 1e-6, None) == 0
+    assert lib.w4a8_add_rms_quant(None, p, p, p, p, p, 4, 8, 1e-6, None) == 1       # null y
+    assert lib.w4a8_add_rms_quant(p + 2, p, p, p, p, p, 4, 8, 1e-6, None) == 1      # misaligned
+    assert lib.w4a8_silu_mul_quant(p, p, p, 4, 12, None) == 1
+    assert b"8-aligned" in lib.w4a8_last_error()
+    assert lib.w4a8_silu_mul_quant(p, p, p, 4, 18440, None) == 1
+    assert lib.w4a8_silu_mul_quant(p, p + 4, p, 4, 16, None) == 1                  # q misaligned
+    assert lib.w4a8_silu_mul_quant(None, None, None, 0, 16, None) == 0
+    assert lib.w4a8_gdn_norm_quant(p, p, 256, p, p, p, 4, 200, 1e-6, None) == 1
+    assert b"multiple of 128" in lib.w4a8_last_error()
+    assert lib.w4a8_gdn_norm_quant(p, p, 100, p, p, p, 4, 128, 1e-6, None) == 1     # stride < N
+    assert lib.w4a8_gdn_norm_quant(p, p, 132, p, p, p, 4, 128, 1e-6, None) == 1     # stride % 8
+    assert b"stride" in lib.w4a8_last_error()
+    assert lib.w4a8_gdn_norm_quant(p, p + 8, 256, p, p, p, 4, 128, 1e-6, None) == 1  # z misaligned

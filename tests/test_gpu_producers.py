@@ -1,0 +1,204 @@
+"""GPU parity of the fused fp8 activation producers against the oracle, through the C ABI and the
+custom ops. Bar: codes, scales and the bf16 residual output bit-exact (every floating-point step of
+the producers is fixed; oracle/producers_oracle.py)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import mxfp4_oracle as O
+from oracle import producers_oracle as P
+from tests._check import bf16_dev, host_u16, host_u8, to_dev
+from vllm_sly_radiance_amd import _native, synthetic
+from vllm_sly_radiance_amd import radiance_fused_norm as FN
+from vllm_sly_radiance_amd import radiance_mxfp4 as R
+
+pytestmark = pytest.mark.gpu
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def weight_bits(K, seed, mean=0.0, sd=0.1):
+    return O.f32_to_bf16((mean + np.random.default_rng(seed).standard_normal(K) * sd)
+                         .astype(np.float32))
+
+
+def gpu_add_rms(y, res, w, eps):
+    M, K = y.shape
+    q = torch.empty((M, K), dtype=torch.uint8, device="cuda")
+    s = torch.empty((M,), dtype=torch.float32, device="cuda")
+    r = torch.empty((M, K), dtype=torch.bfloat16, device="cuda")
+    yd, rd, wd = bf16_dev(y), bf16_dev(res), bf16_dev(w)
+    print(f"[producers] add_rms_quant M={M} K={K}", flush=True)
+    _native.add_rms_quant(yd.data_ptr(), rd.data_ptr(), wd.data_ptr(), q.data_ptr(), s.data_ptr(),
+                          r.data_ptr(), M, K, eps, stream())
+    torch.cuda.synchronize()
+    return host_u8(q), s.cpu().numpy(), host_u16(r)
+
+
+def assert_same_qs(q, s, oq, os_, what):
+    assert np.array_equal(np.isnan(s), np.isnan(os_)), f"{what}: NaN scales differ"
+    fin = ~np.isnan(os_)
+    bad_s = np.argwhere(s[fin].view(np.uint32) != os_[fin].view(np.uint32))
+    assert bad_s.size == 0, f"{what}: {len(bad_s)} scales differ, first rows {bad_s[:3].ravel()}"
+    canon = lambda c: np.where((c & 0x7F) == 0x7F, 0x7F, c)
+    bad = np.argwhere(canon(q) != canon(oq))
+    assert bad.size == 0, f"{what}: {len(bad)} codes differ, first at {bad[:3].tolist()}"
+
+
+@pytest.mark.parametrize("M,K", [(1, 5120), (7, 5120), (64, 8704), (3, 8), (5, 2056),
+                                 (2, 10240), (300, 5120)])
+def test_add_rms_quant_bit_exact(gpu_lib, M, K):
+    y = synthetic.activations(M, K, seed=M + K)
+    res = synthetic.activations(M, K, seed=M + K + 1)
+    w = weight_bits(K, K)
+    q, s, r = gpu_add_rms(y, res, w, 1e-6)
+    oq, os_, orr = P.add_rms_quant(y, res, w, 1e-6)
+    assert np.array_equal(r, orr), "residual_out differs"
+    assert_same_qs(q, s, oq, os_, f"add_rms M={M} K={K}")
+
+
+def test_add_rms_quant_special_rows(gpu_lib):
+    K = 512
+    rows = np.zeros((6, K), np.float32)
+    rows[1, :] = 1e30                                   # huge: sum of squares overflows to inf
+    rows[2, 5] = np.inf
+    rows[3, 9] = np.nan
+    rows[4, :] = np.linspace(-1e-20, 1e-20, K)          # tiny: eps dominates
+    rows[5, :] = 448.0
+    y = O.f32_to_bf16(rows)
+    res = O.f32_to_bf16(np.zeros_like(rows))
+    w = weight_bits(K, 1)
+    q, s, r = gpu_add_rms(y, res, w, 1e-6)
+    oq, os_, orr = P.add_rms_quant(y, res, w, 1e-6)
+    assert np.array_equal(r, orr)
+    assert_same_qs(q, s, oq, os_, "add_rms special rows")
+
+
+def test_add_rms_quant_sampled_rows_at_prefill_size(gpu_lib):
+    """M=4096 K=5120: every row on the GPU, 96 sampled rows (and the first and last) against the
+    oracle; the kernel is row-independent."""
+    M, K = 4096, 5120
+    y = synthetic.activations(M, K, seed=11)
+    res = synthetic.activations(M, K, seed=12)
+    w = weight_bits(K, 13)
+    q, s, r = gpu_add_rms(y, res, w, 1e-6)
+    rows = np.unique(np.r_[np.random.default_rng(0).choice(M, 96, replace=False), 0, M - 1])
+    oq, os_, orr = P.add_rms_quant(y[rows], res[rows], w, 1e-6)
+    assert np.array_equal(r[rows], orr)
+    assert_same_qs(q[rows], s[rows], oq, os_, "add_rms M=4096")
+
+
+def gpu_silu(gu):
+    M, N2 = gu.shape
+    N = N2 // 2
+    q = torch.empty((M, N), dtype=torch.uint8, device="cuda")
+    s = torch.empty((M,), dtype=torch.float32, device="cuda")
+    gd = bf16_dev(gu)
+    print(f"[producers] silu_mul_quant M={M} N={N}", flush=True)
+    _native.silu_mul_quant(gd.data_ptr(), q.data_ptr(), s.data_ptr(), M, N, stream())
+    torch.cuda.synchronize()
+    return host_u8(q), s.cpu().numpy()
+
+
+@pytest.mark.parametrize("M,N", [(1, 17408), (8, 17408), (33, 1000), (2, 18432), (96, 8704),
+                                 (4, 8)])
+def test_silu_mul_quant_bit_exact(gpu_lib, M, N):
+    gu = synthetic.activations(M, 2 * N, seed=M * 3 + N)
+    q, s = gpu_silu(gu)
+    oq, os_ = P.silu_mul_quant(gu)
+    assert_same_qs(q, s, oq, os_, f"silu M={M} N={N}")
+
+
+def test_silu_mul_quant_special_and_wide_range(gpu_lib):
+    """Gate values across the whole range where exp is exercised (-100 .. 100, inf, NaN)."""
+    N = 2048
+    g = np.linspace(-100.0, 100.0, 3 * N).astype(np.float32).reshape(3, N)
+    g[0, 7], g[1, 9], g[2, 11] = np.inf, -np.inf, np.nan
+    u = (np.random.default_rng(1).standard_normal((3, N)) * 2).astype(np.float32)
+    gu = np.concatenate([O.f32_to_bf16(g), O.f32_to_bf16(u)], axis=1)
+    q, s = gpu_silu(gu)
+    oq, os_ = P.silu_mul_quant(gu)
+    assert_same_qs(q, s, oq, os_, "silu special")
+
+
+def gpu_gdn(x, z_wide, col0, w, eps):
+    """z is columns col0 .. col0 + N - 1 of a wider bf16 tensor (row stride = its width)."""
+    M, N = x.shape
+    q = torch.empty((M, N), dtype=torch.uint8, device="cuda")
+    s = torch.empty((M,), dtype=torch.float32, device="cuda")
+    xd, zd, wd = bf16_dev(x), bf16_dev(z_wide), bf16_dev(w)
+    zv = zd[:, col0:col0 + N]
+    print(f"[producers] gdn_norm_quant M={M} N={N} z_stride={zv.stride(0)}", flush=True)
+    _native.gdn_norm_quant(xd.data_ptr(), zv.data_ptr(), zv.stride(0), wd.data_ptr(),
+                           q.data_ptr(), s.data_ptr(), M, N, eps, stream())
+    torch.cuda.synchronize()
+    return host_u8(q), s.cpu().numpy()
+
+
+@pytest.mark.parametrize("M,heads,extra", [(1, 24, 0), (9, 48, 2048), (64, 80, 384), (3, 1, 8)])
+def test_gdn_norm_quant_bit_exact(gpu_lib, M, heads, extra):
+    N = heads * 128
+    x = synthetic.activations(M, N, seed=M + heads)
+    zw = synthetic.activations(M, N + extra, seed=M + heads + 1)
+    w = weight_bits(128, heads, mean=1.0, sd=0.2)
+    q, s = gpu_gdn(x, zw, extra, w, 1e-6)
+    oq, os_ = P.gdn_norm_quant(x, zw[:, extra:extra + N], w, 1e-6)
+    assert_same_qs(q, s, oq, os_, f"gdn M={M} heads={heads} z offset {extra}")
+
+
+# ---- the custom ops on device tensors, and their hand-off to the GEMM -------------------------
+def test_ops_feed_the_gemm_like_the_unfused_chain(gpu_lib):
+    """radiance::add_rms_quant -> mxfp4_linear_pq gives the same bits as quantizing the producer's
+    bf16 output inside radiance::mxfp4_linear (the unfused chain), and likewise for silu_mul."""
+    M, K, N = 16, 5120, 2048
+    w, ws = synthetic.weights(N, K, seed=3)
+    wq, sq = R.repack_weights(to_dev(w), to_dev(ws))
+    wref = R.layout_ref(N, K, wq.device)
+    y, res = synthetic.activations(M, K, seed=4), synthetic.activations(M, K, seed=5)
+    nw = weight_bits(K, 6)
+    q, s, r = torch.ops.radiance.add_rms_quant(bf16_dev(y), bf16_dev(res), bf16_dev(nw), 1e-6)
+    fused = torch.ops.radiance.mxfp4_linear_pq(q, s, wq, sq, wref)
+    n, orr = P.add_rms_norm(y, res, nw, 1e-6)
+    assert np.array_equal(host_u16(r), orr)
+    unfused = torch.ops.radiance.mxfp4_linear(bf16_dev(n), wq, sq, wref)
+    assert torch.equal(fused, unfused)
+
+    w2, ws2 = synthetic.weights(K, N, seed=7)            # down_proj-like: K_in = N
+    wq2, sq2 = R.repack_weights(to_dev(w2), to_dev(ws2))
+    wref2 = R.layout_ref(K, N, wq2.device)
+    gu = synthetic.activations(M, 2 * N, seed=8)
+    q2, s2 = torch.ops.radiance.silu_mul_quant(bf16_dev(gu))
+    fused2 = torch.ops.radiance.mxfp4_linear_pq(q2, s2, wq2, sq2, wref2)
+    unfused2 = torch.ops.radiance.mxfp4_linear(bf16_dev(P.silu_mul(gu)), wq2, sq2, wref2)
+    assert torch.equal(fused2, unfused2)
+
+
+def test_gdn_op_takes_a_column_slice_of_z(gpu_lib):
+    M, heads = 5, 24
+    N = heads * 128
+    x = synthetic.activations(M, N, seed=1)
+    zw = synthetic.activations(M, 3 * N, seed=2)
+    w = weight_bits(128, 3, mean=1.0, sd=0.2)
+    zd = bf16_dev(zw)
+    q, s = torch.ops.radiance.gdn_norm_quant(bf16_dev(x), zd[:, N:2 * N], bf16_dev(w), 1e-6)
+    oq, os_ = P.gdn_norm_quant(x, zw[:, N:2 * N], w, 1e-6)
+    assert_same_qs(host_u8(q), s.cpu().numpy(), oq, os_, "gdn op on a z slice")
+
+
+def test_ops_reject_bad_shapes(gpu_lib):
+    with pytest.raises(RuntimeError, match="8-aligned"):
+        torch.ops.radiance.add_rms_quant(torch.zeros(2, 12, dtype=torch.bfloat16, device="cuda"),
+                                         torch.zeros(2, 12, dtype=torch.bfloat16, device="cuda"),
+                                         torch.zeros(12, dtype=torch.bfloat16, device="cuda"),
+                                         1e-6)
+    with pytest.raises(RuntimeError, match="multiple of 128"):
+        torch.ops.radiance.gdn_norm_quant(torch.zeros(2, 200, dtype=torch.bfloat16, device="cuda"),
+                                          torch.zeros(2, 200, dtype=torch.bfloat16, device="cuda"),
+                                          torch.zeros(128, dtype=torch.bfloat16, device="cuda"),
+                                          1e-6)
+    with pytest.raises(RuntimeError, match="bfloat16"):
+        FN.silu_mul_quant(torch.zeros(2, 16, dtype=torch.float32, device="cuda"))
+    q, s = FN.silu_mul_quant(torch.zeros(0, 16, dtype=torch.bfloat16, device="cuda"))
+    assert q.shape == (0, 8) and s.shape == (0,)

@@ -37,6 +37,9 @@ SIGNATURES = {
     "w4a8_variant_info": (_int, [_int, _int, _pint, _pint, _pint, _pint]),
     "w4a8_scratch_bytes": (_int, [_int, _int, _int, _psz, _psz]),
     "w4a8_linear": (_int, [_vp, _long, _vp, _vp, _vp, _vp, _vp, _int, _int, _int, _vp]),
+    "w4a8_add_rms_quant": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _int, _int, _c.c_float, _vp]),
+    "w4a8_silu_mul_quant": (_int, [_vp, _vp, _vp, _int, _int, _vp]),
+    "w4a8_gdn_norm_quant": (_int, [_vp, _vp, _long, _vp, _vp, _vp, _int, _int, _c.c_float, _vp]),
     "w4a8_mfma_probe": (_int, [_int, _vp, _int, _int, _c.POINTER(_c.c_double), _vp]),
     "w4a8_mfma_tile": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _vp]),
 }
@@ -91,6 +94,20 @@ def gemm(a_ptr, as_ptr, wq_ptr, sq_ptr, c_ptr, M, N, K, stream, kernel=KERNEL_AU
 
 def linear(x_ptr, ldx, q_ptr, s_ptr, wq_ptr, sq_ptr, c_ptr, M, N, K, stream):
     check(lib().w4a8_linear(x_ptr, ldx, q_ptr, s_ptr, wq_ptr, sq_ptr, c_ptr, M, N, K, stream))
+
+
+def add_rms_quant(y_ptr, res_ptr, w_ptr, q_ptr, s_ptr, res_out_ptr, M, K, eps, stream):
+    check(lib().w4a8_add_rms_quant(y_ptr, res_ptr, w_ptr, q_ptr, s_ptr, res_out_ptr, M, K, eps,
+                                   stream))
+
+
+def silu_mul_quant(gu_ptr, q_ptr, s_ptr, M, N, stream):
+    check(lib().w4a8_silu_mul_quant(gu_ptr, q_ptr, s_ptr, M, N, stream))
+
+
+def gdn_norm_quant(x_ptr, z_ptr, z_stride, w_ptr, q_ptr, s_ptr, M, N, eps, stream):
+    check(lib().w4a8_gdn_norm_quant(x_ptr, z_ptr, z_stride, w_ptr, q_ptr, s_ptr, M, N, eps,
+                                    stream))
 
 
 def set_scratch(partial_ptr, partial_bytes, counter_ptr, counter_bytes):

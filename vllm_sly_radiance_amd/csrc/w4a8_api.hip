@@ -401,6 +401,61 @@ W4A8_API int w4a8_linear(const void* x, long ldx, void* q, float* scale, const v
   return w4a8_gemm(q, scale, wq, sq, c, M, N, K, stream);
 }
 
+W4A8_API int w4a8_add_rms_quant(const void* y, const void* residual, const void* weight, void* q,
+                                float* scale, void* residual_out, int M, int K, float eps,
+                                void* stream) {
+  if (M < 0 || K <= 0 || K % 8 || K > 10240)
+    return fail(W4A8_EINVAL, "w4a8_add_rms_quant: K must be 8-aligned and <= 10240 (M=%d K=%d)",
+                M, K);
+  if (M == 0) return W4A8_OK;
+  if (!y || !residual || !weight || !q || !scale || !residual_out)
+    return fail(W4A8_EINVAL, "w4a8_add_rms_quant: null pointer");
+  if (!aligned(y, 16) || !aligned(residual, 16) || !aligned(weight, 16) ||
+      !aligned(residual_out, 16) || !aligned(q, 8) || !aligned(scale, 4))
+    return fail(W4A8_EINVAL,
+                "w4a8_add_rms_quant: y, residual, weight and residual_out need 16-byte alignment, "
+                "q 8-byte, scale 4-byte");
+  return hip_status(launch_add_rms_quant(y, residual, weight, (uint8_t*)q, scale, residual_out, M,
+                                         K, eps, (hipStream_t)stream),
+                    "w4a8_add_rms_quant");
+}
+
+W4A8_API int w4a8_silu_mul_quant(const void* gate_up, void* q, float* scale, int M, int N,
+                                 void* stream) {
+  if (M < 0 || N <= 0 || N % 8 || N > 18432)
+    return fail(W4A8_EINVAL, "w4a8_silu_mul_quant: N must be 8-aligned and <= 18432 (M=%d N=%d)",
+                M, N);
+  if (M == 0) return W4A8_OK;
+  if (!gate_up || !q || !scale) return fail(W4A8_EINVAL, "w4a8_silu_mul_quant: null pointer");
+  if (!aligned(gate_up, 16) || !aligned(q, 8) || !aligned(scale, 4))
+    return fail(W4A8_EINVAL,
+                "w4a8_silu_mul_quant: gate_up needs 16-byte alignment, q 8-byte, scale 4-byte");
+  return hip_status(
+      launch_silu_mul_quant(gate_up, (uint8_t*)q, scale, M, N, (hipStream_t)stream),
+      "w4a8_silu_mul_quant");
+}
+
+W4A8_API int w4a8_gdn_norm_quant(const void* x, const void* z, long z_stride, const void* weight,
+                                 void* q, float* scale, int M, int N, float eps, void* stream) {
+  if (M < 0 || N <= 0 || N % 128 || N > 10240)
+    return fail(W4A8_EINVAL,
+                "w4a8_gdn_norm_quant: N must be a multiple of 128 and <= 10240 (M=%d N=%d)", M, N);
+  if (M == 0) return W4A8_OK;
+  if (z_stride % 8 || (M > 1 && z_stride < N))
+    return fail(W4A8_EINVAL, "w4a8_gdn_norm_quant: z row stride %ld must be 8-aligned and >= N",
+                z_stride);
+  if (!x || !z || !weight || !q || !scale)
+    return fail(W4A8_EINVAL, "w4a8_gdn_norm_quant: null pointer");
+  if (!aligned(x, 16) || !aligned(z, 16) || !aligned(weight, 16) || !aligned(q, 8) ||
+      !aligned(scale, 4))
+    return fail(W4A8_EINVAL,
+                "w4a8_gdn_norm_quant: x, z and weight need 16-byte alignment, q 8-byte, scale "
+                "4-byte");
+  return hip_status(launch_gdn_norm_quant(x, z, z_stride, weight, (uint8_t*)q, scale, M, N, eps,
+                                          (hipStream_t)stream),
+                    "w4a8_gdn_norm_quant");
+}
+
 W4A8_API int w4a8_mfma_probe(int shape, float* out, int blocks, int iters, double* flop,
                              void* stream) {
   if ((shape != 0 && shape != 1) || !out || !flop || blocks <= 0 || iters <= 0)

@@ -1,0 +1,90 @@
+// Per-token e4m3 quantization of bf16 rows held in registers, shared by the quantizer and the
+// fused producers. Semantics: s = max(amax(|x|) * fl32(1/448), 1/(448*512)) (a NaN in the row
+// propagates to s); q = e4m3_rne(clamp(x / s, -448, 448)) with IEEE-correct fp32 division. One
+// 256-thread workgroup (4 wave64) per row; the amax runs on the bf16 bit patterns (|x| bits =
+// x & 0x7FFF), which is exact, orders like the magnitudes and ranks NaN above inf. Codes come
+// from the hardware e4m3 converter (v_cvt_pk_fp8_f32, round to nearest even) on clamped inputs;
+// rows whose scale is not finite take a per-element path that maps NaN quotients to 0x7F.
+#pragma once
+#include "w4a8_internal.h"
+
+namespace w4a8 {
+namespace fp8 {
+
+constexpr int kThreads = 256;
+constexpr float kInv448 = 1.0f / 448.0f;            // fl32(1/448), folded at compile time
+constexpr float kMinScale = 1.0f / (448.0f * 512.0f);
+
+__device__ __forceinline__ uint32_t wave_max(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, 64));
+  return v;
+}
+
+// Row-wide max over the workgroup (all threads get the result).
+__device__ __forceinline__ uint32_t block_max(uint32_t v) {
+  __shared__ uint32_t red[kThreads / 64];
+  v = wave_max(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return max(max(red[0], red[1]), max(red[2], red[3]));
+}
+
+__device__ __forceinline__ uint32_t abs_bits_max8(const uint4 v) {
+  uint32_t m = max(v.x & 0x7FFFu, (v.x >> 16) & 0x7FFFu);
+  m = max(m, max(v.y & 0x7FFFu, (v.y >> 16) & 0x7FFFu));
+  m = max(m, max(v.z & 0x7FFFu, (v.z >> 16) & 0x7FFFu));
+  return max(m, max(v.w & 0x7FFFu, (v.w >> 16) & 0x7FFFu));
+}
+
+__device__ __forceinline__ float clamp448(float v) {
+  v = v > 448.0f ? 448.0f : v;                       // comparisons keep NaN
+  return v < -448.0f ? -448.0f : v;
+}
+
+__device__ __forceinline__ float lo_bf16(uint32_t d) { return __uint_as_float(d << 16); }
+__device__ __forceinline__ float hi_bf16(uint32_t d) { return __uint_as_float(d & 0xFFFF0000u); }
+
+// four quotients -> four e4m3 bytes (little-endian order: first value in byte 0)
+__device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
+}
+
+__device__ __forceinline__ uint32_t code1(float v) {
+  if (v != v) return 0x7Fu;
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v, v, 0, false) & 0xFFu;
+}
+
+__device__ __forceinline__ uint32_t pack4_any(float a, float b, float c, float d) {
+  return code1(a) | (code1(b) << 8) | (code1(c) << 16) | (code1(d) << 24);
+}
+
+template <bool kFinite>
+__device__ __forceinline__ uint32_t quant_dword(uint32_t d0, uint32_t d1, float s) {
+  const float a = clamp448(lo_bf16(d0) / s), b = clamp448(hi_bf16(d0) / s);
+  const float c = clamp448(lo_bf16(d1) / s), d = clamp448(hi_bf16(d1) / s);
+  return kFinite ? pack4(a, b, c, d) : pack4_any(a, b, c, d);
+}
+
+template <bool kFinite>
+__device__ __forceinline__ uint2 quant8(const uint4 v, float s) {
+  return make_uint2(quant_dword<kFinite>(v.x, v.y, s), quant_dword<kFinite>(v.z, v.w, s));
+}
+
+__device__ __forceinline__ float row_scale(uint32_t amax_bits) {
+  const float s = __uint_as_float(amax_bits << 16) * kInv448;
+  return s < kMinScale ? kMinScale : s;               // NaN stays NaN
+}
+
+__device__ __forceinline__ bool finite(float s) {
+  return (__float_as_uint(s) & 0x7F800000u) != 0x7F800000u;
+}
+
+// 8 bf16 values (one 16-byte group) -> 8 e4m3 codes
+__device__ __forceinline__ uint2 quant8_any_scale(const uint4 v, float s) {
+  return finite(s) ? quant8<true>(v, s) : quant8<false>(v, s);
+}
+
+}  // namespace fp8
+}  // namespace w4a8

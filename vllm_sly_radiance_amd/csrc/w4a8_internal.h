@@ -103,6 +103,13 @@ hipError_t launch_quant(const uint16_t* x, long ldx, uint8_t* q, float* s, int M
                         hipStream_t stream);
 hipError_t launch_repack(const uint8_t* w, const uint8_t* ws, uint8_t* wq, uint32_t* sq, int N,
                          int K, hipStream_t stream);
+hipError_t launch_add_rms_quant(const void* y, const void* res, const void* w, uint8_t* q,
+                                float* scale, void* res_out, int M, int K, float eps,
+                                hipStream_t stream);
+hipError_t launch_silu_mul_quant(const void* gate_up, uint8_t* q, float* scale, int M, int N,
+                                 hipStream_t stream);
+hipError_t launch_gdn_norm_quant(const void* x, const void* z, long zs, const void* w, uint8_t* q,
+                                 float* scale, int M, int N, float eps, hipStream_t stream);
 
 // Skinny split-K family (M <= 64). variant indexes the instantiated (MT, NT, WAVES, U) table.
 struct SkinnyCfg { int mt, nt, waves, unroll; };

@@ -1,0 +1,262 @@
+// Fused fp8 activation producers for gfx950: the norm / activation in front of a W4A8 GEMM and the
+// per-token e4m3 quantization in one pass, so the GEMM's (q, scale) input never exists in bf16.
+//
+// Counterparts of the reference's radiance_add_rms_quant, radiance_silu_mul_quant and
+// radiance_gdn_norm_quant (sly/mxfp4/radiance_mxfp4_fp8.hip:1834-2156; ops and call sites in
+// sly/mxfp4/radiance_fused_norm.py:132-304). One 256-thread workgroup per row; thread t owns the
+// row's 8-element groups t, t + 256, ..., read once as 16-byte vectors and kept in registers
+// through the reductions. The quantization tail is the one of the plain quantizer (w4a8_fp8.h),
+// applied to the bf16-rounded producer output, so each op equals "producer -> bf16 -> quant".
+//
+// Every floating-point step is fixed so that the results are reproducible bit for bit on a CPU:
+//  * no fused multiply-add anywhere in this file (the pragma below): each product and sum rounds;
+//  * sums of squares run in a fixed order: a thread adds its groups' squares element by element,
+//    a wave combines by an xor butterfly (32, 16, 8, 4, 2, 1) and the four waves add in order; a
+//    gdn head (16 groups) combines by a 16-lane xor butterfly (8, 4, 2, 1);
+//  * 1/sqrt is a correctly rounded square root and a correctly rounded division;
+//  * exp is exp_f32 below: Cody-Waite reduction by ln 2 (Cody and Waite, "Software Manual for the
+//    Elementary Functions", 1980; ln 2 split into a 16-bit head and a tail) and the degree-7
+//    Taylor polynomial of e^r on |r| <= ln2 / 2 by Horner, then an exact scaling by 2^n.
+#pragma clang fp contract(off)
+
+#include "w4a8_fp8.h"
+
+namespace w4a8 {
+namespace {
+
+using namespace fp8;
+
+constexpr float kLog2e = 0x1.715476p+0f;         // fl32(log2 e)
+constexpr float kLn2Hi = 0x1.62e4p-1f;            // 16 significant bits: n * kLn2Hi is exact
+constexpr float kLn2Lo = 0x1.7f7d1cp-20f;         // ln 2 - kLn2Hi, rounded to fp32
+constexpr float kExpHi = 0x1.62e43p+6f;           // 88.7228394: above, e^y overflows fp32
+constexpr float kExpLo = -0x1.9fe368p+6f;         // fl32(-150 ln 2): below, e^y rounds to +0
+
+__device__ __forceinline__ float exp_f32(float y) {
+  if (y != y) return y;
+  if (y > kExpHi) return __builtin_inff();
+  if (y < kExpLo) return 0.0f;
+  const float n = rintf(y * kLog2e);
+  const float r = (y - n * kLn2Hi) - n * kLn2Lo;
+  float p = 0x1.a01a02p-13f;                      // 1/k!, k = 7 .. 2, rounded to fp32
+  p = p * r + 0x1.6c16c2p-10f;
+  p = p * r + 0x1.111112p-7f;
+  p = p * r + 0x1.555556p-5f;
+  p = p * r + 0x1.555556p-3f;
+  p = p * r + 0.5f;
+  p = p * r + 1.0f;
+  p = p * r + 1.0f;
+  return ldexpf(p, (int)n);
+}
+
+__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + exp_f32(-x)); }
+
+__device__ __forceinline__ float bf16_round(float x) {
+  return __uint_as_float(f32_to_bf16(x) << 16);
+}
+
+__device__ __forceinline__ void unpack8(const uint4 v, float (&f)[8]) {
+  f[0] = __uint_as_float(v.x << 16); f[1] = __uint_as_float(v.x & 0xFFFF0000u);
+  f[2] = __uint_as_float(v.y << 16); f[3] = __uint_as_float(v.y & 0xFFFF0000u);
+  f[4] = __uint_as_float(v.z << 16); f[5] = __uint_as_float(v.z & 0xFFFF0000u);
+  f[6] = __uint_as_float(v.w << 16); f[7] = __uint_as_float(v.w & 0xFFFF0000u);
+}
+
+__device__ __forceinline__ uint4 pack8(const float (&f)[8]) {
+  return make_uint4(f32_to_bf16(f[0]) | (f32_to_bf16(f[1]) << 16),
+                    f32_to_bf16(f[2]) | (f32_to_bf16(f[3]) << 16),
+                    f32_to_bf16(f[4]) | (f32_to_bf16(f[5]) << 16),
+                    f32_to_bf16(f[6]) | (f32_to_bf16(f[7]) << 16));
+}
+
+// Row sum over the workgroup in the fixed order (every thread gets the result).
+__device__ __forceinline__ float block_sum_fixed(float v) {
+  __shared__ float red[kThreads / 64];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float t = red[0];
+#pragma unroll
+  for (int w = 1; w < kThreads / 64; ++w) t = t + red[w];
+  return t;
+}
+
+// The quantization tail: bf16 groups nb[] of this row -> scale[row], q row.
+template <int G>
+__device__ __forceinline__ void quant_tail(const uint4 (&nb)[G], int nv, uint8_t* __restrict__ q,
+                                           float* __restrict__ scale, int row) {
+  const int tid = threadIdx.x;
+  uint32_t am = 0;
+#pragma unroll
+  for (int i = 0; i < G; ++i)
+    if (tid + i * kThreads < nv) am = max(am, abs_bits_max8(nb[i]));
+  const float sc = row_scale(block_max(am));
+  if (tid == 0) scale[row] = sc;
+  uint2* qr = reinterpret_cast<uint2*>(q + (size_t)row * nv * 8);
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int g = tid + i * kThreads;
+    if (g < nv) qr[g] = quant8_any_scale(nb[i], sc);
+  }
+}
+
+// Gemma RMSNorm with residual: v = y + res (fp32); res_out = bf16(v);
+// n = bf16((v * (1 / sqrt(sum(v^2) / K + eps))) * (w + 1)).
+template <int G>
+__global__ __launch_bounds__(kThreads) void add_rms_quant(
+    const uint4* __restrict__ y, const uint4* __restrict__ res, const uint4* __restrict__ w,
+    uint8_t* __restrict__ q, float* __restrict__ scale, uint4* __restrict__ res_out, int K,
+    float eps) {
+  const int row = blockIdx.x, tid = threadIdx.x, nv = K >> 3;
+  y += (size_t)row * nv;
+  res += (size_t)row * nv;
+  res_out += (size_t)row * nv;
+  float v[G][8];
+  float part = 0.0f;
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int g = tid + i * kThreads;
+    if (g < nv) {
+      float a[8], b[8];
+      unpack8(y[g], a);
+      unpack8(res[g], b);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        v[i][j] = a[j] + b[j];
+        part = part + v[i][j] * v[i][j];
+      }
+      res_out[g] = pack8(v[i]);
+    }
+  }
+  const float inv = 1.0f / sqrtf(block_sum_fixed(part) / (float)K + eps);
+  uint4 nb[G];
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int g = tid + i * kThreads;
+    if (g < nv) {
+      float wf[8], n[8];
+      unpack8(w[g], wf);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) n[j] = (v[i][j] * inv) * (wf[j] + 1.0f);
+      nb[i] = pack8(n);
+    }
+  }
+  quant_tail<G>(nb, nv, q, scale, row);
+}
+
+// SiLU-and-mul: gate_up [M, 2N] -> bf16(bf16(silu(gate)) * up).
+template <int G>
+__global__ __launch_bounds__(kThreads) void silu_mul_quant(const uint4* __restrict__ gu,
+                                                          uint8_t* __restrict__ q,
+                                                          float* __restrict__ scale, int N) {
+  const int row = blockIdx.x, tid = threadIdx.x, nv = N >> 3;
+  const uint4* gate = gu + (size_t)row * 2 * nv;
+  const uint4* up = gate + nv;
+  uint4 nb[G];
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int g = tid + i * kThreads;
+    if (g < nv) {
+      float a[8], b[8], p[8];
+      unpack8(gate[g], a);
+      unpack8(up[g], b);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) p[j] = bf16_round(silu_f32(a[j])) * b[j];
+      nb[i] = pack8(p);
+    }
+  }
+  quant_tail<G>(nb, nv, q, scale, row);
+}
+
+// Per-head gated RMSNorm (head = 128 = 16 groups; norm before the gate, weight without +1):
+// n = bf16(((x * (1 / sqrt(sum_head(x^2) / 128 + eps))) * w) * silu(z)).
+template <int G>
+__global__ __launch_bounds__(kThreads) void gdn_norm_quant(
+    const uint4* __restrict__ x, const uint16_t* __restrict__ z, long zs,
+    const uint4* __restrict__ w, uint8_t* __restrict__ q, float* __restrict__ scale, int N,
+    float eps) {
+  const int row = blockIdx.x, tid = threadIdx.x, nv = N >> 3;
+  x += (size_t)row * nv;
+  const uint4* zr = reinterpret_cast<const uint4*>(z + (size_t)row * zs);
+  uint4 nb[G];
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int g = tid + i * kThreads;
+    const bool in = g < nv;                      // whole 16-lane heads are in or out together
+    float v[8];
+    unpack8(in ? x[g] : make_uint4(0, 0, 0, 0), v);
+    float part = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) part = part + v[j] * v[j];
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) part = part + __shfl_xor(part, o, 16);
+    if (in) {
+      const float inv = 1.0f / sqrtf(part * (1.0f / 128.0f) + eps);
+      float zz[8], wf[8], n[8];
+      unpack8(zr[g], zz);
+      unpack8(w[g & 15], wf);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) n[j] = ((v[j] * inv) * wf[j]) * silu_f32(zz[j]);
+      nb[i] = pack8(n);
+    }
+  }
+  quant_tail<G>(nb, nv, q, scale, row);
+}
+
+}  // namespace
+
+hipError_t launch_add_rms_quant(const void* y, const void* res, const void* w, uint8_t* q,
+                                float* scale, void* res_out, int M, int K, float eps,
+                                hipStream_t stream) {
+  if (M == 0) return hipSuccess;
+  const int G = ceil_div(K >> 3, kThreads);
+#define W4A8_ARQ(C)                                                                             \
+  case C:                                                                                       \
+    hipLaunchKernelGGL(add_rms_quant<C>, dim3(M), dim3(kThreads), 0, stream, (const uint4*)y,   \
+                       (const uint4*)res, (const uint4*)w, q, scale, (uint4*)res_out, K, eps);  \
+    break;
+  switch (G) {
+    W4A8_ARQ(1) W4A8_ARQ(2) W4A8_ARQ(3) W4A8_ARQ(4) W4A8_ARQ(5)
+    default: return hipErrorInvalidValue;
+  }
+#undef W4A8_ARQ
+  return hipGetLastError();
+}
+
+hipError_t launch_silu_mul_quant(const void* gate_up, uint8_t* q, float* scale, int M, int N,
+                                 hipStream_t stream) {
+  if (M == 0) return hipSuccess;
+  const int G = ceil_div(N >> 3, kThreads);
+#define W4A8_SMQ(C)                                                                             \
+  case C:                                                                                       \
+    hipLaunchKernelGGL(silu_mul_quant<C>, dim3(M), dim3(kThreads), 0, stream,                   \
+                       (const uint4*)gate_up, q, scale, N);                                     \
+    break;
+  switch (G) {
+    W4A8_SMQ(1) W4A8_SMQ(2) W4A8_SMQ(3) W4A8_SMQ(4) W4A8_SMQ(5) W4A8_SMQ(6) W4A8_SMQ(7)
+    W4A8_SMQ(8) W4A8_SMQ(9)
+    default: return hipErrorInvalidValue;
+  }
+#undef W4A8_SMQ
+  return hipGetLastError();
+}
+
+hipError_t launch_gdn_norm_quant(const void* x, const void* z, long zs, const void* w, uint8_t* q,
+                                 float* scale, int M, int N, float eps, hipStream_t stream) {
+  if (M == 0) return hipSuccess;
+  const int G = ceil_div(N >> 3, kThreads);
+#define W4A8_GNQ(C)                                                                             \
+  case C:                                                                                       \
+    hipLaunchKernelGGL(gdn_norm_quant<C>, dim3(M), dim3(kThreads), 0, stream, (const uint4*)x,  \
+                       (const uint16_t*)z, zs, (const uint4*)w, q, scale, N, eps);              \
+    break;
+  switch (G) {
+    W4A8_GNQ(1) W4A8_GNQ(2) W4A8_GNQ(3) W4A8_GNQ(4) W4A8_GNQ(5)
+    default: return hipErrorInvalidValue;
+  }
+#undef W4A8_GNQ
+  return hipGetLastError();
+}
+
+}  // namespace w4a8
