@@ -196,6 +196,74 @@ def bench_layer_m1():
                 gbs=round(tot_bytes / (tot_us * 1e-6) / 1e9, 1))
 
 
+class Producer:
+    """Device operands of one fused producer (radiance::add_rms_quant / silu_mul_quant /
+    gdn_norm_quant) with `copies` distinct input sets."""
+
+    def __init__(self, kind, M, N, copies, seed):
+        import torch
+        from vllm_sly_radiance_amd import _native, synthetic
+        self.kind, self.M, self.N, self._native = kind, M, N, _native
+
+        def dev(bits):
+            return torch.from_numpy(bits.view(np.int16)).cuda().view(torch.bfloat16)
+        width = {"add_rms": N, "silu": 2 * N, "gdn": N}[kind]
+        self.w = [dev(synthetic.activations(M, width, seed + i)) for i in range(copies)]
+        self.w2 = [dev(synthetic.activations(M, N, seed + 100 + i)) for i in range(copies)] \
+            if kind in ("add_rms", "gdn") else None
+        nw = 128 if kind == "gdn" else N
+        self.weight = dev(synthetic.activations(1, nw, seed + 200)[0])
+        self.q = torch.empty((M, N), dtype=torch.uint8, device="cuda")
+        self.s = torch.empty((M,), dtype=torch.float32, device="cuda")
+        self.r = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+        torch.cuda.synchronize()
+
+    def bytes(self):
+        M, N = self.M, self.N
+        if self.kind == "add_rms":                       # y, res, weight in; res_out, q, s out
+            return 7 * M * N + 2 * N + 4 * M
+        if self.kind == "silu":                          # gate_up in; q, s out
+            return 5 * M * N + 4 * M
+        return 5 * M * N + 256 + 4 * M                   # x, z, weight in; q, s out
+
+    def launch(self, i, stream):
+        n = self._native
+        if self.kind == "add_rms":
+            n.add_rms_quant(self.w[i].data_ptr(), self.w2[i].data_ptr(), self.weight.data_ptr(),
+                            self.q.data_ptr(), self.s.data_ptr(), self.r.data_ptr(), self.M,
+                            self.N, 1e-6, stream)
+        elif self.kind == "silu":
+            n.silu_mul_quant(self.w[i].data_ptr(), self.q.data_ptr(), self.s.data_ptr(), self.M,
+                             self.N, stream)
+        else:
+            n.gdn_norm_quant(self.w[i].data_ptr(), self.w2[i].data_ptr(), self.N,
+                             self.weight.data_ptr(), self.q.data_ptr(), self.s.data_ptr(), self.M,
+                             self.N, 1e-6, stream)
+
+
+# (op, width) at the benchmark model's shapes: the decoder norms feed K = 5120, the MLP activation
+# N = 17408, the GatedDeltaNet output projection N = 6144 (48 heads of 128)
+PRODUCERS = [("add_rms", 5120), ("silu", 17408), ("gdn", 6144)]
+
+
+def bench_producers():
+    import torch
+    res = []
+    for M in (8, 4096):
+        for kind, N in PRODUCERS:
+            per_copy = 4 * M * N                         # bf16 input bytes per launch
+            copies = max(2, min(16, -(-512 * 2 ** 20 // per_copy)))
+            g = Producer(kind, M, N, copies, seed=21)
+            steps, _, sec, _, _ = graph_timed(g, 8 * copies, 2 * copies, warm_seconds=0.2)
+            us = sec / steps * 1e6
+            gbs = g.bytes() / (us * 1e-6) / 1e9
+            res.append(dict(op=kind, M=M, N=N, us=round(us, 2), gbs=round(gbs, 1),
+                            frac=round(gbs / HBM_PEAK_GBS, 4)))
+            del g
+            torch.cuda.empty_cache()
+    return res
+
+
 def mfma_probe():
     """Register-resident rate of the scaled MFMA the GEMMs issue (fp4 A x fp8 B), both shapes."""
     import torch
@@ -461,12 +529,14 @@ def main():
     print(f"[bench] verify M=8: {v['kernel_us']:.2f} us/launch in the graph-timed region, "
           f"event pairs {v['event_pair_us_median']:.2f} us median, plan {v['plan']}",
           file=sys.stderr, flush=True)
-    prefill = layer = None
+    prefill = layer = producers = None
     if not args.only_verify:
         prefill = bench_prefill()
         print(f"[bench] prefill: {prefill}", file=sys.stderr, flush=True)
         layer = bench_layer_m1()
         print(f"[bench] M=1 layer: {layer}", file=sys.stderr, flush=True)
+        producers = bench_producers()
+        print(f"[bench] producers: {producers}", file=sys.stderr, flush=True)
     probe = mfma_probe()
     print(f"[bench] MFMA probe TFLOP/s: {probe}", file=sys.stderr, flush=True)
     cpu = None if args.no_cpu else cpu_baseline()
@@ -497,6 +567,7 @@ def main():
         "prefill_m4096": prefill,
         "mfma_probe_tflops": probe,
         "decode_m1_layer": layer,
+        "producers": producers,
     }
     print(json.dumps(line), flush=True)
 

@@ -102,8 +102,9 @@ def gpu_silu(gu):
     return host_u8(q), s.cpu().numpy()
 
 
+# M <= 128 runs 1024-thread rows, larger M 256-thread rows: both must give the same bits
 @pytest.mark.parametrize("M,N", [(1, 17408), (8, 17408), (33, 1000), (2, 18432), (96, 8704),
-                                 (4, 8)])
+                                 (4, 8), (200, 17408), (129, 18432)])
 def test_silu_mul_quant_bit_exact(gpu_lib, M, N):
     gu = synthetic.activations(M, 2 * N, seed=M * 3 + N)
     q, s = gpu_silu(gu)
@@ -137,7 +138,8 @@ def gpu_gdn(x, z_wide, col0, w, eps):
     return host_u8(q), s.cpu().numpy()
 
 
-@pytest.mark.parametrize("M,heads,extra", [(1, 24, 0), (9, 48, 2048), (64, 80, 384), (3, 1, 8)])
+@pytest.mark.parametrize("M,heads,extra", [(1, 24, 0), (9, 48, 2048), (64, 80, 384), (3, 1, 8),
+                                           (160, 48, 128), (130, 80, 0)])
 def test_gdn_norm_quant_bit_exact(gpu_lib, M, heads, extra):
     N = heads * 128
     x = synthetic.activations(M, N, seed=M + heads)

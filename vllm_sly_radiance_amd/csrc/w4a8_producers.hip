@@ -82,21 +82,34 @@ __device__ __forceinline__ float block_sum_fixed(float v) {
   return t;
 }
 
-// The quantization tail: bf16 groups nb[] of this row -> scale[row], q row.
-template <int G>
+// Row max over a T-thread workgroup (every thread gets the result); max is exact in any order.
+template <int T>
+__device__ __forceinline__ uint32_t block_max_t(uint32_t v) {
+  __shared__ uint32_t red[T / 64];
+  v = wave_max(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  uint32_t m = red[0];
+#pragma unroll
+  for (int w = 1; w < T / 64; ++w) m = max(m, red[w]);
+  return m;
+}
+
+// The quantization tail: bf16 groups nb[] (group g = tid + i T) of this row -> scale[row], q row.
+template <int G, int T>
 __device__ __forceinline__ void quant_tail(const uint4 (&nb)[G], int nv, uint8_t* __restrict__ q,
                                            float* __restrict__ scale, int row) {
   const int tid = threadIdx.x;
   uint32_t am = 0;
 #pragma unroll
   for (int i = 0; i < G; ++i)
-    if (tid + i * kThreads < nv) am = max(am, abs_bits_max8(nb[i]));
-  const float sc = row_scale(block_max(am));
+    if (tid + i * T < nv) am = max(am, abs_bits_max8(nb[i]));
+  const float sc = row_scale(block_max_t<T>(am));
   if (tid == 0) scale[row] = sc;
   uint2* qr = reinterpret_cast<uint2*>(q + (size_t)row * nv * 8);
 #pragma unroll
   for (int i = 0; i < G; ++i) {
-    const int g = tid + i * kThreads;
+    const int g = tid + i * T;
     if (g < nv) qr[g] = quant8_any_scale(nb[i], sc);
   }
 }
@@ -142,21 +155,22 @@ __global__ __launch_bounds__(kThreads) void add_rms_quant(
       nb[i] = pack8(n);
     }
   }
-  quant_tail<G>(nb, nv, q, scale, row);
+  quant_tail<G, kThreads>(nb, nv, q, scale, row);
 }
 
-// SiLU-and-mul: gate_up [M, 2N] -> bf16(bf16(silu(gate)) * up).
-template <int G>
-__global__ __launch_bounds__(kThreads) void silu_mul_quant(const uint4* __restrict__ gu,
-                                                          uint8_t* __restrict__ q,
-                                                          float* __restrict__ scale, int N) {
+// SiLU-and-mul: gate_up [M, 2N] -> bf16(bf16(silu(gate)) * up). T threads per row: the only
+// reduction is the amax, so any T gives the same bits; short rows of work (small M) take 1024.
+template <int G, int T>
+__global__ __launch_bounds__(T) void silu_mul_quant(const uint4* __restrict__ gu,
+                                                    uint8_t* __restrict__ q,
+                                                    float* __restrict__ scale, int N) {
   const int row = blockIdx.x, tid = threadIdx.x, nv = N >> 3;
   const uint4* gate = gu + (size_t)row * 2 * nv;
   const uint4* up = gate + nv;
   uint4 nb[G];
 #pragma unroll
   for (int i = 0; i < G; ++i) {
-    const int g = tid + i * kThreads;
+    const int g = tid + i * T;
     if (g < nv) {
       float a[8], b[8], p[8];
       unpack8(gate[g], a);
@@ -166,13 +180,15 @@ __global__ __launch_bounds__(kThreads) void silu_mul_quant(const uint4* __restri
       nb[i] = pack8(p);
     }
   }
-  quant_tail<G>(nb, nv, q, scale, row);
+  quant_tail<G, T>(nb, nv, q, scale, row);
 }
 
 // Per-head gated RMSNorm (head = 128 = 16 groups; norm before the gate, weight without +1):
-// n = bf16(((x * (1 / sqrt(sum_head(x^2) / 128 + eps))) * w) * silu(z)).
-template <int G>
-__global__ __launch_bounds__(kThreads) void gdn_norm_quant(
+// n = bf16(((x * (1 / sqrt(sum_head(x^2) / 128 + eps))) * w) * silu(z)). The head sums stay
+// inside 16 lanes and the row reduction is the amax, so any T (a multiple of 64) gives the same
+// bits.
+template <int G, int T>
+__global__ __launch_bounds__(T) void gdn_norm_quant(
     const uint4* __restrict__ x, const uint16_t* __restrict__ z, long zs,
     const uint4* __restrict__ w, uint8_t* __restrict__ q, float* __restrict__ scale, int N,
     float eps) {
@@ -182,7 +198,7 @@ __global__ __launch_bounds__(kThreads) void gdn_norm_quant(
   uint4 nb[G];
 #pragma unroll
   for (int i = 0; i < G; ++i) {
-    const int g = tid + i * kThreads;
+    const int g = tid + i * T;
     const bool in = g < nv;                      // whole 16-lane heads are in or out together
     float v[8];
     unpack8(in ? x[g] : make_uint4(0, 0, 0, 0), v);
@@ -201,7 +217,7 @@ __global__ __launch_bounds__(kThreads) void gdn_norm_quant(
       nb[i] = pack8(n);
     }
   }
-  quant_tail<G>(nb, nv, q, scale, row);
+  quant_tail<G, T>(nb, nv, q, scale, row);
 }
 
 }  // namespace
@@ -224,19 +240,31 @@ hipError_t launch_add_rms_quant(const void* y, const void* res, const void* w, u
   return hipGetLastError();
 }
 
+// Rows of work per CU: with fewer rows than half the CUs, each row takes a 1024-thread workgroup.
+constexpr int kWideRowsMax = 128;
+
 hipError_t launch_silu_mul_quant(const void* gate_up, uint8_t* q, float* scale, int M, int N,
                                  hipStream_t stream) {
   if (M == 0) return hipSuccess;
-  const int G = ceil_div(N >> 3, kThreads);
-#define W4A8_SMQ(C)                                                                             \
+  const bool wide = M <= kWideRowsMax;
+  const int T = wide ? 1024 : kThreads;
+  const int G = ceil_div(N >> 3, T);
+#define W4A8_SMQ(C, TT)                                                                         \
   case C:                                                                                       \
-    hipLaunchKernelGGL(silu_mul_quant<C>, dim3(M), dim3(kThreads), 0, stream,                   \
+    hipLaunchKernelGGL((silu_mul_quant<C, TT>), dim3(M), dim3(TT), 0, stream,                   \
                        (const uint4*)gate_up, q, scale, N);                                     \
     break;
-  switch (G) {
-    W4A8_SMQ(1) W4A8_SMQ(2) W4A8_SMQ(3) W4A8_SMQ(4) W4A8_SMQ(5) W4A8_SMQ(6) W4A8_SMQ(7)
-    W4A8_SMQ(8) W4A8_SMQ(9)
-    default: return hipErrorInvalidValue;
+  if (wide) {
+    switch (G) {
+      W4A8_SMQ(1, 1024) W4A8_SMQ(2, 1024) W4A8_SMQ(3, 1024)
+      default: return hipErrorInvalidValue;
+    }
+  } else {
+    switch (G) {
+      W4A8_SMQ(1, 256) W4A8_SMQ(2, 256) W4A8_SMQ(3, 256) W4A8_SMQ(4, 256) W4A8_SMQ(5, 256)
+      W4A8_SMQ(6, 256) W4A8_SMQ(7, 256) W4A8_SMQ(8, 256) W4A8_SMQ(9, 256)
+      default: return hipErrorInvalidValue;
+    }
   }
 #undef W4A8_SMQ
   return hipGetLastError();
@@ -245,15 +273,24 @@ hipError_t launch_silu_mul_quant(const void* gate_up, uint8_t* q, float* scale, 
 hipError_t launch_gdn_norm_quant(const void* x, const void* z, long zs, const void* w, uint8_t* q,
                                  float* scale, int M, int N, float eps, hipStream_t stream) {
   if (M == 0) return hipSuccess;
-  const int G = ceil_div(N >> 3, kThreads);
-#define W4A8_GNQ(C)                                                                             \
+  const bool wide = M <= kWideRowsMax;
+  const int T = wide ? 1024 : kThreads;
+  const int G = ceil_div(N >> 3, T);
+#define W4A8_GNQ(C, TT)                                                                         \
   case C:                                                                                       \
-    hipLaunchKernelGGL(gdn_norm_quant<C>, dim3(M), dim3(kThreads), 0, stream, (const uint4*)x,  \
+    hipLaunchKernelGGL((gdn_norm_quant<C, TT>), dim3(M), dim3(TT), 0, stream, (const uint4*)x,  \
                        (const uint16_t*)z, zs, (const uint4*)w, q, scale, N, eps);              \
     break;
-  switch (G) {
-    W4A8_GNQ(1) W4A8_GNQ(2) W4A8_GNQ(3) W4A8_GNQ(4) W4A8_GNQ(5)
-    default: return hipErrorInvalidValue;
+  if (wide) {
+    switch (G) {
+      W4A8_GNQ(1, 1024) W4A8_GNQ(2, 1024)
+      default: return hipErrorInvalidValue;
+    }
+  } else {
+    switch (G) {
+      W4A8_GNQ(1, 256) W4A8_GNQ(2, 256) W4A8_GNQ(3, 256) W4A8_GNQ(4, 256) W4A8_GNQ(5, 256)
+      default: return hipErrorInvalidValue;
+    }
   }
 #undef W4A8_GNQ
   return hipGetLastError();
