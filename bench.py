@@ -461,8 +461,9 @@ CALIBRATION_BYTES = 256 * 2 ** 20
 
 def profile_workload():
     """The launches the committed rocprofv3 summaries are taken on: the verify GEMM (the bench's
-    graph replay: 16 warmup + 64 timed launches over 16 weight copies, plus 64 event-bracketed
-    single launches), each prefill GEMM (4 launches) and a plain 256 MiB device copy
+    graph replay: one second of warmup replays, then 64 timed launches over 16 weight copies,
+    plus 64 event-bracketed single launches), each prefill GEMM (4 launches), each fused
+    producer at M = 4096 (4 launches over 2 input copies) and a plain 256 MiB device copy
     (torch's copy kernel), whose FETCH_SIZE / WRITE_SIZE readings calibrate the counters: a copy
     of B bytes fetches B and writes B."""
     import torch
@@ -475,6 +476,12 @@ def profile_workload():
     del g
     for _, M, N, K in PREFILL:
         g = Gemm(M, N, K, 2, seed=7)
+        for i in range(4):
+            g.launch(i % 2, st.cuda_stream)
+        torch.cuda.synchronize()
+        del g
+    for kind, N in PRODUCERS:                      # the fused producers at M = 4096
+        g = Producer(kind, 4096, N, 2, seed=21)
         for i in range(4):
             g.launch(i % 2, st.cuda_stream)
         torch.cuda.synchronize()
