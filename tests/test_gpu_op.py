@@ -111,3 +111,38 @@ def test_hip_graph_capture_and_replay(kernel):
         torch.cuda.synchronize()
         assert torch.equal(y, eager), f"replay {i}"
         _ = (x.float() * 2).sum().item()          # unrelated eager work between replays
+
+
+def test_checkpoint_ingestion_end_to_end(kernel, tmp_path):
+    """A merged gate/up linear read from a sharded safetensors checkpoint, repacked in place by
+    process_weights_after_loading and applied: equal to the oracle on the concatenated tensors."""
+    import json
+    import os
+
+    from safetensors.torch import save_file
+
+    from vllm_sly_radiance_amd import checkpoint as CK
+    K = 1024
+    g, gs = synthetic.weights(96, K, 11)
+    u, us = synthetic.weights(64, K, 12)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a))
+    save_file({"l.gate_proj.weight_packed": t(g), "l.gate_proj.weight_scale": t(gs)},
+              os.path.join(tmp_path, "a.safetensors"))
+    save_file({"l.up_proj.weight_packed": t(u), "l.up_proj.weight_scale": t(us)},
+              os.path.join(tmp_path, "b.safetensors"))
+    with open(os.path.join(tmp_path, "model.safetensors.index.json"), "w") as f:
+        json.dump({"weight_map": {"l.gate_proj.weight_packed": "a.safetensors",
+                                  "l.gate_proj.weight_scale": "a.safetensors",
+                                  "l.up_proj.weight_packed": "b.safetensors",
+                                  "l.up_proj.weight_scale": "b.safetensors"}}, f)
+    layer = torch.nn.Module()
+    CK.load_linear(layer, CK.CheckpointIndex(str(tmp_path)), "l", ["gate_proj", "up_proj"])
+    storage = layer.weight.data_ptr()
+    kernel.process_weights_after_loading(layer)
+    assert layer.weight.data_ptr() == storage                    # repacked in the same storage
+    M = 8
+    x = synthetic.activations(M, K, 13)
+    y = kernel.apply_weights(layer, bf16_dev(x))
+    w, ws = np.concatenate([g, u], 0), np.concatenate([gs, us], 0)
+    q, s = O.quant_per_token(x)
+    assert_gemm_close(host_u16(y), q, s, w, ws, "checkpoint gate_up M=8")
