@@ -248,6 +248,8 @@ PRODUCERS = [("add_rms", 5120), ("silu", 17408), ("gdn", 6144)]
 
 def bench_producers():
     import torch
+    from vllm_sly_radiance_amd import radiance_mxfp4 as R
+    R.ensure_scratch("cuda")          # as after the plugin's first layer: silu splits small-M rows
     res = []
     for M in (8, 4096):
         for kind, N in PRODUCERS:

@@ -19,6 +19,19 @@ def stream():
     return torch.cuda.current_stream().cuda_stream
 
 
+@pytest.fixture(params=["one_workgroup_per_row", "split_rows"])
+def producer_path(request, gpu_lib):
+    """silu_mul splits rows of small M over one-wave workgroups when scratch for the partial
+    maxima is registered; without it, it takes one workgroup per row. Runs a test both ways and
+    leaves the scratch registered."""
+    R.ensure_scratch("cuda")
+    part, cnt = R._scratch
+    if request.param == "one_workgroup_per_row":
+        _native.set_scratch(None, 0, cnt.data_ptr(), cnt.numel() * 4)
+    yield request.param
+    _native.set_scratch(part.data_ptr(), part.numel() * 4, cnt.data_ptr(), cnt.numel() * 4)
+
+
 def weight_bits(K, seed, mean=0.0, sd=0.1):
     return O.f32_to_bf16((mean + np.random.default_rng(seed).standard_normal(K) * sd)
                          .astype(np.float32))
@@ -102,20 +115,22 @@ def gpu_silu(gu):
     return host_u8(q), s.cpu().numpy()
 
 
-# M <= 128 runs 1024-thread rows, larger M 256-thread rows: both must give the same bits
-@pytest.mark.parametrize("M,N", [(1, 17408), (8, 17408), (33, 1000), (2, 18432), (96, 8704),
-                                 (4, 8), (200, 17408), (129, 18432)])
-def test_silu_mul_quant_bit_exact(gpu_lib, M, N):
+# M <= 64 splits rows (with scratch) or runs 1024-thread rows, M <= 128 runs 1024-thread rows,
+# larger M 256-thread rows: all must give the same bits
+@pytest.mark.parametrize("M,N", [(1, 17408), (8, 17408), (33, 1000), (2, 18432), (64, 8704),
+                                 (96, 8704), (4, 8), (200, 17408), (129, 18432), (16, 520)])
+def test_silu_mul_quant_bit_exact(producer_path, M, N):
     gu = synthetic.activations(M, 2 * N, seed=M * 3 + N)
     q, s = gpu_silu(gu)
     oq, os_ = P.silu_mul_quant(gu)
     assert_same_qs(q, s, oq, os_, f"silu M={M} N={N}")
 
 
-def test_silu_mul_quant_special_and_wide_range(gpu_lib):
-    """Gate values across the whole range where exp is exercised (-100 .. 100, inf, NaN)."""
+def test_silu_mul_quant_special_and_wide_range(producer_path):
+    """Gate values across the whole range where exp is exercised (-200 .. 200: overflow, the
+    subnormal results and the clamp, inf, NaN)."""
     N = 2048
-    g = np.linspace(-100.0, 100.0, 3 * N).astype(np.float32).reshape(3, N)
+    g = np.linspace(-200.0, 200.0, 3 * N).astype(np.float32).reshape(3, N)
     g[0, 7], g[1, 9], g[2, 11] = np.inf, -np.inf, np.nan
     u = (np.random.default_rng(1).standard_normal((3, N)) * 2).astype(np.float32)
     gu = np.concatenate([O.f32_to_bf16(g), O.f32_to_bf16(u)], axis=1)
@@ -139,7 +154,7 @@ def gpu_gdn(x, z_wide, col0, w, eps):
 
 
 @pytest.mark.parametrize("M,heads,extra", [(1, 24, 0), (9, 48, 2048), (64, 80, 384), (3, 1, 8),
-                                           (160, 48, 128), (130, 80, 0)])
+                                           (160, 48, 128), (130, 80, 0), (8, 5, 0)])
 def test_gdn_norm_quant_bit_exact(gpu_lib, M, heads, extra):
     N = heads * 128
     x = synthetic.activations(M, N, seed=M + heads)
@@ -148,6 +163,29 @@ def test_gdn_norm_quant_bit_exact(gpu_lib, M, heads, extra):
     q, s = gpu_gdn(x, zw, extra, w, 1e-6)
     oq, os_ = P.gdn_norm_quant(x, zw[:, extra:extra + N], w, 1e-6)
     assert_same_qs(q, s, oq, os_, f"gdn M={M} heads={heads} z offset {extra}")
+
+
+def test_split_rows_equal_one_workgroup_rows(gpu_lib):
+    """The two small-M silu paths on the same device inputs: identical codes and scales, a NaN row
+    included (gate values over the whole exp range)."""
+    R.ensure_scratch("cuda")
+    part, cnt = R._scratch
+    M, N = 8, 17408
+    gu = synthetic.activations(M, 2 * N, seed=21)
+    gu[3, :N] = O.f32_to_bf16(np.linspace(-300, 300, N).astype(np.float32))
+    gu[5, 77] = 0x7FC0                                   # NaN gate: a NaN row scale
+    runs = {}
+    for path in ("split", "one"):
+        if path == "one":
+            _native.set_scratch(None, 0, cnt.data_ptr(), cnt.numel() * 4)
+        try:
+            runs[path] = gpu_silu(gu)
+        finally:
+            _native.set_scratch(part.data_ptr(), part.numel() * 4, cnt.data_ptr(),
+                                cnt.numel() * 4)
+    for a, b in zip(runs["split"], runs["one"]):
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8))
+    assert np.isnan(runs["split"][1][5]) and not np.isnan(runs["split"][1][3])
 
 
 # ---- the custom ops on device tensors, and their hand-off to the GEMM -------------------------
@@ -175,6 +213,41 @@ def test_ops_feed_the_gemm_like_the_unfused_chain(gpu_lib):
     fused2 = torch.ops.radiance.mxfp4_linear_pq(q2, s2, wq2, sq2, wref2)
     unfused2 = torch.ops.radiance.mxfp4_linear(bf16_dev(P.silu_mul(gu)), wq2, sq2, wref2)
     assert torch.equal(fused2, unfused2)
+
+
+def test_producer_ops_capture_into_a_hip_graph(gpu_lib):
+    """The three ops (silu on its split path: two launches through the registered scratch) in one
+    captured graph; every replay, with eager work between, equals the eager results."""
+    R.ensure_scratch("cuda")
+    M, K, N, heads = 8, 5120, 17408, 48
+    y = bf16_dev(synthetic.activations(M, K, seed=31))
+    res = bf16_dev(synthetic.activations(M, K, seed=32))
+    nw = bf16_dev(weight_bits(K, 33))
+    gu = bf16_dev(synthetic.activations(M, 2 * N, seed=34))
+    x = bf16_dev(synthetic.activations(M, heads * 128, seed=35))
+    z = bf16_dev(synthetic.activations(M, heads * 128, seed=36))
+    gw = bf16_dev(weight_bits(128, 37, mean=1.0, sd=0.2))
+
+    def run():
+        return (*torch.ops.radiance.add_rms_quant(y, res, nw, 1e-6),
+                *torch.ops.radiance.silu_mul_quant(gu),
+                *torch.ops.radiance.gdn_norm_quant(x, z, gw, 1e-6))
+    eager = [t.clone() for t in run()]
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = run()
+    for i in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(out, eager):
+            assert torch.equal(a.view(torch.uint8), b.view(torch.uint8)), f"replay {i}"
+        _ = (gu.float() * 2).sum().item()         # unrelated eager work between replays
 
 
 def test_gdn_op_takes_a_column_slice_of_z(gpu_lib):

@@ -430,9 +430,12 @@ W4A8_API int w4a8_silu_mul_quant(const void* gate_up, void* q, float* scale, int
   if (!aligned(gate_up, 16) || !aligned(q, 8) || !aligned(scale, 4))
     return fail(W4A8_EINVAL,
                 "w4a8_silu_mul_quant: gate_up needs 16-byte alignment, q 8-byte, scale 4-byte");
-  return hip_status(
-      launch_silu_mul_quant(gate_up, (uint8_t*)q, scale, M, N, (hipStream_t)stream),
-      "w4a8_silu_mul_quant");
+  const int dev = current_device();
+  void* part = dev >= 0 ? (void*)g_scratch[dev].partial : nullptr;
+  const size_t part_bytes = dev >= 0 ? g_scratch[dev].partial_bytes : 0;
+  return hip_status(launch_silu_mul_quant(gate_up, (uint8_t*)q, scale, M, N, part, part_bytes,
+                                          (hipStream_t)stream),
+                    "w4a8_silu_mul_quant");
 }
 
 W4A8_API int w4a8_gdn_norm_quant(const void* x, const void* z, long z_stride, const void* weight,

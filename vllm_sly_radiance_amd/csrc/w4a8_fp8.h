@@ -1,10 +1,18 @@
 // Per-token e4m3 quantization of bf16 rows held in registers, shared by the quantizer and the
 // fused producers. Semantics: s = max(amax(|x|) * fl32(1/448), 1/(448*512)) (a NaN in the row
-// propagates to s); q = e4m3_rne(clamp(x / s, -448, 448)) with IEEE-correct fp32 division. One
+// propagates to s); q = e4m3_rne(clamp(x / s, -448, 448)) with the IEEE fp32 quotient x / s. One
 // 256-thread workgroup (4 wave64) per row; the amax runs on the bf16 bit patterns (|x| bits =
 // x & 0x7FFF), which is exact, orders like the magnitudes and ranks NaN above inf. Codes come
 // from the hardware e4m3 converter (v_cvt_pk_fp8_f32, round to nearest even) on clamped inputs;
 // rows whose scale is not finite take a per-element path that maps NaN quotients to 0x7F.
+//
+// Rows with a finite scale divide by Markstein's correction (P. Markstein, "Computation of
+// elementary functions on the IBM RISC System/6000 processor", IBM J. Res. Dev. 34(1), 1990):
+// y = 1/s once per row (IEEE division), then per element q0 = x*y, r = fma(-s, q0, x) and
+// q = fma(r, y, q0) with the sign of x: three operations instead of a full division. Over every
+// finite row amax and every bf16 x with |x| <= amax (both signs, 1.07e9 pairs) the result equals
+// the IEEE quotient except for quotients below 2^-12, where both round to the same signed zero in
+// e4m3 (tests/test_markstein_cpu.py runs that exhaustive check).
 #pragma once
 #include "w4a8_internal.h"
 
@@ -60,16 +68,33 @@ __device__ __forceinline__ uint32_t pack4_any(float a, float b, float c, float d
   return code1(a) | (code1(b) << 8) | (code1(c) << 16) | (code1(d) << 24);
 }
 
-template <bool kFinite>
-__device__ __forceinline__ uint32_t quant_dword(uint32_t d0, uint32_t d1, float s) {
-  const float a = clamp448(lo_bf16(d0) / s), b = clamp448(hi_bf16(d0) / s);
-  const float c = clamp448(lo_bf16(d1) / s), d = clamp448(hi_bf16(d1) / s);
-  return kFinite ? pack4(a, b, c, d) : pack4_any(a, b, c, d);
+// x / s for a finite s > 0 and y = 1/s (Markstein's correction; see the file header)
+__device__ __forceinline__ float div_rcp(float x, float s, float y) {
+  const float q0 = x * y;
+  const float r = __builtin_fmaf(-s, q0, x);
+  return __builtin_copysignf(__builtin_fmaf(r, y, q0), x);
 }
 
-template <bool kFinite>
-__device__ __forceinline__ uint2 quant8(const uint4 v, float s) {
-  return make_uint2(quant_dword<kFinite>(v.x, v.y, s), quant_dword<kFinite>(v.z, v.w, s));
+__device__ __forceinline__ uint32_t quant_dword(uint32_t d0, uint32_t d1, float s, float y) {
+  const float a = clamp448(div_rcp(lo_bf16(d0), s, y)), b = clamp448(div_rcp(hi_bf16(d0), s, y));
+  const float c = clamp448(div_rcp(lo_bf16(d1), s, y)), d = clamp448(div_rcp(hi_bf16(d1), s, y));
+  return pack4(a, b, c, d);
+}
+
+// non-finite s: IEEE division per element, NaN quotients to the canonical code
+__device__ __forceinline__ uint32_t quant_dword_any(uint32_t d0, uint32_t d1, float s) {
+  const float a = clamp448(lo_bf16(d0) / s), b = clamp448(hi_bf16(d0) / s);
+  const float c = clamp448(lo_bf16(d1) / s), d = clamp448(hi_bf16(d1) / s);
+  return pack4_any(a, b, c, d);
+}
+
+// 8 bf16 values (one 16-byte group) -> 8 e4m3 codes, finite s with y = 1/s
+__device__ __forceinline__ uint2 quant8(const uint4 v, float s, float y) {
+  return make_uint2(quant_dword(v.x, v.y, s, y), quant_dword(v.z, v.w, s, y));
+}
+
+__device__ __forceinline__ uint2 quant8_any(const uint4 v, float s) {
+  return make_uint2(quant_dword_any(v.x, v.y, s), quant_dword_any(v.z, v.w, s));
 }
 
 __device__ __forceinline__ float row_scale(uint32_t amax_bits) {
@@ -81,9 +106,9 @@ __device__ __forceinline__ bool finite(float s) {
   return (__float_as_uint(s) & 0x7F800000u) != 0x7F800000u;
 }
 
-// 8 bf16 values (one 16-byte group) -> 8 e4m3 codes
-__device__ __forceinline__ uint2 quant8_any_scale(const uint4 v, float s) {
-  return finite(s) ? quant8<true>(v, s) : quant8<false>(v, s);
+// 8 bf16 values -> 8 e4m3 codes for any s; y = 1/s (used only when s is finite)
+__device__ __forceinline__ uint2 quant8_any_scale(const uint4 v, float s, float y) {
+  return finite(s) ? quant8(v, s, y) : quant8_any(v, s);
 }
 
 }  // namespace fp8

@@ -38,7 +38,6 @@ __global__ __launch_bounds__(W * 64) void gemm_stream(
     const uint32_t* __restrict__ Sq, uint16_t* __restrict__ C, int M, int N, int K, int KT,
     int KG, int NTILES, int vec_out) {
   static_assert(KPW % 4 == 0 && NT >= 1 && W >= 1 && W <= 16, "stream variant");
-  constexpr int kOut = 0x7FFFFFF0;               // an offset past every buffer resource here
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   // Wave-uniform work selection in scalar registers; 32-bit products only (the host bounds them).

@@ -51,6 +51,16 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
   return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
+// The same with a select instead of a branch: two more VALU operations, no exec-mask branching.
+// Cheaper where a SIMD runs one or two waves (nothing hides the scalar branch work); the branch
+// form is cheaper in VALU-bound code with many waves per SIMD.
+__device__ __forceinline__ uint32_t f32_to_bf16_sel(float f) {
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rne = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t nan = ((u >> 16) & 0x8000u) | 0x7FC0u;
+  return (u & 0x7FFFFFFFu) > 0x7F800000u ? nan : rne;
+}
+
 // Word 3 of a raw (stride 0) buffer resource on gfx9-family GPUs: 32-bit data format, no swizzle.
 // Loads through such a resource return 0 for offsets at or past num_records, without a memory access.
 constexpr int kBufferWord3 = 0x00020000;
@@ -106,8 +116,11 @@ hipError_t launch_repack(const uint8_t* w, const uint8_t* ws, uint8_t* wq, uint3
 hipError_t launch_add_rms_quant(const void* y, const void* res, const void* w, uint8_t* q,
                                 float* scale, void* res_out, int M, int K, float eps,
                                 hipStream_t stream);
+// silu_mul splits rows of small M over several workgroups when `part` (the registered scratch)
+// holds producer_split_bytes(M, N); otherwise one workgroup per row. Same bits either way.
+size_t producer_split_bytes(int M, int N);
 hipError_t launch_silu_mul_quant(const void* gate_up, uint8_t* q, float* scale, int M, int N,
-                                 hipStream_t stream);
+                                 void* part, size_t part_bytes, hipStream_t stream);
 hipError_t launch_gdn_norm_quant(const void* x, const void* z, long zs, const void* w, uint8_t* q,
                                  float* scale, int M, int N, float eps, hipStream_t stream);
 

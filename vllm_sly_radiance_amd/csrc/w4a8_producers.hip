@@ -3,13 +3,17 @@
 //
 // Counterparts of the reference's radiance_add_rms_quant, radiance_silu_mul_quant and
 // radiance_gdn_norm_quant (sly/mxfp4/radiance_mxfp4_fp8.hip:1834-2156; ops and call sites in
-// sly/mxfp4/radiance_fused_norm.py:132-304). One 256-thread workgroup per row; thread t owns the
-// row's 8-element groups t, t + 256, ..., read once as 16-byte vectors and kept in registers
-// through the reductions. The quantization tail is the one of the plain quantizer (w4a8_fp8.h),
-// applied to the bf16-rounded producer output, so each op equals "producer -> bf16 -> quant".
+// sly/mxfp4/radiance_fused_norm.py:132-304). One workgroup per row (256 threads; 1024 for silu
+// and gdn at up to 128 rows); thread t owns the row's 8-element groups t, t + T, ..., read once as
+// 16-byte vectors and kept in registers through the reductions. With few rows and registered
+// scratch, silu splits each row over one-wave workgroups instead (below). The quantization tail
+// is the one of the plain quantizer (w4a8_fp8.h), applied to the bf16-rounded producer output, so
+// each op equals "producer -> bf16 -> quant".
 //
 // Every floating-point step is fixed so that the results are reproducible bit for bit on a CPU:
-//  * no fused multiply-add anywhere in this file (the pragma below): each product and sum rounds;
+//  * no contracted multiply-add (the pragma below): each product and sum rounds; the only fused
+//    multiply-adds are the explicit ones of the quantizer's division (w4a8_fp8.h), whose codes
+//    equal those of the IEEE quotient;
 //  * sums of squares run in a fixed order: a thread adds its groups' squares element by element,
 //    a wave combines by an xor butterfly (32, 16, 8, 4, 2, 1) and the four waves add in order; a
 //    gdn head (16 groups) combines by a 16-lane xor butterfly (8, 4, 2, 1);
@@ -31,11 +35,15 @@ constexpr float kLn2Hi = 0x1.62e4p-1f;            // 16 significant bits: n * kL
 constexpr float kLn2Lo = 0x1.7f7d1cp-20f;         // ln 2 - kLn2Hi, rounded to fp32
 constexpr float kExpHi = 0x1.62e43p+6f;           // 88.7228394: above, e^y overflows fp32
 constexpr float kExpLo = -0x1.9fe368p+6f;         // fl32(-150 ln 2): below, e^y rounds to +0
+static_assert(kExpHi < 89.0f && kExpLo > -104.0f, "exp_f32's clamp must bracket its range");
 
-__device__ __forceinline__ float exp_f32(float y) {
-  if (y != y) return y;
-  if (y > kExpHi) return __builtin_inff();
-  if (y < kExpLo) return 0.0f;
+// e^y for y in [kExpLo, kExpHi] as described above; NaN stays NaN, above kExpHi it is +inf and
+// below kExpLo +0. Branch-free: y is first clamped to [-104, 89], where the same steps already
+// give +inf at and above kExpHi (n = 128 and e^r > 1) and +0 below kExpLo (p * 2^-150 < 2^-150
+// rounds to zero); a NaN is put back at the end. Over all 2^32 inputs this equals the branching
+// form bit for bit (checked on the CPU with the same operations).
+__device__ __forceinline__ float exp_f32(float y_in) {
+  const float y = fminf(fmaxf(y_in, -104.0f), 89.0f);
   const float n = rintf(y * kLog2e);
   const float r = (y - n * kLn2Hi) - n * kLn2Lo;
   float p = 0x1.a01a02p-13f;                      // 1/k!, k = 7 .. 2, rounded to fp32
@@ -46,13 +54,21 @@ __device__ __forceinline__ float exp_f32(float y) {
   p = p * r + 0.5f;
   p = p * r + 1.0f;
   p = p * r + 1.0f;
-  return ldexpf(p, (int)n);
+  const float e = ldexpf(p, (int)n);
+  return y_in != y_in ? y_in : e;
 }
 
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + exp_f32(-x)); }
 
+// kSel: round to bf16 with a select rather than a branch (kernels with one wave per SIMD)
+template <bool kSel>
+__device__ __forceinline__ uint32_t to_bf16(float x) {
+  return kSel ? f32_to_bf16_sel(x) : f32_to_bf16(x);
+}
+
+template <bool kSel>
 __device__ __forceinline__ float bf16_round(float x) {
-  return __uint_as_float(f32_to_bf16(x) << 16);
+  return __uint_as_float(to_bf16<kSel>(x) << 16);
 }
 
 __device__ __forceinline__ void unpack8(const uint4 v, float (&f)[8]) {
@@ -62,11 +78,12 @@ __device__ __forceinline__ void unpack8(const uint4 v, float (&f)[8]) {
   f[6] = __uint_as_float(v.w << 16); f[7] = __uint_as_float(v.w & 0xFFFF0000u);
 }
 
+template <bool kSel>
 __device__ __forceinline__ uint4 pack8(const float (&f)[8]) {
-  return make_uint4(f32_to_bf16(f[0]) | (f32_to_bf16(f[1]) << 16),
-                    f32_to_bf16(f[2]) | (f32_to_bf16(f[3]) << 16),
-                    f32_to_bf16(f[4]) | (f32_to_bf16(f[5]) << 16),
-                    f32_to_bf16(f[6]) | (f32_to_bf16(f[7]) << 16));
+  return make_uint4(to_bf16<kSel>(f[0]) | (to_bf16<kSel>(f[1]) << 16),
+                    to_bf16<kSel>(f[2]) | (to_bf16<kSel>(f[3]) << 16),
+                    to_bf16<kSel>(f[4]) | (to_bf16<kSel>(f[5]) << 16),
+                    to_bf16<kSel>(f[6]) | (to_bf16<kSel>(f[7]) << 16));
 }
 
 // Row sum over the workgroup in the fixed order (every thread gets the result).
@@ -105,17 +122,19 @@ __device__ __forceinline__ void quant_tail(const uint4 (&nb)[G], int nv, uint8_t
   for (int i = 0; i < G; ++i)
     if (tid + i * T < nv) am = max(am, abs_bits_max8(nb[i]));
   const float sc = row_scale(block_max_t<T>(am));
+  const float rcp = 1.0f / sc;
   if (tid == 0) scale[row] = sc;
   uint2* qr = reinterpret_cast<uint2*>(q + (size_t)row * nv * 8);
 #pragma unroll
   for (int i = 0; i < G; ++i) {
     const int g = tid + i * T;
-    if (g < nv) qr[g] = quant8_any_scale(nb[i], sc);
+    if (g < nv) qr[g] = quant8_any_scale(nb[i], sc, rcp);
   }
 }
 
 // Gemma RMSNorm with residual: v = y + res (fp32); res_out = bf16(v);
-// n = bf16((v * (1 / sqrt(sum(v^2) / K + eps))) * (w + 1)).
+// n = bf16((v * (1 / sqrt(sum(v^2) / K + eps))) * (w + 1)). Rounds with selects: at decode sizes
+// a row's four waves are alone on their CU.
 template <int G>
 __global__ __launch_bounds__(kThreads) void add_rms_quant(
     const uint4* __restrict__ y, const uint4* __restrict__ res, const uint4* __restrict__ w,
@@ -139,7 +158,7 @@ __global__ __launch_bounds__(kThreads) void add_rms_quant(
         v[i][j] = a[j] + b[j];
         part = part + v[i][j] * v[i][j];
       }
-      res_out[g] = pack8(v[i]);
+      res_out[g] = pack8<true>(v[i]);
     }
   }
   const float inv = 1.0f / sqrtf(block_sum_fixed(part) / (float)K + eps);
@@ -152,7 +171,7 @@ __global__ __launch_bounds__(kThreads) void add_rms_quant(
       unpack8(w[g], wf);
 #pragma unroll
       for (int j = 0; j < 8; ++j) n[j] = (v[i][j] * inv) * (wf[j] + 1.0f);
-      nb[i] = pack8(n);
+      nb[i] = pack8<true>(n);
     }
   }
   quant_tail<G, kThreads>(nb, nv, q, scale, row);
@@ -160,6 +179,16 @@ __global__ __launch_bounds__(kThreads) void add_rms_quant(
 
 // SiLU-and-mul: gate_up [M, 2N] -> bf16(bf16(silu(gate)) * up). T threads per row: the only
 // reduction is the amax, so any T gives the same bits; short rows of work (small M) take 1024.
+template <bool kSel>
+__device__ __forceinline__ uint4 silu_mul_group(const uint4 gv, const uint4 uv) {
+  float a[8], b[8], p[8];
+  unpack8(gv, a);
+  unpack8(uv, b);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) p[j] = bf16_round<kSel>(silu_f32(a[j])) * b[j];
+  return pack8<kSel>(p);
+}
+
 template <int G, int T>
 __global__ __launch_bounds__(T) void silu_mul_quant(const uint4* __restrict__ gu,
                                                     uint8_t* __restrict__ q,
@@ -171,16 +200,31 @@ __global__ __launch_bounds__(T) void silu_mul_quant(const uint4* __restrict__ gu
 #pragma unroll
   for (int i = 0; i < G; ++i) {
     const int g = tid + i * T;
-    if (g < nv) {
-      float a[8], b[8], p[8];
-      unpack8(gate[g], a);
-      unpack8(up[g], b);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) p[j] = bf16_round(silu_f32(a[j])) * b[j];
-      nb[i] = pack8(p);
-    }
+    if (g < nv) nb[i] = silu_mul_group<false>(gate[g], up[g]);
   }
   quant_tail<G, T>(nb, nv, q, scale, row);
+}
+
+// One 8-element group of the per-head gated RMSNorm. All 16 lanes of a head call it together
+// (`in` is the same for the whole head); lanes past the row return zeros.
+__device__ __forceinline__ uint4 gdn_group(const uint4* __restrict__ x,
+                                           const uint4* __restrict__ zr,
+                                           const uint4* __restrict__ w, int g, bool in, float eps) {
+  float v[8];
+  unpack8(in ? x[g] : make_uint4(0, 0, 0, 0), v);
+  float part = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) part = part + v[j] * v[j];
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) part = part + __shfl_xor(part, o, 16);
+  if (!in) return make_uint4(0, 0, 0, 0);
+  const float inv = 1.0f / sqrtf(part * (1.0f / 128.0f) + eps);
+  float zz[8], wf[8], n[8];
+  unpack8(zr[g], zz);
+  unpack8(w[g & 15], wf);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) n[j] = ((v[j] * inv) * wf[j]) * silu_f32(zz[j]);
+  return pack8<false>(n);
 }
 
 // Per-head gated RMSNorm (head = 128 = 16 groups; norm before the gate, weight without +1):
@@ -199,28 +243,66 @@ __global__ __launch_bounds__(T) void gdn_norm_quant(
 #pragma unroll
   for (int i = 0; i < G; ++i) {
     const int g = tid + i * T;
-    const bool in = g < nv;                      // whole 16-lane heads are in or out together
-    float v[8];
-    unpack8(in ? x[g] : make_uint4(0, 0, 0, 0), v);
-    float part = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) part = part + v[j] * v[j];
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) part = part + __shfl_xor(part, o, 16);
-    if (in) {
-      const float inv = 1.0f / sqrtf(part * (1.0f / 128.0f) + eps);
-      float zz[8], wf[8], n[8];
-      unpack8(zr[g], zz);
-      unpack8(w[g & 15], wf);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) n[j] = ((v[j] * inv) * wf[j]) * silu_f32(zz[j]);
-      nb[i] = pack8(n);
-    }
+    nb[i] = gdn_group(x, zr, w, g, g < nv, eps);
   }
   quant_tail<G, T>(nb, nv, q, scale, row);
 }
 
+// ---- silu_mul at few rows: each row split over one-wave workgroups ------------------------------
+// With few rows, one workgroup per row leaves most CUs idle and runs VALU-bound (exp and two
+// divisions per element) on the rest: 9.6 us for one row of 17408. Here a row's 8-element groups
+// are cut into chunks of 64, one group per lane of a one-wave workgroup (grid S x M,
+// S = ceil(groups / 64) <= 64). Pass 1 computes each chunk's bf16 output and writes its amax bits
+// to part[row * S + chunk]; pass 2 computes the chunk again (same code, same bits), takes the
+// row's amax over the S partials (max is exact in any order) and quantizes. The result equals the
+// one-workgroup kernel's bit for bit; the price is a second launch and computing the chunk twice
+// (6.1 us at 1 to 16 rows of 17408). gdn_norm rows (N <= 10240, cheaper per element) are faster
+// in one launch.
+template <bool kQuant>
+__device__ __forceinline__ void split_tail(const uint4 nb, bool in, uint8_t* __restrict__ q,
+                                           float* __restrict__ scale, uint32_t* __restrict__ part,
+                                           int row, int chunk, int S, int nv) {
+  const int lane = threadIdx.x, g = chunk * 64 + lane;
+  if constexpr (!kQuant) {
+    const uint32_t am = wave_max(in ? abs_bits_max8(nb) : 0u);
+    if (lane == 0) part[row * S + chunk] = am;
+  } else {
+    const float sc = row_scale(wave_max(lane < S ? part[row * S + lane] : 0u));
+    if (chunk == 0 && lane == 0) scale[row] = sc;
+    if (in) reinterpret_cast<uint2*>(q + (size_t)row * nv * 8)[g] =
+        quant8_any_scale(nb, sc, 1.0f / sc);
+  }
+}
+
+template <bool kQuant>
+__global__ __launch_bounds__(64) void silu_mul_quant_split(const uint4* __restrict__ gu,
+                                                           uint8_t* __restrict__ q,
+                                                           float* __restrict__ scale,
+                                                           uint32_t* __restrict__ part, int N,
+                                                           int S) {
+  const int chunk = blockIdx.x, row = blockIdx.y, nv = N >> 3, g = chunk * 64 + threadIdx.x;
+  const uint4* gate = gu + (size_t)row * 2 * nv;
+  const bool in = g < nv;
+  const uint4 nb = in ? silu_mul_group<true>(gate[g], gate[nv + g]) : make_uint4(0, 0, 0, 0);
+  split_tail<kQuant>(nb, in, q, scale, part, row, chunk, S, nv);
+}
+
 }  // namespace
+
+// Rows at or below which silu_mul splits each row over one-wave workgroups (when the caller
+// registered scratch for the partial maxima); at 128 rows one workgroup per row is faster.
+#ifndef W4A8_SPLIT_ROWS_MAX
+#define W4A8_SPLIT_ROWS_MAX 64
+#endif
+constexpr int kSplitRowsMax = W4A8_SPLIT_ROWS_MAX;
+
+size_t producer_split_bytes(int M, int N) { return (size_t)M * ceil_div(N >> 3, 64) * 4; }
+
+// pass 2 reads a row's partials with one lane each
+bool split_rows(int M, int N, const void* part, size_t part_bytes) {
+  return M <= kSplitRowsMax && ceil_div(N >> 3, 64) <= 64 && part &&
+         producer_split_bytes(M, N) <= part_bytes;
+}
 
 hipError_t launch_add_rms_quant(const void* y, const void* res, const void* w, uint8_t* q,
                                 float* scale, void* res_out, int M, int K, float eps,
@@ -244,8 +326,16 @@ hipError_t launch_add_rms_quant(const void* y, const void* res, const void* w, u
 constexpr int kWideRowsMax = 128;
 
 hipError_t launch_silu_mul_quant(const void* gate_up, uint8_t* q, float* scale, int M, int N,
-                                 hipStream_t stream) {
+                                 void* part, size_t part_bytes, hipStream_t stream) {
   if (M == 0) return hipSuccess;
+  if (split_rows(M, N, part, part_bytes)) {
+    const int S = ceil_div(N >> 3, 64);
+    hipLaunchKernelGGL(silu_mul_quant_split<false>, dim3(S, M), dim3(64), 0, stream,
+                       (const uint4*)gate_up, q, scale, (uint32_t*)part, N, S);
+    hipLaunchKernelGGL(silu_mul_quant_split<true>, dim3(S, M), dim3(64), 0, stream,
+                       (const uint4*)gate_up, q, scale, (uint32_t*)part, N, S);
+    return hipGetLastError();
+  }
   const bool wide = M <= kWideRowsMax;
   const int T = wide ? 1024 : kThreads;
   const int G = ceil_div(N >> 3, T);

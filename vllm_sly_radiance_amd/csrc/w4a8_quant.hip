@@ -3,7 +3,7 @@
 // Semantics are those of the reference's pure-torch quantizer _traced_quant
 // (sly/mxfp4/radiance_mxfp4.py:392-396), evaluated in fp32 exactly as torch's CPU kernels do:
 //   s = max(amax(|x|) * fl32(1/448), 1/(448*512))      NaN in the row propagates to s
-//   q = e4m3_rne(clamp(x / s, -448, 448))               IEEE-correct fp32 division
+//   q = e4m3_rne(clamp(x / s, -448, 448))               the IEEE fp32 quotient
 // One workgroup (4 wave64) per token. Each thread keeps its 16-byte chunks in registers across
 // the amax reduction, so the row is read from HBM once. The amax runs on the bf16 bit patterns
 // (|x| bits = x & 0x7FFF): integer max is exact, orders like the magnitudes and ranks NaN above
@@ -39,16 +39,17 @@ __global__ __launch_bounds__(kThreads) void quant_rows_vec(const uint16_t* __res
   if (tid == 0) s[row] = sc;
   uint2* qr = reinterpret_cast<uint2*>(q + (size_t)row * K);
   if (finite(sc)) {
+    const float rcp = 1.0f / sc;
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int c = tid + i * kThreads;
-      if (c < nch) qr[c] = quant8<true>(v[i], sc);
+      if (c < nch) qr[c] = quant8(v[i], sc, rcp);
     }
   } else {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int c = tid + i * kThreads;
-      if (c < nch) qr[c] = quant8<false>(v[i], sc);
+      if (c < nch) qr[c] = quant8_any(v[i], sc);
     }
   }
 }
