@@ -25,15 +25,16 @@ be held to bit-exact parity:
     16 groups by a 16-lane xor butterfly (8, 4, 2, 1).
   * 1/sqrt is two correctly rounded fp32 operations, 1 / sqrt(.), where the reference uses the
     hardware rsqrt approximation.
-  * exp is exp_f32 below (Cody-Waite reduction by ln 2 and a degree-7 Taylor polynomial, every
-    step a correctly rounded fp32 operation), where the reference calls libm's expf.
+  * exp is exp_f32 below (Cody-Waite reduction by ln 2 and a degree-7 Taylor polynomial by
+    Horner, the reduction and every Horner step one fused multiply-add, fma_f32), where the
+    reference calls libm's expf.
   * The e4m3 codes divide by the scale (IEEE fp32 division), as _traced_quant does; the
     reference's HIP producers multiply by fl32(1/scale) instead and document a possible 1-code
     difference (sly/mxfp4/radiance_mxfp4.py:383-386). With division the fused op equals
     "producer -> bf16 -> quant_per_token" bit for bit.
 
-Pins (tests/test_oracle_producers.py): exp_f32 and silu_f32 against float64 numpy within 4 fp32
-ulp over a dense sweep and at the special values (0, +-inf, NaN, overflow and underflow edges);
+Pins (tests/test_oracle_producers.py): fma_f32 against C's fmaf bit for bit on edge-case and
+random triples; exp_f32 and silu_f32 against float64 numpy within 2 / 4 fp32 ulp over a dense sweep and at the special values (0, +-inf, NaN, overflow and underflow edges);
 the fixed-order sums against float64 sums within their rounding bound and against the same sums
 re-associated by plain loops on tiny rows; every producer against the float64 formula of the
 reference's native chain within one bf16 rounding, and against quant_per_token of its own bf16
@@ -60,18 +61,42 @@ TAYLOR = [F32(1.0 / 5040.0), F32(1.0 / 720.0), F32(1.0 / 120.0), F32(1.0 / 24.0)
           F32(1.0 / 6.0), F32(0.5), F32(1.0), F32(1.0)]
 
 
+def fma_f32(a, b, c) -> np.ndarray:
+    """fl32(a * b + c) with one rounding (IEEE fusedMultiplyAdd in binary32), elementwise.
+
+    a * b is exact in float64 (two 24-bit significands). The float64 sum s = RN64(a*b + c) may
+    round; its error e = (a*b + c) - s is exact by Knuth's TwoSum. Round-to-odd repairs the double
+    rounding: when e != 0 and s's last bit is even, s moves one float64 ulp towards the exact value,
+    and RN32 of a round-to-odd float64 (53 >= 24 + 2 bits) equals RN32 of the exact value
+    (Boldo and Melquiond, "Emulation of FMA and correctly rounded sums: proved algorithms using
+    rounding to odd", IEEE TC 57(4), 2008). Non-finite results pass through from the float64 sum."""
+    a64 = np.asarray(a, dtype=F32).astype(np.float64)
+    b64 = np.asarray(b, dtype=F32).astype(np.float64)
+    c64 = np.asarray(c, dtype=F32).astype(np.float64)
+    with np.errstate(over="ignore", invalid="ignore"):
+        p = a64 * b64
+        s = p + c64
+        bv = s - p
+        err = (p - (s - bv)) + (c64 - bv)
+        bits = np.ascontiguousarray(s).view(np.int64)
+        fix = np.isfinite(s) & np.isfinite(err) & (err != 0) & ((bits & 1) == 0)
+        step = np.where(np.signbit(s) == (err < 0), 1, -1).astype(np.int64)   # away from / to 0
+        s_odd = np.where(fix, bits + step, bits).view(np.float64)
+        return s_odd.astype(F32)
+
+
 def exp_f32(y: np.ndarray) -> np.ndarray:
-    """e^y in fp32, every step a correctly rounded fp32 operation (no fused multiply-add):
-        n = rint(y * log2e);  r = (y - n ln2_hi) - n ln2_lo;  p = Taylor_7(r) by Horner;
-        e^y = ldexp(p, n);  y > EXP_HI -> inf, y < EXP_LO -> +0, NaN -> NaN."""
+    """e^y in fp32, every step one correctly rounded fp32 operation or fused multiply-add:
+        n = rint(y * log2e);  r = fma(-n, ln2_lo, fma(-n, ln2_hi, y));  p = Taylor_7(r) by Horner
+        with fma;  e^y = ldexp(p, n);  y > EXP_HI -> inf, y < EXP_LO -> +0, NaN -> NaN."""
     y = np.asarray(y, dtype=F32)
     with np.errstate(over="ignore", invalid="ignore"):
         yc = np.where(np.isfinite(y), y, F32(0)).astype(F32)
         n = np.rint((yc * LOG2E).astype(F32)).astype(F32)
-        r = ((yc - (n * LN2_HI).astype(F32)).astype(F32) - (n * LN2_LO).astype(F32)).astype(F32)
+        r = fma_f32(-n, LN2_LO, fma_f32(-n, LN2_HI, yc))
         p = TAYLOR[0]
         for c in TAYLOR[1:]:
-            p = ((p * r).astype(F32) + c).astype(F32)
+            p = fma_f32(p, r, c)
         e = np.ldexp(p, n.astype(np.int32)).astype(F32)
         e = np.where(y > EXP_HI, F32(np.inf), e)
         e = np.where(y < EXP_LO, F32(0), e)

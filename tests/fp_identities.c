@@ -9,8 +9,9 @@
 //   exp        The branch-free exp_f32 (clamp to [-104, 89], put NaN back) equals the branching
 //              form (NaN -> NaN, y > 88.7228394 -> +inf, y < fl32(-150 ln 2) -> +0) bit for bit,
 //              over every fp32 input (or every `stride`-th one).
+//   fma        fmaf of float32 triples read from stdin, for pinning the oracle's fma emulation.
 //
-// Prints "ok <count>" and exits 0, or prints the first mismatches and exits 1.
+// The checks print "ok <count>" and exit 0, or print the first mismatches and exit 1.
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -52,15 +53,15 @@ static const float kExpHi = 0x1.62e43p+6f, kExpLo = -0x1.9fe368p+6f;
 
 static inline float exp_core(float y) {
   const float n = rintf(y * kLog2e);
-  const float r = (y - n * kLn2Hi) - n * kLn2Lo;
+  const float r = fmaf(-n, kLn2Lo, fmaf(-n, kLn2Hi, y));
   float p = 0x1.a01a02p-13f;
-  p = p * r + 0x1.6c16c2p-10f;
-  p = p * r + 0x1.111112p-7f;
-  p = p * r + 0x1.555556p-5f;
-  p = p * r + 0x1.555556p-3f;
-  p = p * r + 0.5f;
-  p = p * r + 1.0f;
-  p = p * r + 1.0f;
+  p = fmaf(p, r, 0x1.6c16c2p-10f);
+  p = fmaf(p, r, 0x1.111112p-7f);
+  p = fmaf(p, r, 0x1.555556p-5f);
+  p = fmaf(p, r, 0x1.555556p-3f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
   return ldexpf(p, (int)n);
 }
 
@@ -103,9 +104,20 @@ static int exp_check(long stride) {
   return 0;
 }
 
+// fma: reads float32 triples (a, b, c) from stdin, writes fmaf(a, b, c) for each to stdout
+static int fma_vectors(void) {
+  float t[3];
+  while (fread(t, sizeof(float), 3, stdin) == 3) {
+    const float r = fmaf(t[0], t[1], t[2]);
+    if (fwrite(&r, sizeof(float), 1, stdout) != 1) return 1;
+  }
+  return 0;
+}
+
 int main(int argc, char** argv) {
   if (argc >= 2 && !strcmp(argv[1], "markstein")) return markstein();
   if (argc >= 2 && !strcmp(argv[1], "exp")) return exp_check(argc >= 3 ? atol(argv[2]) : 1);
-  fprintf(stderr, "usage: %s markstein | exp [stride]\n", argv[0]);
+  if (argc >= 2 && !strcmp(argv[1], "fma")) return fma_vectors();
+  fprintf(stderr, "usage: %s markstein | exp [stride] | fma < triples\n", argv[0]);
   return 2;
 }

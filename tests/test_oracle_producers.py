@@ -6,6 +6,7 @@ other than itself: float64 numpy for exp and silu; float64 sums and plain scalar
 fixed-order sums of squares; the reference's native chains (m_add_rms / m_silu / m_gdn,
 sly/check_fused_norm.py:119-136) evaluated by torch's CPU kernels for the producers; closed forms."""
 import math
+import os
 
 import numpy as np
 import pytest
@@ -23,6 +24,57 @@ def ulps(a, ref):
     a = np.asarray(a, dtype=np.float64)
     sp = np.spacing(np.abs(ref).astype(F32)).astype(np.float64)
     return np.abs(a - ref) / sp
+
+
+def fma_triples(n, seed):
+    """Edge cases (signed zeros, subnormals, infinities, NaN, overflow), random triples with c near
+    -a*b (cancellation), and double-rounding traps: a = 1 + i 2^-12, b = 1 + j 2^-12 with i j odd
+    make a*b an fp32 midpoint exactly, and c = +-2^-e (e = 60..100) moves the exact sum off it by
+    less than a float64 ulp, so float64 arithmetic alone rounds such triples the wrong way."""
+    rng = np.random.default_rng(seed)
+    sp = np.array([0.0, -0.0, 1.0, -1.0, 1e-45, -1e-45, 1.17549435e-38, 3.4028235e38, -3.4028235e38,
+                   np.inf, -np.inf, np.nan, 0.5, 2.0 ** -24, 1.0 + 2.0 ** -23, 3.0, 1.0 / 3.0],
+                  np.float32)
+    edge = np.stack(np.meshgrid(sp, sp, sp, indexing="ij"), -1).reshape(-1, 3)
+    a = rng.integers(0, 2 ** 32, n, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    b = rng.integers(0, 2 ** 32, n, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    a = np.ldexp(np.frexp(np.where(np.isfinite(a), a, 1.5))[0], rng.integers(-60, 60, n))
+    b = np.ldexp(np.frexp(np.where(np.isfinite(b), b, -0.75))[0], rng.integers(-60, 60, n))
+    prod = a.astype(np.float64) * b.astype(np.float64)
+    c = -prod * np.ldexp(1.0, rng.integers(-30, 30, n)) * rng.choice([1.0, 1.0 + 2.0 ** -23, 0.5], n)
+    with np.errstate(over="ignore"):
+        rand = np.stack([a, b, c], 1).astype(np.float32)          # some c overflow to +-inf
+    i = 2 * rng.integers(0, 2048, n) + 1
+    j = 2 * rng.integers(0, 2048, n) + 1
+    e2 = rng.integers(-20, 20, n)
+    ta = np.ldexp(1.0 + i * 2.0 ** -12, e2)
+    tb = 1.0 + j * 2.0 ** -12
+    tc = np.ldexp(rng.choice([1.0, -1.0], n), e2 - rng.integers(60, 100, n))
+    traps = np.stack([ta, tb, tc], 1).astype(np.float32)
+    return np.concatenate([edge, rand, traps]).astype(np.float32)
+
+
+def test_fma_emulation_matches_c_fmaf(tmp_path):
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    exe = str(tmp_path / "fpid")
+    subprocess.run([gcc, "-O2", "-ffp-contract=off", "-fopenmp",
+                    os.path.join(os.path.dirname(__file__), "fp_identities.c"), "-o", exe, "-lm"],
+                   check=True)
+    tr = fma_triples(200_000, 7)
+    out = subprocess.run([exe, "fma"], input=tr.tobytes(), capture_output=True, check=True).stdout
+    want = np.frombuffer(out, np.float32)
+    got = P.fma_f32(tr[:, 0], tr[:, 1], tr[:, 2])
+    same = (got.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got) & np.isnan(want))
+    bad = np.flatnonzero(~same)
+    assert bad.size == 0, f"{bad.size} differ, first {tr[bad[:3]]} -> {got[bad[:3]]} vs {want[bad[:3]]}"
+    # the emulation is not plain float64 arithmetic: some triples round differently
+    with np.errstate(over="ignore", invalid="ignore"):
+        plain = (tr[:, 0].astype(np.float64) * tr[:, 1] + tr[:, 2]).astype(np.float32)
+    assert np.count_nonzero(plain.view(np.uint32) != want.view(np.uint32)) > 0
 
 
 def test_exp_within_two_ulp_of_float64():

@@ -11,16 +11,17 @@
 // each op equals "producer -> bf16 -> quant".
 //
 // Every floating-point step is fixed so that the results are reproducible bit for bit on a CPU:
-//  * no contracted multiply-add (the pragma below): each product and sum rounds; the only fused
-//    multiply-adds are the explicit ones of the quantizer's division (w4a8_fp8.h), whose codes
-//    equal those of the IEEE quotient;
+//  * no contracted multiply-add (the pragma below): each product and sum rounds, except the
+//    explicit fused multiply-adds of exp_f32 and of the quantizer's division (w4a8_fp8.h, whose
+//    codes equal those of the IEEE quotient);
 //  * sums of squares run in a fixed order: a thread adds its groups' squares element by element,
 //    a wave combines by an xor butterfly (32, 16, 8, 4, 2, 1) and the four waves add in order; a
 //    gdn head (16 groups) combines by a 16-lane xor butterfly (8, 4, 2, 1);
 //  * 1/sqrt is a correctly rounded square root and a correctly rounded division;
 //  * exp is exp_f32 below: Cody-Waite reduction by ln 2 (Cody and Waite, "Software Manual for the
 //    Elementary Functions", 1980; ln 2 split into a 16-bit head and a tail) and the degree-7
-//    Taylor polynomial of e^r on |r| <= ln2 / 2 by Horner, then an exact scaling by 2^n.
+//    Taylor polynomial of e^r on |r| <= ln2 / 2 by Horner, the reduction and each Horner step one
+//    fused multiply-add, then an exact scaling by 2^n.
 #pragma clang fp contract(off)
 
 #include "w4a8_fp8.h"
@@ -45,15 +46,15 @@ static_assert(kExpHi < 89.0f && kExpLo > -104.0f, "exp_f32's clamp must bracket 
 __device__ __forceinline__ float exp_f32(float y_in) {
   const float y = fminf(fmaxf(y_in, -104.0f), 89.0f);
   const float n = rintf(y * kLog2e);
-  const float r = (y - n * kLn2Hi) - n * kLn2Lo;
+  const float r = __builtin_fmaf(-n, kLn2Lo, __builtin_fmaf(-n, kLn2Hi, y));
   float p = 0x1.a01a02p-13f;                      // 1/k!, k = 7 .. 2, rounded to fp32
-  p = p * r + 0x1.6c16c2p-10f;
-  p = p * r + 0x1.111112p-7f;
-  p = p * r + 0x1.555556p-5f;
-  p = p * r + 0x1.555556p-3f;
-  p = p * r + 0.5f;
-  p = p * r + 1.0f;
-  p = p * r + 1.0f;
+  p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+  p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+  p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+  p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
   const float e = ldexpf(p, (int)n);
   return y_in != y_in ? y_in : e;
 }
