@@ -81,7 +81,9 @@ def canon_nan(c):
 @pytest.mark.parametrize("M,K,ldx", [(1, 5120, None), (8, 5120, None), (17, 1000, None),
                                      (64, 8704, None), (3, 17408, None), (5, 24, None),
                                      (9, 5120, 5128), (7, 640, 641), (1, 40000, None),
-                                     (4096, 5120, None)])
+                                     (4096, 5120, None), (300, 5120, None), (257, 8704, 8712),
+                                     (256, 24, None), (261, 10240, None), (256, 10248, None),
+                                     (258, 1000, 1001)])
 def test_quant_bit_exact(gpu_lib, M, K, ldx):
     x = synthetic.activations(M, K, seed=M * 7 + K)
     q, s = gpu_quant(x, ldx)
@@ -110,6 +112,27 @@ def test_quant_special_rows(gpu_lib):
     assert np.array_equal(s[fin].view(np.uint32), os_[fin].view(np.uint32))
     assert np.array_equal(canon_nan(q), canon_nan(oq))
     assert q[2, 7] == 0x80 and q[5, 4] == 0x80       # -0 kept; finite / inf -> -0
+
+
+def test_quant_special_rows_many(gpu_lib):
+    """The special rows again, 33 copies each (264 rows, several workgroups per CU)."""
+    K = 256
+    rows = np.zeros((8, K), np.float32)
+    rows[3, :] = np.linspace(-1e-30, 1e-30, K)
+    rows[4, :] = np.linspace(-3e38, 3e38, K)
+    rows[5, 3] = np.inf
+    rows[5, 4] = -2.0
+    rows[6, 9] = np.nan
+    rows[7, :] = 448.0
+    x = np.tile(O.f32_to_bf16(rows), (33, 1))
+    x[2::8, 7] = 0x8000
+    q, s = gpu_quant(x)
+    oq, os_ = O.quant_per_token(x)
+    assert np.array_equal(np.isnan(s), np.isnan(os_)) and np.isnan(s).sum() == 33
+    fin = ~np.isnan(os_)
+    assert np.array_equal(s[fin].view(np.uint32), os_[fin].view(np.uint32))
+    assert np.array_equal(canon_nan(q), canon_nan(oq))
+    assert np.all(q[2::8, 7] == 0x80) and np.all(q[5::8, 4] == 0x80)
 
 
 def test_quant_rounding_ties_and_subnormals(gpu_lib):
