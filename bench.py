@@ -11,8 +11,9 @@ graph of launches (a single launch is shorter than the host's launch overhead); 
 duration comes from HIP event pairs around individual launches on the launch stream.
 
 Alongside: the M=4096 prefill GEMMs (gate_up 17408x5120, down 5120x8704) in TFLOP/s against the
-fp8 x fp4 MFMA peak, the M=1 per-layer linear set, and the CPU baseline (the oracle's dequant +
-fp32 matmul, timed on this host). Prints ONE JSON line.
+fp8 x fp4 MFMA peak, the M=1 per-layer linear set, the fused producers and the per-token quantizer
+at M=8 and M=4096 in GB/s, and the CPU baseline (the oracle's dequant + fp32 matmul, timed on this
+host). Prints ONE JSON line.
 
   python bench.py [--gpus 1] [--steps 1024] [--warmup 64]
 """
@@ -58,8 +59,8 @@ def parse():
     ap.add_argument("--sweep-layers", type=int, default=64)
     ap.add_argument("--profile", action="store_true",
                     help="counter-run workload: the verify-GEMM graph replay, 4 launches of each "
-                         "prefill GEMM and one 256 MiB device copy (the counter calibration); "
-                         "prints no JSON")
+                         "prefill GEMM, fused producer and quantizer shape at M=4096, and one "
+                         "256 MiB device copy (the counter calibration); prints no JSON")
     return ap.parse_args()
 
 
@@ -239,6 +240,48 @@ class Producer:
             n.gdn_norm_quant(self.w[i].data_ptr(), self.w2[i].data_ptr(), self.N,
                              self.weight.data_ptr(), self.q.data_ptr(), self.s.data_ptr(), self.M,
                              self.N, 1e-6, stream)
+
+
+class Quant:
+    """Device operands of the per-token quantizer (w4a8_quant_per_token) on `copies` distinct bf16
+    activation sets."""
+
+    def __init__(self, M, K, copies, seed):
+        import torch
+        from vllm_sly_radiance_amd import _native, synthetic
+        self.M, self.K, self._native = M, K, _native
+        self.w = [torch.from_numpy(synthetic.activations(M, K, seed + i).view(np.int16)).cuda()
+                  for i in range(copies)]
+        self.q = torch.empty((M, K), dtype=torch.uint8, device="cuda")
+        self.s = torch.empty((M,), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+
+    def bytes(self):
+        return 3 * self.M * self.K + 4 * self.M          # bf16 in; codes and scales out
+
+    def launch(self, i, stream):
+        self._native.quant_per_token(self.w[i].data_ptr(), self.K, self.q.data_ptr(),
+                                     self.s.data_ptr(), self.M, self.K, stream)
+
+
+# the quantizer in front of every GEMM whose input no fused producer makes: (M, K)
+QUANT_SHAPES = [(8, 5120), (4096, 5120), (4096, 8704)]
+
+
+def bench_quant():
+    import torch
+    res = []
+    for M, K in QUANT_SHAPES:
+        copies = max(2, min(16, -(-512 * 2 ** 20 // (2 * M * K))))
+        g = Quant(M, K, copies, seed=31)
+        steps, _, sec, _, _ = graph_timed(g, 8 * copies, 2 * copies, warm_seconds=0.2)
+        us = sec / steps * 1e6
+        gbs = g.bytes() / (us * 1e-6) / 1e9
+        res.append(dict(M=M, K=K, us=round(us, 2), gbs=round(gbs, 1),
+                        frac=round(gbs / HBM_PEAK_GBS, 4)))
+        del g
+        torch.cuda.empty_cache()
+    return res
 
 
 # (op, width) at the benchmark model's shapes: the decoder norms feed K = 5120, the MLP activation
@@ -465,7 +508,8 @@ def profile_workload():
     """The launches the committed rocprofv3 summaries are taken on: the verify GEMM (the bench's
     graph replay: one second of warmup replays, then 64 timed launches over 16 weight copies,
     plus 64 event-bracketed single launches), each prefill GEMM (4 launches), each fused
-    producer at M = 4096 (4 launches over 2 input copies) and a plain 256 MiB device copy
+    producer and the quantizer at M = 4096 (4 launches over 2 input copies each) and a plain
+    256 MiB device copy
     (torch's copy kernel), whose FETCH_SIZE / WRITE_SIZE readings calibrate the counters: a copy
     of B bytes fetches B and writes B."""
     import torch
@@ -484,6 +528,12 @@ def profile_workload():
         del g
     for kind, N in PRODUCERS:                      # the fused producers at M = 4096
         g = Producer(kind, 4096, N, 2, seed=21)
+        for i in range(4):
+            g.launch(i % 2, st.cuda_stream)
+        torch.cuda.synchronize()
+        del g
+    for M, K in QUANT_SHAPES[1:]:                  # the quantizer at M = 4096
+        g = Quant(M, K, 2, seed=31)
         for i in range(4):
             g.launch(i % 2, st.cuda_stream)
         torch.cuda.synchronize()
@@ -538,7 +588,7 @@ def main():
     print(f"[bench] verify M=8: {v['kernel_us']:.2f} us/launch in the graph-timed region, "
           f"event pairs {v['event_pair_us_median']:.2f} us median, plan {v['plan']}",
           file=sys.stderr, flush=True)
-    prefill = layer = producers = None
+    prefill = layer = producers = quant = None
     if not args.only_verify:
         prefill = bench_prefill()
         print(f"[bench] prefill: {prefill}", file=sys.stderr, flush=True)
@@ -546,6 +596,8 @@ def main():
         print(f"[bench] M=1 layer: {layer}", file=sys.stderr, flush=True)
         producers = bench_producers()
         print(f"[bench] producers: {producers}", file=sys.stderr, flush=True)
+        quant = bench_quant()
+        print(f"[bench] quantizer: {quant}", file=sys.stderr, flush=True)
     probe = mfma_probe()
     print(f"[bench] MFMA probe TFLOP/s: {probe}", file=sys.stderr, flush=True)
     cpu = None if args.no_cpu else cpu_baseline()
@@ -577,6 +629,7 @@ def main():
         "mfma_probe_tflops": probe,
         "decode_m1_layer": layer,
         "producers": producers,
+        "quantizer": quant,
     }
     print(json.dumps(line), flush=True)
 
