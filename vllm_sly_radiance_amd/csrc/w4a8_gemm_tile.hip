@@ -3,9 +3,10 @@
 //
 // Counterpart of the reference's folded / A-tiled prefill kernels
 // (sly/mxfp4/radiance_mxfp4_fp8.hip:326-590, :664-944), redesigned for CDNA4:
-//  * 4 wave64 in a 2 x 2 arrangement; each wave owns WM x WN MFMA tiles of 16 tokens x 16
-//    columns (up to 128 x 128 per wave), so the workgroup tile is (32 WM) tokens x (32 WN) columns
-//    and a 128-k slab is 32 WM * 128 B of activations, 2 WN weight granules and their scale dwords.
+//  * NW wave64 (4 or 8) in an (NW / 2) x 2 arrangement; each wave owns WM x WN MFMA tiles of 16
+//    tokens x 16 columns, so the workgroup tile is (8 NW WM) tokens x (32 WN) columns (up to
+//    256 x 256) and a 128-k slab is 8 NW WM * 128 B of activations, 2 WN weight granules and their
+//    scale dwords.
 //  * One load instruction moves one 1 KiB unit of a slab straight into LDS: a weight granule
 //    verbatim (already in MFMA fragment order), or 8 tokens x 128 k of activations. For the latter,
 //    8 consecutive lanes read one token's 128-byte line: lanes that read scattered tokens instead
