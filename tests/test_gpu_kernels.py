@@ -340,8 +340,10 @@ def test_gemm_every_stream_variant(gpu_lib, N, K):
     assert (ran > 0) == served
 
 
+# K = 640, 96 and 1056 end inside a k-group: the k-loop runs whole k-groups over zero slabs
 @pytest.mark.parametrize("M,N,K", [(65, 544, 1024), (300, 1040, 2560), (1000, 17408 // 8, 5120),
-                                   (129, 33, 640), (513, 5120, 8704)])
+                                   (129, 33, 640), (513, 5120, 8704), (70, 200, 96),
+                                   (257, 300, 1056)])
 def test_gemm_every_tile_variant(gpu_lib, M, N, K):
     x = synthetic.activations(M, K, seed=M)
     w, ws = synthetic.weights(N, K, seed=N)

@@ -46,18 +46,27 @@ struct TileShape {
   static constexpr int S_ROWS = BN / 16;         // 256 B scale-dword rows per k-group (one per n-tile)
   static constexpr int A_PER_WAVE = A_UNITS / NW;
   static constexpr int W_PER_WAVE = ceil_div(W_UNITS, NW);
-  static constexpr int S_QUARTER = ceil_div(S_ROWS, 4);        // rows filled per slab
-  static constexpr int S_PER_WAVE = ceil_div(S_QUARTER, NW);
-  static constexpr int OPS = A_PER_WAVE + W_PER_WAVE + S_PER_WAVE;   // fills per wave per slab
-  // every wave issues the same number of fills; the surplus ones (past W_UNITS, or past a
-  // quarter's scale rows) are zero fills into padding slots of their own
+  // Every slab, each wave fills OPS units (activations and weight granules; surplus granule slots
+  // past W_UNITS are zero fills into padding units of their own). Every fourth slab each wave
+  // also fills one 1 KiB scale unit, 4 rows of the next k-group (waves past S_OPS fill a junk
+  // unit), so a k-group's rows take one fill per wave instead of one 4-byte fill per row.
+  static constexpr int OPS = A_PER_WAVE + W_PER_WAVE;
+  static constexpr int S_OPS = ceil_div(S_ROWS, 4);          // 1 KiB scale units per k-group
   static constexpr int W_OFF = A_UNITS * 1024;
   static constexpr int STAGE = W_OFF + NW * W_PER_WAVE * 1024;
-  // scale ring: 3 k-groups of S_ROWS rows, plus one junk row
-  static constexpr int S_SLOT = (4 * S_QUARTER + 1) * 256;
+  // scale ring: 3 k-groups of S_ROWS rows (rounded up to whole units)
+  static constexpr int S_SLOT = S_OPS * 1024;
   // the tile's per-token fp32 scales, one 256-byte row per 64 tokens
   static constexpr int TSCALE = 256 * ceil_div(BM, 64);
-  static_assert(NW % 2 == 0 && A_UNITS % NW == 0, "tile");
+  static_assert(NW % 2 == 0 && A_UNITS % NW == 0 && S_OPS <= NW, "tile");
+  // fills one wave issues for slab s: the scale unit rides with every slab s % 4 == 0
+  static constexpr int fills(int s) { return OPS + (s % 4 == 0 ? 1 : 0); }
+  // fills issued for slabs s0 + 1 .. s0 + n (all younger than slab s0's), s0 known modulo 4
+  static constexpr int fills_after(int s0, int n) {
+    int t = 0;
+    for (int d = 1; d <= n; ++d) t += fills(s0 + d);
+    return t;
+  }
 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -76,17 +85,23 @@ __device__ __forceinline__ void bare_barrier() {
   asm volatile("" ::: "memory");
 }
 
+template <int Q>
+struct IntC {
+  static constexpr int value = Q;
+};
+
 template <int WM, int WN, int NS, int NW>
 __global__ __launch_bounds__(NW * 64) void gemm_tile(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
     const uint32_t* __restrict__ Sq, uint16_t* __restrict__ C, int M, int N, int K, int KTp,
     int KTe, int KG, int NTILES, int grid_m, int grid_n, int ldc, int vec_out) {
   using S = TileShape<WM, WN, NW>;
-  static_assert(NS >= 2 && NS <= 5 && (NS - 2) * S::OPS < 64, "pipeline depth");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * S::STAGE + 3 * S::S_SLOT +
+  static_assert(NS >= 2 && NS <= 5 && (NS - 1) * (S::OPS + 1) < 64, "pipeline depth");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * S::STAGE + 3 * S::S_SLOT + 1024 +
                                                          S::TSCALE];
   uint8_t* const sring = lds + NS * S::STAGE;
-  uint8_t* const tscale = sring + 3 * S::S_SLOT;   // the tile's per-token fp32 scales
+  uint8_t* const junk = sring + 3 * S::S_SLOT;     // where the surplus scale fills land
+  uint8_t* const tscale = junk + 1024;             // the tile's per-token fp32 scales
 
   // ---- tile order: XCD-contiguous runs, grouped by 8 row blocks ----
   const int total = grid_m * grid_n;
@@ -123,9 +138,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile(
   const int f_lo = 1024 * (f_row >> 3) + 16 * (8 * (f_row & 7) + ((lane >> 4) ^ ((f_row >> 1) & 7)));
   const int f_hi = f_lo ^ 64;                               // chunk + 4: slot bit 2 flips
 
-  // Fill op o of slab kt into stage base: an activation unit (o < A_PER_WAVE), a weight granule,
-  // or a scale row. Scale rows are per k-group of 4 slabs: the fills of slab kt carry quarter
-  // kt % 4 of the rows of k-group kt / 4 + 1, into ring slot (kt / 4 + 1) % 3.
+  // Fill op o of slab kt into stage base: an activation unit (o < A_PER_WAVE) or a weight granule.
   auto fill_op = [&](int kt, uint8_t* base, int o) {
     const bool kin = kt < KTe;
     if (o < S::A_PER_WAVE) {
@@ -140,22 +153,31 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile(
       const int off = (kin & (g < S::W_UNITS)) ? (g * KTp + kt) * kGranuleBytes + lane * 16 : kOut;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(w_src, (lds_ptr_t)(base + S::W_OFF + g * 1024), 16,
                                                off, 0, 0, kBufferNT);
-    } else {
-      const int grp = (kt >> 2) + 1, q = kt & 3;
-      const int i = wave * S::S_PER_WAVE + (o - S::A_PER_WAVE - S::W_PER_WAVE);
-      const int r = q * S::S_QUARTER + i;
-      const bool real = (i < S::S_QUARTER) & (r < S::S_ROWS);
-      const int off = (real & (grp < KG)) ? ((r * KG + grp) * 64 + lane) * 4 : kOut;
-      const int slot = grp % 3;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          s_src, (lds_ptr_t)(sring + slot * S::S_SLOT + (real ? r : 4 * S::S_QUARTER) * 256), 4,
-          off, 0, 0, 0);
     }
+  };
+  // Scale unit of k-group grp into ring slot grp % 3: wave w < S_OPS moves rows 4w .. 4w+3 (lanes
+  // 16 r .. 16 r + 15 read row 4w + r's 256 bytes, which land contiguously); the other waves move
+  // zeros into the junk unit. Rows past S_ROWS or k-groups past KG read zero.
+  auto fill_scales = [&](int grp) {
+    const int r = 4 * wave + (lane >> 4);
+    const bool mine = wave < S::S_OPS;
+    const int off = (mine & (r < S::S_ROWS) & (grp < KG)) ? (r * KG + grp) * 256 + (lane & 15) * 16
+                                                          : kOut;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        s_src, (lds_ptr_t)(mine ? sring + (grp % 3) * S::S_SLOT + wave * 1024 : junk), 16, off, 0,
+        0, 0);
+  };
+  // Fill op o < S::fills(kt) of slab kt: the slab's units, then (kt % 4 == 0) k-group kt/4 + 1's
+  // scale unit, which slabs 4 (kt/4 + 1) .. + 3 read.
+  auto fill_any = [&](int kt, uint8_t* base, int o) {
+    if (o < S::OPS) fill_op(kt, base, o);
+    else fill_scales((kt >> 2) + 1);
   };
   auto fill = [&](int kt, int st) {
     uint8_t* base = lds + st * S::STAGE;
 #pragma unroll
     for (int o = 0; o < S::OPS; ++o) fill_op(kt, base, o);
+    if ((kt & 3) == 0) fill_scales((kt >> 2) + 1);
   };
 
   v4f acc[WM][WN];
@@ -194,20 +216,14 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile(
                                                0, 0, 0);
   }
 
-  // k-group 0's scale rows go out first (4 quarters), so the wait for slab 0 covers them too
-  {
-    const int i = wave * S::S_PER_WAVE;
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-#pragma unroll
-      for (int e = 0; e < S::S_PER_WAVE; ++e) {
-        const int r = q * S::S_QUARTER + i + e;
-        const bool real = (i + e < S::S_QUARTER) & (r < S::S_ROWS);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            s_src, (lds_ptr_t)(sring + (real ? r : 4 * S::S_QUARTER) * 256), 4,
-            real ? (r * KG * 64 + lane) * 4 : kOut, 0, 0, 0);
-      }
-  }
+  // k-group 0's scale unit goes out first, so the wait for slab 0 covers it too
+  fill_scales(0);
+
+  // The k-loops run whole k-groups (4 slabs, the last group padded with zero slabs: the weight
+  // stripes are padded to whole k-groups and activations past K fill zeros), unrolled so that
+  // every slab knows at compile time whether its refill carries a scale unit, and so how many
+  // fills its wait may leave in flight.
+  const int KT4 = (KTe + 3) & ~3;
 
   if constexpr (WM >= 3) {
     // ---- NS-stage pipeline, barrier two MFMA groups before the end of each slab. At the
@@ -216,11 +232,13 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile(
     //      and first activation fragment, and refills slab kt's stage with slab kt+NS, while the
     //      last two groups of slab kt's MFMAs run. A slab is requested NS-1 slabs before its
     //      barrier, and no wave idles at a barrier with an empty MFMA queue behind it. ----
-    constexpr int R = WM >= 4 ? 3 : 2;             // MFMA groups past the barrier
+    // MFMA groups past the barrier: 3, or 2 for the 8-wave 256-wide tile, whose waves have 256
+    // registers each (the third group's fragments would spill)
+    constexpr int R = WM >= 4 ? ((NW == 8 && WN >= 8) ? 2 : 3) : 2;
     constexpr int P = WM - R;
 #pragma unroll
     for (int p = 0; p < NS; ++p) fill(p, p);
-    wait_vmcnt<(NS - 1) * S::OPS>();             // slab 0 (and k-group 0's scales) have landed
+    wait_vmcnt<S::fills_after(0, NS - 1)>();     // slab 0 (and k-group 0's scales) have landed
     bare_barrier();
     v4i wf[WN], lo, hi;
     uint32_t sc[WN];
@@ -228,7 +246,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile(
     read_a(0, 0, lo, hi);
     __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0): the loop starts with nothing pending
     int st = 0;
-    for (int kt = 0; kt < KTe; ++kt) {
+    auto slab = [&](int kt, auto qc) {
+      constexpr int q = decltype(qc)::value;    // kt % 4
+      constexpr int NF = S::fills(q + NS);       // fills of the refill, slab kt + NS
+      asm volatile("" : "+s"(kt));               // kt opaque: no per-copy loop invariants
       const int nst = st + 1 == NS ? 0 : st + 1;
       uint8_t* fbase = lds + st * S::STAGE;      // slab kt's stage, refilled with slab kt+NS
       v4i wfn[WN], lon, hin;
@@ -250,14 +271,14 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile(
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < WN; ++j)
-          acc[i][j] = mfma_w4a8(wf[j], xf, acc[i][j], sc[j] >> (8 * (kt & 3)));
+          acc[i][j] = mfma_w4a8(wf[j], xf, acc[i][j], sc[j] >> (8 * q));
         __builtin_amdgcn_sched_barrier(0);
       }
       {
         // the last R groups: their fragments are read before the barrier; past it, the next
         // slab's fragment reads and this slab's refill go out one or two per MFMA, so the MFMA
         // queue never waits behind a run of memory instructions
-        wait_vmcnt<(NS - 2) * S::OPS>();         // this wave's fills of slab kt+1 have landed
+        wait_vmcnt<S::fills_after(q + 1, NS - 2)>();  // this wave's fills of slab kt+1 landed
         __builtin_amdgcn_s_waitcnt(0xC07F);      // lgkmcnt(0): this wave's reads of slab kt done
         bare_barrier();
         __builtin_amdgcn_sched_barrier(0);
@@ -266,17 +287,19 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile(
 #pragma unroll
         for (int m = 0; m < R * WN; ++m) {
           const int r = m / WN, j = m % WN;
-          acc[P + r][j] = mfma_w4a8(wf[j], xr[r], acc[P + r][j], sc[j] >> (8 * (kt & 3)));
+          acc[P + r][j] = mfma_w4a8(wf[j], xr[r], acc[P + r][j], sc[j] >> (8 * q));
           __builtin_amdgcn_sched_barrier(0);
           if (m < WN) {
             wfn[m] = *reinterpret_cast<const v4i*>(nbase + S::W_OFF + (wn * WN + m) * 1024 +
                                                    lane * 16);
-            scn[m] = *reinterpret_cast<const uint32_t*>(srow + (wn * WN + m) * 256);
+            // a k-group's scale dwords serve its 4 slabs: read them only for its first slab
+            if constexpr (q == 3)
+              scn[m] = *reinterpret_cast<const uint32_t*>(srow + (wn * WN + m) * 256);
           }
           if (m == WN) read_a(nst, 0, lon, hin);
 #pragma unroll
-          for (int o = m * S::OPS / (R * WN); o < (m + 1) * S::OPS / (R * WN); ++o)
-            fill_op(kt + NS, fbase, o);
+          for (int o = m * NF / (R * WN); o < (m + 1) * NF / (R * WN); ++o)
+            fill_any(kt + NS, fbase, o);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
@@ -284,10 +307,19 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile(
       // here, the compiler does not make the next slab's first MFMAs wait on every LDS read
       __builtin_amdgcn_s_waitcnt(0xC07F);
 #pragma unroll
-      for (int j = 0; j < WN; ++j) wf[j] = wfn[j], sc[j] = scn[j];
+      for (int j = 0; j < WN; ++j) {
+        wf[j] = wfn[j];
+        if constexpr (q == 3) sc[j] = scn[j];
+      }
       lo = lon;
       hi = hin;
       st = nst;
+    };
+    for (int kt = 0; kt < KT4; kt += 4) {
+      slab(kt, IntC<0>{});
+      slab(kt + 1, IntC<1>{});
+      slab(kt + 2, IntC<2>{});
+      slab(kt + 3, IntC<3>{});
     }
   } else {
     // ---- NS-stage pipeline, barrier at the head of each slab: slab kt+NS-1 is requested in
@@ -296,8 +328,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile(
 #pragma unroll
     for (int p = 0; p < NS - 1; ++p) fill(p, p);
     int st = 0;
-    for (int kt = 0; kt < KTe; ++kt) {
-      wait_vmcnt<(NS - 2) * S::OPS>();           // this wave's fills of slab kt have landed
+    auto slab = [&](int kt, auto qc) {
+      constexpr int q = decltype(qc)::value;    // kt % 4
+      constexpr int NF = S::fills(q + NS - 1);   // fills of the refill, slab kt + NS - 1
+      wait_vmcnt<S::fills_after(q, NS - 2)>();   // this wave's fills of slab kt have landed
       bare_barrier();                            // ... and every wave's; slab kt-1 is consumed
       const int fst = st == 0 ? NS - 1 : st - 1; // stage of slab kt+NS-1 == stage of slab kt-1
       uint8_t* fbase = lds + fst * S::STAGE;
@@ -310,15 +344,21 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile(
         const v8i xf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         if (i + 1 < WM) read_a(st, i + 1, lo, hi);
 #pragma unroll
-        for (int o = i * S::OPS / WM; o < (i + 1) * S::OPS / WM; ++o)
-          fill_op(kt + NS - 1, fbase, o);
+        for (int o = i * NF / WM; o < (i + 1) * NF / WM; ++o)
+          fill_any(kt + NS - 1, fbase, o);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < WN; ++j)
-          acc[i][j] = mfma_w4a8(wf[j], xf, acc[i][j], sc[j] >> (8 * (kt & 3)));
+          acc[i][j] = mfma_w4a8(wf[j], xf, acc[i][j], sc[j] >> (8 * q));
         __builtin_amdgcn_sched_barrier(0);
       }
       st = st + 1 == NS ? 0 : st + 1;
+    };
+    for (int kt = 0; kt < KT4; kt += 4) {
+      slab(kt, IntC<0>{});
+      slab(kt + 1, IntC<1>{});
+      slab(kt + 2, IntC<2>{});
+      slab(kt + 3, IntC<3>{});
     }
   }
   wait_vmcnt<0>();                               // no fill may outlive the workgroup's LDS
@@ -381,7 +421,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile(
 
 #define W4A8_TILE_CFG(wm, wn, ns, nw)                                                             \
   TileCfg{wm, wn, TileShape<wm, wn, nw>::BM, TileShape<wm, wn, nw>::BN, nw,                        \
-          ns * TileShape<wm, wn, nw>::STAGE + 3 * TileShape<wm, wn, nw>::S_SLOT +                \
+          ns * TileShape<wm, wn, nw>::STAGE + 3 * TileShape<wm, wn, nw>::S_SLOT + 1024 +         \
               TileShape<wm, wn, nw>::TSCALE},
 constexpr TileCfg kTile[] = {W4A8_TILE_TABLE(W4A8_TILE_CFG)};
 #undef W4A8_TILE_CFG
