@@ -12,8 +12,9 @@ duration comes from HIP event pairs around individual launches on the launch str
 
 Alongside: the M=4096 prefill GEMMs (gate_up 17408x5120, down 5120x8704) in TFLOP/s against the
 fp8 x fp4 MFMA peak, the M=1 per-layer linear set, the fused producers and the per-token quantizer
-at M=8 and M=4096 in GB/s, and the CPU baseline (the oracle's dequant + fp32 matmul, timed on this
-host). Prints ONE JSON line.
+at M=8 and M=4096 in GB/s, the register-resident MFMA rate and a streaming read of the verify
+GEMM's bytes in its launch shape (the HBM ceiling it is held against), and the CPU baseline (the
+oracle's dequant + fp32 matmul, timed on this host). Prints ONE JSON line.
 
   python bench.py [--gpus 1] [--steps 1024] [--warmup 64]
 """
@@ -309,6 +310,37 @@ def bench_producers():
     return res
 
 
+class ReadProbe:
+    """`copies` device buffers of `nbytes` each, read by w4a8_read_probe (the decode GEMM's launch
+    shape over plain bytes)."""
+
+    def __init__(self, nbytes, copies):
+        import torch
+        from vllm_sly_radiance_amd import _native
+        self.n, self._native = nbytes, _native
+        self.w = [torch.full((nbytes,), i + 1, dtype=torch.uint8, device="cuda")
+                  for i in range(copies)]
+        self.out = torch.zeros(1, dtype=torch.int32, device="cuda")
+        torch.cuda.synchronize()
+
+    def launch(self, i, stream):
+        self._native.read_probe(self.w[i].data_ptr(), self.n, self.out.data_ptr(), stream)
+
+
+def bench_read_probe(steps, warmup):
+    """The HBM read ceiling for the verify GEMM: as many bytes per launch as its algorithmic
+    traffic, the same rotation over 16 copies and the same graph replay, nothing but reads."""
+    import torch
+    g = ReadProbe(gemm_bytes(VERIFY["M"], VERIFY["N"], VERIFY["K"]), COPIES)
+    n_steps, _, sec, _, _ = graph_timed(g, steps, warmup, warm_seconds=0.5)
+    us = sec / n_steps * 1e6
+    gbs = g.n / (us * 1e-6) / 1e9
+    del g
+    torch.cuda.empty_cache()
+    return dict(bytes=gemm_bytes(VERIFY["M"], VERIFY["N"], VERIFY["K"]), us=round(us, 3),
+                gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4))
+
+
 def mfma_probe():
     """Register-resident rate of the scaled MFMA the GEMMs issue (fp4 A x fp8 B), both shapes."""
     import torch
@@ -600,6 +632,9 @@ def main():
         print(f"[bench] quantizer: {quant}", file=sys.stderr, flush=True)
     probe = mfma_probe()
     print(f"[bench] MFMA probe TFLOP/s: {probe}", file=sys.stderr, flush=True)
+    rprobe = bench_read_probe(args.steps, args.warmup)
+    print(f"[bench] HBM read probe (verify-GEMM shape and bytes): {rprobe}", file=sys.stderr,
+          flush=True)
     cpu = None if args.no_cpu else cpu_baseline()
     achieved = v["bytes"] / (v["kernel_us"] * 1e-6) / 1e9
     line = {
@@ -627,6 +662,8 @@ def main():
         "event_pair_us_median": round(v["event_pair_us_median"], 3),
         "prefill_m4096": prefill,
         "mfma_probe_tflops": probe,
+        "hbm_read_probe": rprobe,
+        "value_vs_read_probe": round(v["gbs"] / rprobe["gbs"], 4),
         "decode_m1_layer": layer,
         "producers": producers,
         "quantizer": quant,

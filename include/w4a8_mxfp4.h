@@ -154,6 +154,14 @@ int w4a8_gdn_norm_quant(const void* x, const void* z, long z_stride, const void*
  * sly/mxfp4/radiance_mxfp4_fp8.hip:6-10. */
 int w4a8_mfma_probe(int shape, float* out, int blocks, int iters, double* flop, void* stream);
 
+/* Diagnostic: streaming read of `bytes` (1 .. 2^31 - 2^20, 16-byte aligned buffer) with the
+ * decode GEMM's launch shape (10-wave workgroups, 20 KiB of 128-bit loads in flight per wave,
+ * all issued before any is used); out receives nothing unless the data xor to a fixed pattern.
+ * The caller times it: the HBM read ceiling the M <= 16 GEMMs are compared against. No
+ * counterpart in the reference, which quotes its decode kernel against the GDDR6 specification
+ * (autoround-tests/RESULTS.md:404-405). */
+int w4a8_read_probe(const void* buf, long bytes, int* out, void* stream);
+
 /* Diagnostic: `count` independent scaled MFMAs (16x16x128, fp4 e2m1 A x fp8 e4m3 B, the instruction
  * every GEMM here issues) on raw lane operands, one wave per tile: a [count][64][4] dwords (16 fp4
  * bytes per lane), b [count][64][8] dwords (32 fp8 bytes per lane), sa / sb [count][64] scale

@@ -173,3 +173,12 @@ def test_producers_validate_before_launch(lib):
     assert lib.w4a8_gdn_norm_quant(p, p, 132, p, p, p, 4, 128, 1e-6, None) == 1     # stride % 8
     assert b"stride" in lib.w4a8_last_error()
     assert lib.w4a8_gdn_norm_quant(p, p + 8, 256, p, p, p, 4, 128, 1e-6, None) == 1  # z misaligned
+
+
+def test_read_probe_validates_before_launch(lib):
+    p = 4096
+    assert lib.w4a8_read_probe(None, 1024, p, None) == 1
+    assert lib.w4a8_read_probe(p, 0, p, None) == 1
+    assert lib.w4a8_read_probe(p + 4, 1024, p, None) == 1                         # misaligned
+    assert lib.w4a8_read_probe(p, 1 << 31, p, None) == 1
+    assert b"w4a8_read_probe" in lib.w4a8_last_error()

@@ -440,3 +440,16 @@ def test_split_k_reduction_has_no_race(gpu_lib, scratch):
         for j in range(2):
             miss = int((outs[j] != gold[j]).flatten(1).any(1).sum())
             assert miss == 0, f"split {ks}: {miss}/64 launches differ from golden {j}"
+
+
+# ---- diagnostics --------------------------------------------------------------------------------
+@pytest.mark.parametrize("nbytes", [1000, 204800, 47_669_280])
+def test_read_probe_reads_without_writing(gpu_lib, nbytes):
+    """The HBM read probe over buffers shorter than, equal to and longer than one workgroup's
+    share: it runs, and with data that never xors to its pattern it writes nothing."""
+    buf = torch.full((nbytes + 16,), 3, dtype=torch.uint8, device="cuda")
+    out = torch.zeros(2, dtype=torch.int32, device="cuda")
+    print(f"[probe] read {nbytes} B", flush=True)
+    _native.read_probe(buf.data_ptr(), nbytes, out.data_ptr(), stream())
+    torch.cuda.synchronize()
+    assert out.cpu().tolist() == [0, 0]

@@ -41,6 +41,7 @@ SIGNATURES = {
     "w4a8_silu_mul_quant": (_int, [_vp, _vp, _vp, _int, _int, _vp]),
     "w4a8_gdn_norm_quant": (_int, [_vp, _vp, _long, _vp, _vp, _vp, _int, _int, _c.c_float, _vp]),
     "w4a8_mfma_probe": (_int, [_int, _vp, _int, _int, _c.POINTER(_c.c_double), _vp]),
+    "w4a8_read_probe": (_int, [_vp, _long, _vp, _vp]),
     "w4a8_mfma_tile": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _vp]),
 }
 
@@ -142,6 +143,10 @@ def scratch_bytes(variant: int, N: int, split_k: int):
     a, b = _sz(), _sz()
     check(lib().w4a8_scratch_bytes(variant, N, split_k, _c.byref(a), _c.byref(b)))
     return a.value, b.value
+
+
+def read_probe(buf_ptr, nbytes, out_ptr, stream) -> None:
+    check(lib().w4a8_read_probe(buf_ptr, nbytes, out_ptr, stream))
 
 
 def mfma_probe(shape, out_ptr, blocks, iters, stream) -> float:

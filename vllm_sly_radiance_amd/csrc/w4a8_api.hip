@@ -459,6 +459,14 @@ W4A8_API int w4a8_gdn_norm_quant(const void* x, const void* z, long z_stride, co
                     "w4a8_gdn_norm_quant");
 }
 
+W4A8_API int w4a8_read_probe(const void* buf, long bytes, int* out, void* stream) {
+  if (!buf || !out || bytes <= 0 || bytes > (1L << 31) - (1L << 20) || !aligned(buf, 16))
+    return fail(W4A8_EINVAL,
+                "w4a8_read_probe: need a 16-byte aligned buffer of 1 .. 2^31 - 2^20 bytes and out");
+  return hip_status(launch_read_probe(buf, (int)bytes, out, (hipStream_t)stream),
+                    "w4a8_read_probe");
+}
+
 W4A8_API int w4a8_mfma_probe(int shape, float* out, int blocks, int iters, double* flop,
                              void* stream) {
   if ((shape != 0 && shape != 1) || !out || !flop || blocks <= 0 || iters <= 0)

@@ -155,6 +155,7 @@ bool tile_fits(int M, int N, int K);
 hipError_t launch_tile(const GemmArgs& g, int variant, hipStream_t stream);
 
 // Register-resident MFMA throughput probe (shape 0: 16x16x128, 1: 32x32x64).
+hipError_t launch_read_probe(const void* buf, int bytes, int* out, hipStream_t stream);
 hipError_t launch_mfma_probe(int shape, float* out, int blocks, int iters, double* flop,
                              hipStream_t stream);
 // Raw scaled-MFMA tiles on caller-given lane operands (layout diagnostic).

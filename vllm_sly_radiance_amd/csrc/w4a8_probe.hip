@@ -5,6 +5,10 @@
 // Each wave runs 8 independent accumulator chains so the issue rate, not the dependency latency,
 // bounds it; operands never leave registers. One thread per wave writes a checksum so nothing is
 // optimised away.
+//
+// Also a streaming-read probe with the decode GEMM's launch shape, the HBM ceiling the verify GEMM
+// is compared against: 10-wave workgroups, every wave holding 20 KiB of 128-bit loads in flight,
+// all issued before any is used (the shape of gemm_stream<5, 4, 10>), over one buffer.
 #include "w4a8_internal.h"
 
 namespace w4a8 {
@@ -76,7 +80,35 @@ __global__ __launch_bounds__(256) void mfma_tiles(const int* __restrict__ a,
   pd[3] = acc[3];
 }
 
+// Wave w of the grid reads bytes [w * kReadRun, (w + 1) * kReadRun) of buf as 64-lane 16-byte
+// loads (non-temporal, like the GEMM's weight stream); loads past `bytes` return zero. The
+// xor of everything read goes to out[0] only if it equals a value no data here produces.
+constexpr int kReadWaves = 10, kReadUnits = 20, kReadRun = kReadUnits * 1024;
+
+__global__ __launch_bounds__(kReadWaves * 64) void read_stream(const uint8_t* __restrict__ buf,
+                                                              int bytes, int* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int w = blockIdx.x * kReadWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const auto rs = __builtin_amdgcn_make_buffer_rsrc((void*)buf, 0, bytes, kBufferWord3);
+  v4i v[kReadUnits];
+#pragma unroll
+  for (int u = 0; u < kReadUnits; ++u)
+    v[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, w * kReadRun + u * 1024 + lane * 16, 0,
+                                                 kBufferNT);
+  v4i acc = v[0];
+#pragma unroll
+  for (int u = 1; u < kReadUnits; ++u) acc ^= v[u];
+  if ((acc[0] ^ acc[1] ^ acc[2] ^ acc[3]) == 0x5A17C0DE) out[0] = w;
+}
+
 }  // namespace
+
+hipError_t launch_read_probe(const void* buf, int bytes, int* out, hipStream_t stream) {
+  const int blocks = ceil_div(ceil_div(bytes, kReadRun), kReadWaves);
+  hipLaunchKernelGGL(read_stream, dim3(blocks), dim3(kReadWaves * 64), 0, stream,
+                     (const uint8_t*)buf, bytes, out);
+  return hipGetLastError();
+}
 
 hipError_t launch_mfma_tiles(const int* a, const int* b, const int* sa, const int* sb, float* d,
                              int count, hipStream_t stream) {
