@@ -453,3 +453,28 @@ def test_read_probe_reads_without_writing(gpu_lib, nbytes):
     _native.read_probe(buf.data_ptr(), nbytes, out.data_ptr(), stream())
     torch.cuda.synchronize()
     assert out.cpu().tolist() == [0, 0]
+
+
+def random_shapes(count, seed):
+    """Seeded (M, N, K): M over the decode, skinny and tile bands, ragged N, K any multiple of 32."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(count):
+        M = int(rng.choice([rng.integers(1, 17), rng.integers(17, 65), rng.integers(65, 700)]))
+        N = int(rng.integers(1, 2600))
+        K = int(32 * rng.integers(1, 97))
+        out.append((M, N, K))
+    return out
+
+
+@pytest.mark.parametrize("M,N,K", random_shapes(18, 2024))
+def test_gemm_random_shapes_planned(gpu_lib, M, N, K):
+    """The automatic plan on seeded random shapes, every output against the oracle."""
+    x = synthetic.activations(M, K, seed=M * 31 + K)
+    w, ws = synthetic.weights(N, K, seed=N * 7 + K)
+    q, s = O.quant_per_token(x)
+    wq, sq = gpu_repack(w, ws)
+    plan = _native.plan(M, N, K)
+    print(f"[random] M={M} N={N} K={K} plan {plan}", flush=True)
+    out = gpu_gemm(q, s, wq, sq, N, K)
+    assert_gemm_close(out, q, s, w, ws, f"random M={M} N={N} K={K} plan {plan}")
