@@ -122,10 +122,13 @@ def test_plan_bands(lib):
     # small M: the smallest tile whose workgroup count stays within 5/8 of 256 CUs
     (32, 10240, 5120, (32, 64)), (32, 17408, 5120, (32, 128)), (64, 17408, 5120, (64, 128)),
     (64, 5120, 8704, (32, 64)), (128, 5120, 6144, (32, 128)), (128, 17408, 5120, (128, 128)),
-    (256, 17408, 5120, (128, 128)), (512, 17408, 5120, (128, 128)),
+    (256, 17408, 5120, (128, 128)),
+    # 256 < M < 1024: 256 x 160 when those tiles fill one round at least half, else 128 x 128
+    (512, 17408, 5120, (256, 160)), (512, 10240, 5120, (256, 160)), (512, 5120, 8704, (128, 128)),
+    (768, 17408, 5120, (128, 128)),
     # prefill: 256 x 256 (8 waves) for wide N, 256 x 160 when N splits into 160-column tiles
     (1024, 17408, 5120, (256, 256)), (4096, 17408, 5120, (256, 256)),
-    (4096, 5120, 8704, (256, 160))])
+    (1024, 10240, 5120, (256, 160)), (4096, 5120, 8704, (256, 160))])
 def test_plan_tile_shapes(lib, M, N, K, tile):
     k, v, s = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     assert lib.w4a8_plan(M, N, K, ctypes.byref(k), ctypes.byref(v), ctypes.byref(s)) == 0

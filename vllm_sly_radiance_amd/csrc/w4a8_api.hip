@@ -100,10 +100,11 @@ int find_skinny(int mt, int nt, int waves) {
   return -1;
 }
 
-int find_tile(int wm, int wn, int nw = 4) {
+// The first tile variant of the shape (WM, WN, NW), or of that shape and NS stages (ns > 0).
+int find_tile(int wm, int wn, int nw = 4, int ns = 0) {
   for (int v = 0; v < tile_variant_count(); ++v) {
     const TileCfg c = tile_variant(v);
-    if (c.wm == wm && c.wn == wn && c.nw == nw) return v;
+    if (c.wm == wm && c.wn == wn && c.nw == nw && (ns == 0 || c.ns == ns)) return v;
   }
   return -1;
 }
@@ -171,15 +172,23 @@ void plan_impl(int M, int N, int K, int dev, int* kernel, int* variant, int* spl
     *split_k = ks;
     return;
   }
-  // Prefill band (measured on MI355X): 8-wave 256 x 256 tiles for wide N (the automatic path
-  // splits N so the last round of these one-per-CU workgroups is not mostly idle, see
-  // tile_split), 256 x 160 where N divides into 160-column tiles that fill the CUs evenly
-  // (N = 5120: 512 tiles at M = 4096), 128 x 128 below M = 1024, and the small-M rule below that.
+  // Prefill band (measured on MI355X, every tile variant on the four Qwen3.8-27B linear shapes at
+  // M = 32 .. 2048): 8-wave 256 x 256 tiles for wide N (the automatic path splits N so the last
+  // round of these one-per-CU workgroups is not mostly idle, see tile_split), 256 x 160 where N
+  // divides into 160-column tiles (N = 5120: 512 tiles at M = 4096; N = 10240 at M = 1024: 256
+  // tiles, 44 against 56 us on 256 x 256), 128 x 128 below M = 1024 unless 256 x 160 tiles fill
+  // one round at least half (N = 17408 at M = 512: 218 tiles, 43 against 58 us), and the small-M
+  // rule below that. 128 x 128 tiles run 4 stages when they fit one round (N = 5120 at M = 512:
+  // 24 against 26 us for o_proj, 32 against 35 us for down), 3 when they take several rounds.
   *kernel = W4A8_KERNEL_TILE;
-  if (M >= 1024 && N % 160 == 0 && N <= 8192) *variant = find_tile(4, 5, 8);
+  const int cus = device_info(dev).cus;
+  const long t160 = (long)ceil_div(M, 256) * ceil_div(N, 160);
+  const long t128 = (long)ceil_div(M, 128) * ceil_div(N, 128);
+  if (M >= 1024 && N % 160 == 0) *variant = find_tile(4, 5, 8);
   else if (M >= 1024) *variant = find_tile(4, 8, 8);
-  else if (M > 256) *variant = find_tile(4, 4);
-  else *variant = small_m_tile(M, N, device_info(dev).cus);
+  else if (M > 256 && 2 * t160 >= cus && t160 <= cus) *variant = find_tile(4, 5, 8);
+  else if (M > 256) *variant = find_tile(4, 4, 4, t128 <= cus ? 4 : 3);
+  else *variant = small_m_tile(M, N, cus);
   *split_k = 1;
 }
 
@@ -197,7 +206,9 @@ int tile_split(int M, int N, int variant, int dev, int* tail_variant) {
   if (total < slots || total % slots == 0 || 2 * (total % slots) >= slots) return 0;
   int nbm = nb - 1;
   while (nbm > 0 && ((long)mb * nbm) % slots) --nbm;
-  const int tv = find_tile(4, 4);
+  // the tail's 128 x 128 tiles: 4 stages when they fit one round (the plan's rule)
+  const long tail_tiles = (long)ceil_div(M, 128) * ceil_div(N - nbm * c.bn, 128);
+  const int tv = find_tile(4, 4, 4, tail_tiles <= slots ? 4 : 3);
   if (nbm <= 0 || tv < 0) return 0;
   *tail_variant = tv;
   return nbm * c.bn;

@@ -422,7 +422,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile(
 #define W4A8_TILE_CFG(wm, wn, ns, nw)                                                             \
   TileCfg{wm, wn, TileShape<wm, wn, nw>::BM, TileShape<wm, wn, nw>::BN, nw,                        \
           ns * TileShape<wm, wn, nw>::STAGE + 3 * TileShape<wm, wn, nw>::S_SLOT + 1024 +         \
-              TileShape<wm, wn, nw>::TSCALE},
+              TileShape<wm, wn, nw>::TSCALE,                                                     \
+          ns},
 constexpr TileCfg kTile[] = {W4A8_TILE_TABLE(W4A8_TILE_CFG)};
 #undef W4A8_TILE_CFG
 constexpr int kTileCount = sizeof(kTile) / sizeof(kTile[0]);

@@ -148,7 +148,7 @@ hipError_t launch_stream(const GemmArgs& g, int variant, int cus, hipStream_t st
 
 // Macro-tile family (M > 16). variant indexes the instantiated (WM, WN, NS, NW) table: nw waves of
 // wm x wn 16 x 16 MFMA tiles, a bm x bn workgroup tile.
-struct TileCfg { int wm, wn, bm, bn, nw, lds; };
+struct TileCfg { int wm, wn, bm, bn, nw, lds, ns; };
 int tile_variant_count();
 TileCfg tile_variant(int v);
 bool tile_fits(int M, int N, int K);
