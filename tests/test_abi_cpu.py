@@ -119,10 +119,12 @@ def test_plan_bands(lib):
 
 
 @pytest.mark.parametrize("M,N,K,tile", [
-    # small M: the smallest tile whose workgroup count stays within 5/8 of 256 CUs
+    # small M: the first tile (32x64, 64x64, 32x128, 64x128, 128x128, 128x256) whose workgroup
+    # count stays within 5/8 of 256 CUs
     (32, 10240, 5120, (32, 64)), (32, 17408, 5120, (32, 128)), (64, 17408, 5120, (64, 128)),
-    (64, 5120, 8704, (32, 64)), (128, 5120, 6144, (32, 128)), (128, 17408, 5120, (128, 128)),
-    (256, 17408, 5120, (128, 128)),
+    (64, 5120, 8704, (32, 64)), (64, 10240, 5120, (64, 64)), (128, 5120, 6144, (64, 64)),
+    (128, 17408, 5120, (128, 128)), (256, 10240, 5120, (128, 128)),
+    (256, 17408, 5120, (128, 256)),
     # 256 < M < 1024: 256 x 160 when those tiles fill one round at least half, else 128 x 128
     (512, 17408, 5120, (256, 160)), (512, 10240, 5120, (256, 160)), (512, 5120, 8704, (128, 128)),
     (768, 17408, 5120, (128, 128)),

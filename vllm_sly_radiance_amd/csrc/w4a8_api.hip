@@ -132,15 +132,21 @@ int find_stream(int M, int N, int K, int dev) {
   return best;
 }
 
-// Smallest-area macro tile, in the order 32x64, 32x128, 64x128, 128x128, whose workgroup count
-// stays within 5/8 of the CUs: at M <= 256 the tile GEMM streams the weights once per row block,
-// and on MI355X fewer, longer workgroups beat one workgroup per CU (measured on the Qwen3.8-27B
-// linear shapes at M = 24..256).
+// The first macro tile, in the order 32x64, 64x64 (5 stages), 32x128, 64x128, 128x128, 128x256
+// (4 stages), whose workgroup count stays within 5/8 of the CUs: at M <= 256 the tile GEMM
+// streams the weights once per row block, and on MI355X fewer, longer workgroups beat one
+// workgroup per CU (measured on the Qwen3.8-27B linear shapes at M = 24..256; 64x64 beats 32x128
+// at the same count, e.g. down at M = 128: 17.5 against 19.5 us). 128x128 runs 4 stages when it
+// fits one round.
 int small_m_tile(int M, int N, int cus) {
-  static const int cand[][2] = {{1, 2}, {1, 4}, {2, 4}, {4, 4}};
+  static const int cand[][3] = {{1, 2, 0}, {2, 2, 5}, {1, 4, 0}, {2, 4, 0}, {4, 4, 0}, {4, 8, 4}};
   for (const auto& c : cand) {
     const int bm = 32 * c[0], bn = 32 * c[1];
-    if ((long)ceil_div(M, bm) * ceil_div(N, bn) <= (long)cus * 5 / 8) return find_tile(c[0], c[1]);
+    const long tiles = (long)ceil_div(M, bm) * ceil_div(N, bn);
+    if (tiles <= (long)cus * 5 / 8) {
+      const int ns = c[2] ? c[2] : (c[0] == 4 && c[1] == 4 ? (tiles <= cus ? 4 : 3) : 0);
+      return find_tile(c[0], c[1], 4, ns);
+    }
   }
   return find_tile(4, 4);
 }
