@@ -286,14 +286,15 @@ def bench_quant():
 
 
 # (op, width) at the benchmark model's shapes: the decoder norms feed K = 5120, the MLP activation
-# N = 17408, the GatedDeltaNet output projection N = 6144 (48 heads of 128)
-PRODUCERS = [("add_rms", 5120), ("silu", 17408), ("gdn", 6144)]
+# N = 8704 (the gate_up GEMM's 17408 columns are gate and up; down has K = 8704), the GatedDeltaNet
+# output projection N = 6144 (48 heads of 128)
+PRODUCERS = [("add_rms", 5120), ("silu", 8704), ("gdn", 6144)]
 
 
 def bench_producers():
     import torch
     from vllm_sly_radiance_amd import radiance_mxfp4 as R
-    R.ensure_scratch("cuda")          # as after the plugin's first layer: silu splits small-M rows
+    R.ensure_scratch("cuda")          # as after the plugin's first layer (silu's split path)
     res = []
     for M in (8, 4096):
         for kind, N in PRODUCERS:

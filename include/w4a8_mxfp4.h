@@ -133,10 +133,18 @@ int w4a8_add_rms_quant(const void* y, const void* residual, const void* weight, 
 /* SiLU-and-mul, then quant: gate_up bf16 [M, 2N] (gate = columns 0..N-1, up = N..2N-1) ->
  * x = bf16(bf16(silu(gate)) * up), q [M, N]; N % 8 == 0, N <= 18432. Replaces
  * launch_silu_mul_quant (sly/mxfp4/radiance_mxfp4_fp8.hip:2019-2066; kernel :1935-2010), behind
- * radiance::silu_mul_quant (sly/mxfp4/radiance_fused_norm.py:163-187). At M <= 64 with scratch
- * registered by w4a8_set_scratch (M * ceil(N / 512) * 4 bytes of partials), rows are split over
- * several workgroups in two launches; the results are the same bits either way. */
+ * radiance::silu_mul_quant (sly/mxfp4/radiance_fused_norm.py:163-187). At M <= 64 and
+ * N > 16384 with scratch registered by w4a8_set_scratch (M * ceil(N / 512) * 4 bytes of
+ * partials), rows are split over several workgroups in two launches; the results are the same
+ * bits either way. */
 int w4a8_silu_mul_quant(const void* gate_up, void* q, float* scale, int M, int N, void* stream);
+
+/* The bf16 stage of w4a8_silu_mul_quant without the quantization: out bf16 [M, N] =
+ * bf16(bf16(silu(gate)) * up), the same bits the fused op quantizes; gate_up and out 16-byte
+ * aligned, N % 8 == 0, N <= 18432. The reference swaps vLLM's SiluAndMul for the fused op
+ * (sly/mxfp4/radiance_fused_norm.py:271) and has no bf16-output kernel of its own; this entry
+ * point serves callers that need the bf16 activation and lets the stage be tested bit for bit. */
+int w4a8_silu_mul(const void* gate_up, void* out, int M, int N, void* stream);
 
 /* Per-head gated RMSNorm (heads of 128, norm before the gate, silu gate, weight without +1), then
  * quant: x = bf16(x * rsqrt(mean_head(x^2) + eps) * weight * silu(z)). x bf16 [M, N] contiguous,

@@ -172,6 +172,11 @@ def test_producers_validate_before_launch(lib):
     assert lib.w4a8_silu_mul_quant(p, p, p, 4, 18440, None) == 1
     assert lib.w4a8_silu_mul_quant(p, p + 4, p, 4, 16, None) == 1                  # q misaligned
     assert lib.w4a8_silu_mul_quant(None, None, None, 0, 16, None) == 0
+    assert lib.w4a8_silu_mul(p, p, 4, 12, None) == 1
+    assert b"w4a8_silu_mul: N must be 8-aligned" in lib.w4a8_last_error()
+    assert lib.w4a8_silu_mul(p, p + 8, 4, 16, None) == 1                           # out misaligned
+    assert lib.w4a8_silu_mul(p, None, 4, 16, None) == 1
+    assert lib.w4a8_silu_mul(None, None, 0, 16, None) == 0
     assert lib.w4a8_gdn_norm_quant(p, p, 256, p, p, p, 4, 200, 1e-6, None) == 1
     assert b"multiple of 128" in lib.w4a8_last_error()
     assert lib.w4a8_gdn_norm_quant(p, p, 100, p, p, p, 4, 128, 1e-6, None) == 1     # stride < N

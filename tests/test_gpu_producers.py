@@ -115,8 +115,8 @@ def gpu_silu(gu):
     return host_u8(q), s.cpu().numpy()
 
 
-# M <= 64 splits rows (with scratch) or runs 1024-thread rows, M <= 128 runs 1024-thread rows,
-# larger M 256-thread rows: all must give the same bits
+# M <= 64 splits rows of N > 16384 (with scratch) or runs 1024-thread rows, M <= 128 runs
+# 1024-thread rows, larger M 256-thread rows: all must give the same bits
 @pytest.mark.parametrize("M,N", [(1, 17408), (8, 17408), (33, 1000), (2, 18432), (64, 8704),
                                  (96, 8704), (4, 8), (200, 17408), (129, 18432), (16, 520)])
 def test_silu_mul_quant_bit_exact(producer_path, M, N):
@@ -137,6 +137,44 @@ def test_silu_mul_quant_special_and_wide_range(producer_path):
     q, s = gpu_silu(gu)
     oq, os_ = P.silu_mul_quant(gu)
     assert_same_qs(q, s, oq, os_, "silu special")
+
+
+def all_gates(M, N, seed):
+    """[M, 2N] bf16 bits whose gate halves hold each of the 65536 bf16 patterns (shuffled; M N >=
+    65536, the rest random patterns), with finite random up values."""
+    rng = np.random.default_rng(seed)
+    extra = rng.integers(0, 65536, M * N - 65536)
+    gate = rng.permutation(np.r_[np.arange(65536), extra]).astype(np.uint16).reshape(M, N)
+    up = O.f32_to_bf16((rng.standard_normal((M, N)) * 3).astype(np.float32))
+    return np.concatenate([gate, up], axis=1)
+
+
+@pytest.mark.parametrize("M,N", [(4, 17408), (8, 8192), (256, 256)])
+def test_silu_mul_bf16_stage_every_gate(gpu_lib, M, N):
+    """The bf16 stage over every bf16 gate, bit for bit (exp's overflow, underflow and clamp,
+    the subnormal results, zero, inf and NaN gates), at 1024-thread rows of 3 and 1 groups per
+    thread and at 256-thread rows."""
+    gu = all_gates(M, N, seed=M)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    gd = bf16_dev(gu)
+    print(f"[producers] silu_mul M={M} N={N}", flush=True)
+    _native.silu_mul(gd.data_ptr(), out.data_ptr(), M, N, stream())
+    torch.cuda.synchronize()
+    got = host_u16(out)
+    ref = P.silu_mul(gu)
+    bad = np.argwhere(got != ref)
+    assert bad.size == 0, [(int(r), int(c), hex(int(gu[r, c])), hex(int(got[r, c])),
+                            hex(int(ref[r, c]))) for r, c in bad[:6]]
+
+
+@pytest.mark.parametrize("M,N", [(4, 17408), (32, 2048), (256, 256)])
+def test_silu_mul_quant_every_gate(producer_path, M, N):
+    """Every gate through the fused op: split rows (M = 4 with scratch), 1024- and 256-thread
+    rows."""
+    gu = all_gates(M, N, seed=M + 1)
+    q, s = gpu_silu(gu)
+    oq, os_ = P.silu_mul_quant(gu)
+    assert_same_qs(q, s, oq, os_, f"silu every gate M={M}")
 
 
 def gpu_gdn(x, z_wide, col0, w, eps):

@@ -39,6 +39,7 @@ SIGNATURES = {
     "w4a8_linear": (_int, [_vp, _long, _vp, _vp, _vp, _vp, _vp, _int, _int, _int, _vp]),
     "w4a8_add_rms_quant": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _int, _int, _c.c_float, _vp]),
     "w4a8_silu_mul_quant": (_int, [_vp, _vp, _vp, _int, _int, _vp]),
+    "w4a8_silu_mul": (_int, [_vp, _vp, _int, _int, _vp]),
     "w4a8_gdn_norm_quant": (_int, [_vp, _vp, _long, _vp, _vp, _vp, _int, _int, _c.c_float, _vp]),
     "w4a8_mfma_probe": (_int, [_int, _vp, _int, _int, _c.POINTER(_c.c_double), _vp]),
     "w4a8_read_probe": (_int, [_vp, _long, _vp, _vp]),
@@ -104,6 +105,10 @@ def add_rms_quant(y_ptr, res_ptr, w_ptr, q_ptr, s_ptr, res_out_ptr, M, K, eps, s
 
 def silu_mul_quant(gu_ptr, q_ptr, s_ptr, M, N, stream):
     check(lib().w4a8_silu_mul_quant(gu_ptr, q_ptr, s_ptr, M, N, stream))
+
+
+def silu_mul(gu_ptr, out_ptr, M, N, stream):
+    check(lib().w4a8_silu_mul(gu_ptr, out_ptr, M, N, stream))
 
 
 def gdn_norm_quant(x_ptr, z_ptr, z_stride, w_ptr, q_ptr, s_ptr, M, N, eps, stream):

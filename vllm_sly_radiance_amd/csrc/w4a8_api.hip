@@ -450,9 +450,21 @@ W4A8_API int w4a8_silu_mul_quant(const void* gate_up, void* q, float* scale, int
   const int dev = current_device();
   void* part = dev >= 0 ? (void*)g_scratch[dev].partial : nullptr;
   const size_t part_bytes = dev >= 0 ? g_scratch[dev].partial_bytes : 0;
-  return hip_status(launch_silu_mul_quant(gate_up, (uint8_t*)q, scale, M, N, part, part_bytes,
-                                          (hipStream_t)stream),
+  return hip_status(launch_silu_mul_quant(gate_up, (uint8_t*)q, scale, nullptr, M, N, part,
+                                          part_bytes, (hipStream_t)stream),
                     "w4a8_silu_mul_quant");
+}
+
+W4A8_API int w4a8_silu_mul(const void* gate_up, void* out, int M, int N, void* stream) {
+  if (M < 0 || N <= 0 || N % 8 || N > 18432)
+    return fail(W4A8_EINVAL, "w4a8_silu_mul: N must be 8-aligned and <= 18432 (M=%d N=%d)", M, N);
+  if (M == 0) return W4A8_OK;
+  if (!gate_up || !out) return fail(W4A8_EINVAL, "w4a8_silu_mul: null pointer");
+  if (!aligned(gate_up, 16) || !aligned(out, 16))
+    return fail(W4A8_EINVAL, "w4a8_silu_mul: gate_up and out need 16-byte alignment");
+  return hip_status(launch_silu_mul_quant(gate_up, nullptr, nullptr, out, M, N, nullptr, 0,
+                                          (hipStream_t)stream),
+                    "w4a8_silu_mul");
 }
 
 W4A8_API int w4a8_gdn_norm_quant(const void* x, const void* z, long z_stride, const void* weight,

@@ -117,10 +117,11 @@ hipError_t launch_add_rms_quant(const void* y, const void* res, const void* w, u
                                 float* scale, void* res_out, int M, int K, float eps,
                                 hipStream_t stream);
 // silu_mul splits rows of small M over several workgroups when `part` (the registered scratch)
-// holds producer_split_bytes(M, N); otherwise one workgroup per row. Same bits either way.
+// holds producer_split_bytes(M, N); otherwise one workgroup per row. Same bits either way. With
+// `out` set (bf16 [M, N]) it writes the bf16 stage instead of quantizing, one workgroup per row.
 size_t producer_split_bytes(int M, int N);
-hipError_t launch_silu_mul_quant(const void* gate_up, uint8_t* q, float* scale, int M, int N,
-                                 void* part, size_t part_bytes, hipStream_t stream);
+hipError_t launch_silu_mul_quant(const void* gate_up, uint8_t* q, float* scale, void* out, int M,
+                                 int N, void* part, size_t part_bytes, hipStream_t stream);
 hipError_t launch_gdn_norm_quant(const void* x, const void* z, long zs, const void* w, uint8_t* q,
                                  float* scale, int M, int N, float eps, hipStream_t stream);
 

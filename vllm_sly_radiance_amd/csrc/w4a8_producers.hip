@@ -190,10 +190,13 @@ __device__ __forceinline__ uint4 silu_mul_group(const uint4 gv, const uint4 uv) 
   return pack8<kSel>(p);
 }
 
+// One workgroup per row. With `out` set the bf16 stage is written there ([M, N]) and nothing is
+// quantized (the w4a8_silu_mul entry point); otherwise the row is quantized into q and scale.
 template <int G, int T>
 __global__ __launch_bounds__(T) void silu_mul_quant(const uint4* __restrict__ gu,
                                                     uint8_t* __restrict__ q,
-                                                    float* __restrict__ scale, int N) {
+                                                    float* __restrict__ scale,
+                                                    uint4* __restrict__ out, int N) {
   const int row = blockIdx.x, tid = threadIdx.x, nv = N >> 3;
   const uint4* gate = gu + (size_t)row * 2 * nv;
   const uint4* up = gate + nv;
@@ -202,6 +205,14 @@ __global__ __launch_bounds__(T) void silu_mul_quant(const uint4* __restrict__ gu
   for (int i = 0; i < G; ++i) {
     const int g = tid + i * T;
     if (g < nv) nb[i] = silu_mul_group<false>(gate[g], up[g]);
+  }
+  if (out) {
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const int g = tid + i * T;
+      if (g < nv) out[(size_t)row * nv + g] = nb[i];
+    }
+    return;
   }
   quant_tail<G, T>(nb, nv, q, scale, row);
 }
@@ -257,8 +268,10 @@ __global__ __launch_bounds__(T) void gdn_norm_quant(
 // to part[row * S + chunk]; pass 2 computes the chunk again (same code, same bits), takes the
 // row's amax over the S partials (max is exact in any order) and quantizes. The result equals the
 // one-workgroup kernel's bit for bit; the price is a second launch and computing the chunk twice
-// (6.1 us at 1 to 16 rows of 17408). gdn_norm rows (N <= 10240, cheaper per element) are faster
-// in one launch.
+// (5.8-6.0 us at 1 to 16 rows of 17408, against 8.4-8.6 us in one 1024-thread workgroup per row).
+// It pays only where a 1024-thread workgroup holds three or more groups per thread: at N = 8704
+// (two groups) one launch takes 5.4-6.1 us at 1 to 64 rows and the split 5.7-7.5 us. gdn_norm rows
+// (N <= 10240) are faster in one launch too.
 template <bool kQuant>
 __device__ __forceinline__ void split_tail(const uint4 nb, bool in, uint8_t* __restrict__ q,
                                            float* __restrict__ scale, uint32_t* __restrict__ part,
@@ -290,8 +303,9 @@ __global__ __launch_bounds__(64) void silu_mul_quant_split(const uint4* __restri
 
 }  // namespace
 
-// Rows at or below which silu_mul splits each row over one-wave workgroups (when the caller
-// registered scratch for the partial maxima); at 128 rows one workgroup per row is faster.
+// Rows at or below which silu_mul splits rows of more than 2048 groups (N > 16384) over one-wave
+// workgroups (when the caller registered scratch for the partial maxima); at 128 rows one
+// workgroup per row is faster.
 #ifndef W4A8_SPLIT_ROWS_MAX
 #define W4A8_SPLIT_ROWS_MAX 64
 #endif
@@ -301,7 +315,7 @@ size_t producer_split_bytes(int M, int N) { return (size_t)M * ceil_div(N >> 3, 
 
 // pass 2 reads a row's partials with one lane each
 bool split_rows(int M, int N, const void* part, size_t part_bytes) {
-  return M <= kSplitRowsMax && ceil_div(N >> 3, 64) <= 64 && part &&
+  return M <= kSplitRowsMax && (N >> 3) > 2 * 1024 && ceil_div(N >> 3, 64) <= 64 && part &&
          producer_split_bytes(M, N) <= part_bytes;
 }
 
@@ -326,10 +340,10 @@ hipError_t launch_add_rms_quant(const void* y, const void* res, const void* w, u
 // Rows of work per CU: with fewer rows than half the CUs, each row takes a 1024-thread workgroup.
 constexpr int kWideRowsMax = 128;
 
-hipError_t launch_silu_mul_quant(const void* gate_up, uint8_t* q, float* scale, int M, int N,
-                                 void* part, size_t part_bytes, hipStream_t stream) {
+hipError_t launch_silu_mul_quant(const void* gate_up, uint8_t* q, float* scale, void* out, int M,
+                                 int N, void* part, size_t part_bytes, hipStream_t stream) {
   if (M == 0) return hipSuccess;
-  if (split_rows(M, N, part, part_bytes)) {
+  if (!out && split_rows(M, N, part, part_bytes)) {
     const int S = ceil_div(N >> 3, 64);
     hipLaunchKernelGGL(silu_mul_quant_split<false>, dim3(S, M), dim3(64), 0, stream,
                        (const uint4*)gate_up, q, scale, (uint32_t*)part, N, S);
@@ -343,7 +357,7 @@ hipError_t launch_silu_mul_quant(const void* gate_up, uint8_t* q, float* scale, 
 #define W4A8_SMQ(C, TT)                                                                         \
   case C:                                                                                       \
     hipLaunchKernelGGL((silu_mul_quant<C, TT>), dim3(M), dim3(TT), 0, stream,                   \
-                       (const uint4*)gate_up, q, scale, N);                                     \
+                       (const uint4*)gate_up, q, scale, (uint4*)out, N);                        \
     break;
   if (wide) {
     switch (G) {
