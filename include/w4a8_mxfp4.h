@@ -72,7 +72,8 @@ int w4a8_repack(const void* w, const void* ws, void* wq, void* sq, int N, int K,
  * The counters must be zeroed once by the caller; the kernel's last-arriving workgroup resets each
  * counter it used, so they stay zeroed. Launches that overlap on one device race on it. Replaces
  * set_decode_scratch (sly/mxfp4/radiance_mxfp4_fp8.hip:1356-1360, registered from
- * sly/mxfp4/radiance_mxfp4.py:1054-1080). Pass NULLs to unregister. */
+ * sly/mxfp4/radiance_mxfp4.py:1054-1080). Pass NULLs to unregister. Registration is not
+ * synchronized with launches on other host threads: register before they start. */
 int w4a8_set_scratch(void* partial, size_t partial_bytes, void* counters, size_t counter_bytes);
 
 /* (3) The GEMM: c[M, N] bf16 = (a[M, K] e4m3 * a_scale[m]) . dequant(wq, sq)^T, fp32 accumulate.

@@ -1,6 +1,8 @@
 // C ABI of libw4a8_mxfp4.so: argument validation, plan selection and dispatch.
 // Declarations and the reference interfaces each entry point replaces: include/w4a8_mxfp4.h.
 #include <stdarg.h>
+#include <atomic>
+#include <mutex>
 #include <stdio.h>
 #include <string.h>
 
@@ -53,12 +55,17 @@ struct DeviceInfo {
   int cus = 256;
   size_t lds = 160 * 1024;
 };
+// Filled once per device under a lock; the flag is published after the entry, so a reader that
+// sees it set reads a complete entry without taking the lock.
 DeviceInfo g_devinfo[kMaxDevices];
-bool g_devinfo_set[kMaxDevices];
+std::atomic<bool> g_devinfo_set[kMaxDevices];
 
 DeviceInfo device_info(int dev) {
   if (dev < 0) return DeviceInfo{};
-  if (!g_devinfo_set[dev]) {
+  if (!g_devinfo_set[dev].load(std::memory_order_acquire)) {
+    static std::mutex fill;
+    std::lock_guard<std::mutex> lock(fill);
+    if (g_devinfo_set[dev].load(std::memory_order_relaxed)) return g_devinfo[dev];
     DeviceInfo d;
     int v = 0;
     if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
@@ -68,7 +75,7 @@ DeviceInfo device_info(int dev) {
         v > 0)
       d.lds = (size_t)v;
     g_devinfo[dev] = d;
-    g_devinfo_set[dev] = true;
+    g_devinfo_set[dev].store(true, std::memory_order_release);
   }
   return g_devinfo[dev];
 }
