@@ -511,7 +511,7 @@ def bench_sweep(n_layers):
                                  lin.weight_scale.data_ptr(), out.data_ptr(), M, N, K,
                                  torch.cuda.current_stream().cuda_stream, kernel, variant, split)
 
-            tile_v = _native.plan(max(M, 17), N, K)[1]
+            tile_v = _native.plan(max(M, 24), N, K)[1]     # the tile plan's shape at M <= 32
             row = dict(M=M, tile_us=round(_timed_graph(
                 lambda: run(_native.KERNEL_TILE, tile_v, 1), 5) * 1e3 / 16, 2))
             k, v, sp = _native.plan(M, N, K)

@@ -107,11 +107,14 @@ def test_split_k_without_scratch_is_refused(lib):
 def test_plan_bands(lib):
     k, v, s = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     # M <= 16: the streaming family when a wave's run and the LDS staging fit, else skinny; above
-    # M = 16 the macro-tile family. N=17408 K=8704 would need 43-granule runs, past the largest
-    # stream variant; K=640 has fewer k-tiles per n-tile than the smallest run.
+    # M = 16 the macro-tile family, except skinny up to M = 21 on N = 2048 .. 5120. N=17408 K=8704
+    # would need 43-granule runs, past the largest stream variant; K=640 has fewer k-tiles per
+    # n-tile than the smallest run.
     for M, N, K, kernel in [(1, 17408, 5120, 3), (8, 17408, 5120, 3), (16, 17408, 5120, 3),
                             (8, 5120, 8704, 3), (8, 17408, 8704, 1), (8, 33, 640, 1),
                             (17, 17408, 5120, 2), (64, 17408, 5120, 2), (65, 17408, 5120, 2),
+                            (17, 5120, 6144, 1), (21, 5120, 8704, 1), (22, 5120, 8704, 2),
+                            (21, 10240, 5120, 2), (17, 1024, 6144, 2),
                             (4096, 17408, 5120, 2)]:
         assert lib.w4a8_plan(M, N, K, ctypes.byref(k), ctypes.byref(v), ctypes.byref(s)) == 0
         assert (M, N, K, k.value) == (M, N, K, kernel) and v.value >= 0 and s.value >= 1

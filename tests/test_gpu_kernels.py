@@ -467,9 +467,11 @@ def random_shapes(count, seed):
     return out
 
 
-@pytest.mark.parametrize("M,N,K", random_shapes(18, 2024))
+@pytest.mark.parametrize("M,N,K", random_shapes(18, 2024) + [
+    (17, 5120, 6144), (21, 5120, 8704), (19, 2048, 1024), (20, 4000, 544)])
 def test_gemm_random_shapes_planned(gpu_lib, M, N, K):
-    """The automatic plan on seeded random shapes, every output against the oracle."""
+    """The automatic plan on seeded random shapes, every output against the oracle; the last four
+    take the skinny kernel just above the streaming band (M = 17 .. 21, N = 2048 .. 5120)."""
     x = synthetic.activations(M, K, seed=M * 31 + K)
     w, ws = synthetic.weights(N, K, seed=N * 7 + K)
     q, s = O.quant_per_token(x)

@@ -161,7 +161,8 @@ int small_m_tile(int M, int N, int cus) {
 // Decode / verify band: M <= 16 takes the streaming family when a variant fits (whole-K
 // workgroups, every weight load in flight at once), else the skinny family, whose workgroup count
 // should cover the 256 CUs several times over (for small N the K dimension is split across
-// workgroups too). Above M = 16 the macro-tile family wins from M = 24 on every Qwen3.8-27B shape.
+// workgroups too). Above M = 16 the macro-tile family wins on every Qwen3.8-27B shape, except up
+// to M = 21 on N = 2048 .. 5120 (below).
 void plan_impl(int M, int N, int K, int dev, int* kernel, int* variant, int* split_k) {
   if (M <= 16) {
     const int v = find_stream(M, N, K, dev);
@@ -184,6 +185,20 @@ void plan_impl(int M, int N, int K, int dev, int* kernel, int* variant, int* spl
     *variant = v2;
     *split_k = ks;
     return;
+  }
+  // Just above the streaming band on N = 2048 .. 5120: the skinny kernel with two 16-row
+  // M-fragments (one n-tile per wave, 8 waves) beats the smallest macro tile up to M = 21 (N = 5120,
+  // K = 6144: 11.2-12.1 against 12.3 us; K = 8704: 14.5-15.9 against 16.9 us); from M = 22 the tile
+  // wins, and on wider N it wins from M = 17.
+  if (M <= 21) {
+    const int ntiles = padded_n(N) / kNTile;
+    const int v = find_skinny(2, 1, 8);
+    if (ntiles >= 128 && ntiles <= 320 && v >= 0) {
+      *kernel = W4A8_KERNEL_SKINNY;
+      *variant = v;
+      *split_k = 1;
+      return;
+    }
   }
   // Prefill band (measured on MI355X, every tile variant on the four Qwen3.8-27B linear shapes at
   // M = 32 .. 2048): 8-wave 256 x 256 tiles for wide N (the automatic path splits N so the last
