@@ -111,6 +111,12 @@ int w4a8_variant_info(int kernel, int variant, int* p0, int* p1, int* p2, int* p
 int w4a8_scratch_bytes(int variant, int N, int split_k, size_t* partial_bytes,
                        size_t* counter_bytes);
 
+/* Scratch the automatic plan may use for any M <= max_m, N <= max_n and any K, plus what
+ * w4a8_silu_mul_quant's split rows use: register at least this much with w4a8_set_scratch and
+ * w4a8_gemm never has to give up a split for lack of room. The reference sized its decode
+ * scratch from its own band limits (sly/mxfp4/radiance_mxfp4.py:1064-1070). max_n <= 2^22. */
+int w4a8_workspace_bytes(int max_m, int max_n, size_t* partial_bytes, size_t* counter_bytes);
+
 /* Quantize + GEMM in one call (two launches on the stream): the body of radiance::mxfp4_linear
  * (sly/mxfp4/radiance_mxfp4.py:644-816) minus the output allocation, which stays with the caller
  * (torch.empty at sly/mxfp4/radiance_mxfp4.py:737). q [M, K] and scale [M] are caller workspace. */

@@ -195,3 +195,18 @@ def test_read_probe_validates_before_launch(lib):
     assert lib.w4a8_read_probe(p + 4, 1024, p, None) == 1                         # misaligned
     assert lib.w4a8_read_probe(p, 1 << 31, p, None) == 1
     assert b"w4a8_read_probe" in lib.w4a8_last_error()
+
+
+def test_workspace_bytes_is_a_few_hundred_kib(lib):
+    """The scratch the plugin registers, sized by the library's own plan: split-K partials for the
+    decode band's small-N shapes plus SiLU-mul's split-row maxima, well under 1 MiB at the model's
+    widths (the reference registered 37.7 MB, sly/mxfp4/radiance_mxfp4.py:1064-1070)."""
+    part, cnt = _native.workspace_bytes(64, 36864)
+    assert 9216 <= part < 1 << 20 and 0 < cnt <= 4096
+    # monotone in the limits, and never below SiLU-mul's own need (64 rows x 36 chunks x 4 B)
+    p2, c2 = _native.workspace_bytes(64, 65536)
+    assert p2 >= part and c2 >= cnt
+    assert _native.workspace_bytes(1, 16)[0] >= 36 * 4
+    for bad in ((0, 16), (1, 0), (1, (1 << 22) + 1)):
+        with pytest.raises(RuntimeError):
+            _native.workspace_bytes(*bad)

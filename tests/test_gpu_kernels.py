@@ -23,13 +23,21 @@ SKINNY, TILE, STREAM = _native.KERNEL_SKINNY, _native.KERNEL_TILE, _native.KERNE
 
 @pytest.fixture(scope="module")
 def scratch(gpu_lib):
-    """Split-K scratch for every plan these tests force (up to 16 splits, N <= 36864)."""
+    """Split-K scratch for every plan these tests force (up to 16 splits of 4 M-fragments,
+    N <= 36864): far more than the plugin registers, which covers only the automatic plans. The
+    plugin's registration, if any, is put back afterwards."""
+    from vllm_sly_radiance_amd import radiance_mxfp4 as R
     partial = torch.empty(36864 // 16 * 16 * 4 * 64 * 4, dtype=torch.float32, device="cuda")
     counters = torch.zeros(36864 // 16 + 8, dtype=torch.int32, device="cuda")
     _native.set_scratch(partial.data_ptr(), partial.numel() * 4, counters.data_ptr(),
                         counters.numel() * 4)
     yield partial, counters
-    _native.set_scratch(None, 0, None, 0)
+    torch.cuda.synchronize()
+    part, cnt = R._scratch
+    if part is None:
+        _native.set_scratch(None, 0, None, 0)
+    else:
+        _native.set_scratch(part.data_ptr(), part.numel() * 4, cnt.data_ptr(), cnt.numel() * 4)
 
 
 @functools.lru_cache(maxsize=4)
@@ -443,6 +451,37 @@ def test_split_k_reduction_has_no_race(gpu_lib, scratch):
 
 
 # ---- diagnostics --------------------------------------------------------------------------------
+BASELINE_SHAPES = [(10240, 5120), (5120, 6144), (17408, 5120), (5120, 8704)]
+
+
+def test_plugin_scratch_covers_every_automatic_plan(gpu_lib):
+    """The scratch the plugin registers (w4a8_workspace_bytes for M <= 64, N <= 36864) lets the
+    automatic plan take every split it would take with unlimited room: the plans agree on the
+    Qwen3.8-27B linear shapes and on every N up to 2048 (where the decode band splits K), at
+    every M of the decode band and K of the model."""
+    from vllm_sly_radiance_amd import radiance_mxfp4 as R
+    R.ensure_scratch("cuda")
+    part, cnt = R._scratch
+    assert part.numel() * 4 < 8 << 20, "the plugin scratch should be a few MB at most"
+    big_p = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
+    big_c = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
+    shapes = BASELINE_SHAPES + [(n, k) for n in range(16, 2049, 16) for k in (5120, 8704)]
+    ms = list(range(1, 65))
+    try:
+        plans = {}
+        _native.set_scratch(big_p.data_ptr(), big_p.numel(), big_c.data_ptr(), big_c.numel() * 4)
+        for N, K in shapes:
+            for M in ms:
+                plans[(M, N, K)] = _native.plan(M, N, K)
+        _native.set_scratch(part.data_ptr(), part.numel() * 4, cnt.data_ptr(), cnt.numel() * 4)
+        differ = [(key, plans[key], _native.plan(*key)) for key in plans
+                  if _native.plan(*key) != plans[key]]
+        assert not differ, differ[:5]
+        assert any(p[2] > 1 for p in plans.values()), "no split plan was exercised"
+    finally:
+        _native.set_scratch(part.data_ptr(), part.numel() * 4, cnt.data_ptr(), cnt.numel() * 4)
+
+
 @pytest.mark.parametrize("nbytes", [1000, 204800, 47_669_280])
 def test_read_probe_reads_without_writing(gpu_lib, nbytes):
     """The HBM read probe over buffers shorter than, equal to and longer than one workgroup's

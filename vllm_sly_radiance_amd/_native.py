@@ -36,6 +36,7 @@ SIGNATURES = {
     "w4a8_variant_count": (_int, [_int]),
     "w4a8_variant_info": (_int, [_int, _int, _pint, _pint, _pint, _pint]),
     "w4a8_scratch_bytes": (_int, [_int, _int, _int, _psz, _psz]),
+    "w4a8_workspace_bytes": (_int, [_int, _int, _psz, _psz]),
     "w4a8_linear": (_int, [_vp, _long, _vp, _vp, _vp, _vp, _vp, _int, _int, _int, _vp]),
     "w4a8_add_rms_quant": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _int, _int, _c.c_float, _vp]),
     "w4a8_silu_mul_quant": (_int, [_vp, _vp, _vp, _int, _int, _vp]),
@@ -147,6 +148,13 @@ def variants(kernel: int):
 def scratch_bytes(variant: int, N: int, split_k: int):
     a, b = _sz(), _sz()
     check(lib().w4a8_scratch_bytes(variant, N, split_k, _c.byref(a), _c.byref(b)))
+    return a.value, b.value
+
+
+def workspace_bytes(max_m: int, max_n: int):
+    """(partial bytes, counter bytes) the automatic plan may use for M <= max_m, N <= max_n."""
+    a, b = _sz(), _sz()
+    check(lib().w4a8_workspace_bytes(max_m, max_n, _c.byref(a), _c.byref(b)))
     return a.value, b.value
 
 

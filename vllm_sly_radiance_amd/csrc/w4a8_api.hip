@@ -33,15 +33,23 @@ int hip_status(hipError_t e, const char* what) {
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
-// Per-device split-K scratch (caller-owned; registered once at load time).
+// Split-K scratch: fp32 partials and int counters. A view names one buffer; the registered one is
+// caller-owned (w4a8_set_scratch, once per device at load time), the static one belongs to the
+// allocation-free entry point (below).
 struct Scratch {
   float* partial = nullptr;
   size_t partial_bytes = 0;
   int* counters = nullptr;
   size_t counter_bytes = 0;
+  const char* what = "the scratch registered with w4a8_set_scratch";
 };
 constexpr int kMaxDevices = 64;
 Scratch g_scratch[kMaxDevices];
+// A view with unlimited room: plans as if every split fitted (scratch sizing queries only).
+constexpr size_t kUnbounded = ~(size_t)0;
+// The automatic plan splits K across workgroups only in the decode band, M <= kMaxSplitM.
+constexpr int kMaxSplitM = 64;
+const Scratch kPlanAnySplit{nullptr, kUnbounded, nullptr, kUnbounded, "unbounded scratch"};
 
 int current_device() {
   int d = 0;
@@ -116,14 +124,14 @@ int find_tile(int wm, int wn, int nw = 4, int ns = 0) {
   return -1;
 }
 
-bool scratch_fits(int dev, int variant, int N, int split_k) {
+bool scratch_fits(const Scratch& s, int variant, int N, int split_k) {
   if (split_k <= 1) return true;
-  if (dev < 0) return false;
-  const Scratch& s = g_scratch[dev];
-  return s.partial && s.counters &&
-         skinny_scratch_bytes(variant, N, split_k) <= s.partial_bytes &&
+  const bool room = s.partial_bytes == kUnbounded || (s.partial && s.counters);
+  return room && skinny_scratch_bytes(variant, N, split_k) <= s.partial_bytes &&
          (size_t)skinny_counter_count(variant, N) * sizeof(int) <= s.counter_bytes;
 }
+
+Scratch registered_scratch(int dev) { return dev >= 0 ? g_scratch[dev] : Scratch{}; }
 
 // The stream variant that serves (M, N, K) with the fewest granules on its busiest wave, then the
 // fewest n-tile slots, then the fewest waves.
@@ -163,7 +171,8 @@ int small_m_tile(int M, int N, int cus) {
 // should cover the 256 CUs several times over (for small N the K dimension is split across
 // workgroups too). Above M = 16 the macro-tile family wins on every Qwen3.8-27B shape, except up
 // to M = 21 on N = 2048 .. 5120 (below).
-void plan_impl(int M, int N, int K, int dev, int* kernel, int* variant, int* split_k) {
+void plan_impl(int M, int N, int K, int dev, const Scratch& sc, int* kernel, int* variant,
+               int* split_k) {
   if (M <= 16) {
     const int v = find_stream(M, N, K, dev);
     if (v >= 0) {
@@ -179,7 +188,7 @@ void plan_impl(int M, int N, int K, int dev, int* kernel, int* variant, int* spl
     const int kte = ceil_div(K, kKTile);
     if (ntiles < 128) {
       for (int c = 2; c <= 16 && ntiles * ks < 256; c *= 2)
-        if (c <= kte / 2 && scratch_fits(dev, v2, N, c)) ks = c;
+        if (c <= kte / 2 && scratch_fits(sc, v2, N, c)) ks = c;
     }
     *kernel = W4A8_KERNEL_SKINNY;
     *variant = v2;
@@ -245,61 +254,86 @@ int tile_split(int M, int N, int variant, int dev, int* tail_variant) {
 // Output columns [n0, n0 + n) of an M x N GEMM on one tile variant: the weights, scales and
 // output are offset by n0 / 16 n-tiles; the output keeps its row stride N.
 int tile_columns(const void* a, const float* as, const void* wq, const void* sq, void* c, int M,
-                 int N, int K, int n0, int n, int variant, hipStream_t st) {
+                 int N, int K, int n0, int n, int variant, const char* who, hipStream_t st) {
   const size_t kt = padded_k(K) / kKTile, nt0 = n0 / kNTile;
   const GemmArgs g{(const uint8_t*)a, as, (const uint8_t*)wq + nt0 * kt * kGranuleBytes,
                    (const uint32_t*)sq + nt0 * (kt / kKGroup) * 64, (uint16_t*)c + n0, M, n, K,
                    N};
-  return hip_status(launch_tile(g, variant, st), "w4a8_gemm");
+  return hip_status(launch_tile(g, variant, st), who);
 }
 
 int gemm_dispatch(const void* a, const float* as, const void* wq, const void* sq, void* c, int M,
-                  int N, int K, int kernel, int variant, int split_k, void* stream) {
+                  int N, int K, int kernel, int variant, int split_k, const Scratch& sc,
+                  const char* who, void* stream) {
   const GemmArgs g{(const uint8_t*)a, as, (const uint8_t*)wq, (const uint32_t*)sq, (uint16_t*)c,
                    M, N, K, N};
   const hipStream_t st = (hipStream_t)stream;
   if (kernel == W4A8_KERNEL_SKINNY) {
     if (variant < 0 || variant >= skinny_variant_count())
-      return fail(W4A8_EINVAL, "w4a8_gemm: skinny variant %d out of range", variant);
+      return fail(W4A8_EINVAL, "%s: skinny variant %d out of range", who, variant);
     const SkinnyCfg cfg = skinny_variant(variant);
     if (M > 16 * cfg.mt)
-      return fail(W4A8_EINVAL, "w4a8_gemm: skinny variant %d covers M <= %d, got M=%d", variant,
+      return fail(W4A8_EINVAL, "%s: skinny variant %d covers M <= %d, got M=%d", who, variant,
                   16 * cfg.mt, M);
     if (split_k < 1 || split_k > 64)
-      return fail(W4A8_EINVAL, "w4a8_gemm: split_k=%d outside 1..64", split_k);
+      return fail(W4A8_EINVAL, "%s: split_k=%d outside 1..64", who, split_k);
     float* partial = nullptr;
     int* counters = nullptr;
     if (split_k > 1) {
-      const int dev = current_device();
-      if (!scratch_fits(dev, variant, N, split_k))
+      if (!scratch_fits(sc, variant, N, split_k))
         return fail(W4A8_ESCRATCH,
-                    "w4a8_gemm: split_k=%d needs %zu B of partials and %zu B of counters; "
-                    "register them with w4a8_set_scratch",
-                    split_k, skinny_scratch_bytes(variant, N, split_k),
-                    (size_t)skinny_counter_count(variant, N) * sizeof(int));
-      partial = g_scratch[dev].partial;
-      counters = g_scratch[dev].counters;
+                    "%s: split_k=%d needs %zu B of partials and %zu B of counters; %s holds "
+                    "%zu and %zu B",
+                    who, split_k, skinny_scratch_bytes(variant, N, split_k),
+                    (size_t)skinny_counter_count(variant, N) * sizeof(int), sc.what,
+                    sc.partial_bytes, sc.counter_bytes);
+      partial = sc.partial;
+      counters = sc.counters;
     }
-    return hip_status(launch_skinny(g, variant, split_k, partial, counters, st), "w4a8_gemm");
+    return hip_status(launch_skinny(g, variant, split_k, partial, counters, st), who);
   }
   if (kernel == W4A8_KERNEL_TILE) {
     if (variant < 0 || variant >= tile_variant_count())
-      return fail(W4A8_EINVAL, "w4a8_gemm: tile variant %d out of range", variant);
+      return fail(W4A8_EINVAL, "%s: tile variant %d out of range", who, variant);
     if (!tile_fits(M, N, K))
-      return fail(W4A8_EINVAL, "w4a8_gemm: M=%d K=%d exceeds the tile kernel's 32-bit offsets", M,
-                  K);
-    return hip_status(launch_tile(g, variant, st), "w4a8_gemm");
+      return fail(W4A8_EINVAL, "%s: M=%d K=%d exceeds the tile kernel's 32-bit offsets", who,
+                  M, K);
+    return hip_status(launch_tile(g, variant, st), who);
   }
   if (kernel == W4A8_KERNEL_STREAM) {
     if (variant < 0 || variant >= stream_variant_count())
-      return fail(W4A8_EINVAL, "w4a8_gemm: stream variant %d out of range", variant);
+      return fail(W4A8_EINVAL, "%s: stream variant %d out of range", who, variant);
     const DeviceInfo d = device_info(current_device());
     if (!stream_fits(variant, M, N, K, d.cus, d.lds))
-      return fail(W4A8_EINVAL, "w4a8_gemm: stream variant %d does not serve M=%d N=%d K=%d",
-                  variant, M, N, K);
-    return hip_status(launch_stream(g, variant, d.cus, st), "w4a8_gemm");
+      return fail(W4A8_EINVAL, "%s: stream variant %d does not serve M=%d N=%d K=%d",
+                  who, variant, M, N, K);
+    return hip_status(launch_stream(g, variant, d.cus, st), who);
   }
-  return fail(W4A8_EINVAL, "w4a8_gemm: unknown kernel %d", kernel);
+  return fail(W4A8_EINVAL, "%s: unknown kernel %d", who, kernel);
+}
+
+// The GEMM on one scratch view: validation, the automatic plan (kernel == W4A8_KERNEL_AUTO) or
+// the forced one, and the launch(es) on `stream`.
+int gemm_run(const void* a, const float* as, const void* wq, const void* sq, void* c, int M, int N,
+             int K, int kernel, int variant, int split_k, const Scratch& sc, const char* who,
+             void* stream) {
+  if (int e = check_gemm_shape(who, M, N, K)) return e;
+  if (M == 0) return W4A8_OK;
+  if (int e = check_gemm_ptrs(who, a, as, wq, sq, c)) return e;
+  if (kernel == W4A8_KERNEL_AUTO) {
+    const int dev = current_device();
+    plan_impl(M, N, K, dev, sc, &kernel, &variant, &split_k);
+    int tail = -1;
+    const int n_main = kernel == W4A8_KERNEL_TILE && tile_fits(M, N, K)
+                           ? tile_split(M, N, variant, dev, &tail)
+                           : 0;
+    if (n_main > 0 && n_main < N && n_main % kNTile == 0) {
+      const hipStream_t st = (hipStream_t)stream;
+      if (int e = tile_columns(a, as, wq, sq, c, M, N, K, 0, n_main, variant, who, st)) return e;
+      return tile_columns(a, as, wq, sq, c, M, N, K, n_main, N - n_main, tail, who, st);
+    }
+  }
+  return gemm_dispatch(a, as, wq, sq, c, M, N, K, kernel, variant, split_k, sc, who, stream);
 }
 
 }  // namespace
@@ -361,30 +395,16 @@ W4A8_API int w4a8_set_scratch(void* partial, size_t partial_bytes, void* counter
 W4A8_API int w4a8_plan(int M, int N, int K, int* kernel, int* variant, int* split_k) {
   if (int e = check_gemm_shape("w4a8_plan", M, N, K)) return e;
   if (!kernel || !variant || !split_k) return fail(W4A8_EINVAL, "w4a8_plan: null output");
-  plan_impl(M, N, K, current_device(), kernel, variant, split_k);
+  const int dev = current_device();
+  plan_impl(M, N, K, dev, registered_scratch(dev), kernel, variant, split_k);
   return W4A8_OK;
 }
 
 W4A8_API int w4a8_gemm_planned(const void* a, const float* a_scale, const void* wq,
                                const void* sq, void* c, int M, int N, int K, int kernel,
                                int variant, int split_k, void* stream) {
-  if (int e = check_gemm_shape("w4a8_gemm", M, N, K)) return e;
-  if (M == 0) return W4A8_OK;
-  if (int e = check_gemm_ptrs("w4a8_gemm", a, a_scale, wq, sq, c)) return e;
-  if (kernel == W4A8_KERNEL_AUTO) {
-    const int dev = current_device();
-    plan_impl(M, N, K, dev, &kernel, &variant, &split_k);
-    int tail = -1;
-    const int n_main = kernel == W4A8_KERNEL_TILE && tile_fits(M, N, K)
-                           ? tile_split(M, N, variant, dev, &tail)
-                           : 0;
-    if (n_main > 0 && n_main < N && n_main % kNTile == 0) {
-      const hipStream_t st = (hipStream_t)stream;
-      if (int e = tile_columns(a, a_scale, wq, sq, c, M, N, K, 0, n_main, variant, st)) return e;
-      return tile_columns(a, a_scale, wq, sq, c, M, N, K, n_main, N - n_main, tail, st);
-    }
-  }
-  return gemm_dispatch(a, a_scale, wq, sq, c, M, N, K, kernel, variant, split_k, stream);
+  return gemm_run(a, a_scale, wq, sq, c, M, N, K, kernel, variant, split_k,
+                  registered_scratch(current_device()), "w4a8_gemm", stream);
 }
 
 W4A8_API int w4a8_gemm(const void* a, const float* a_scale, const void* wq, const void* sq,
@@ -431,6 +451,30 @@ W4A8_API int w4a8_scratch_bytes(int variant, int N, int split_k, size_t* partial
   return W4A8_OK;
 }
 
+W4A8_API int w4a8_workspace_bytes(int max_m, int max_n, size_t* partial_bytes,
+                                  size_t* counter_bytes) {
+  if (max_m < 1 || max_n < 1 || max_n > (1 << 22))
+    return fail(W4A8_EINVAL, "w4a8_workspace_bytes: need max_m >= 1 and 1 <= max_n <= 2^22");
+  const int dev = current_device();
+  // The plan splits K only at M <= kMaxSplitM; a larger K never splits less, so K = 2^16 bounds
+  // every K. SiLU-mul's split rows (M <= 64, N <= 18432) keep their partial maxima here too.
+  size_t part = producer_split_bytes(max_m < 64 ? max_m : 64, 18432), cnt = 0;
+  for (int M = 1; M <= max_m && M <= kMaxSplitM; ++M)
+    for (int N = kNTile; N < max_n + kNTile; N += kNTile) {
+      const int n = N < max_n ? N : max_n;
+      int kernel = 0, variant = 0, split = 1;
+      plan_impl(M, n, 1 << 16, dev, kPlanAnySplit, &kernel, &variant, &split);
+      if (kernel != W4A8_KERNEL_SKINNY || split <= 1) continue;
+      const size_t p = skinny_scratch_bytes(variant, n, split);
+      const size_t c = (size_t)skinny_counter_count(variant, n) * sizeof(int);
+      if (p > part) part = p;
+      if (c > cnt) cnt = c;
+    }
+  if (partial_bytes) *partial_bytes = part;
+  if (counter_bytes) *counter_bytes = cnt;
+  return W4A8_OK;
+}
+
 W4A8_API int w4a8_linear(const void* x, long ldx, void* q, float* scale, const void* wq,
                          const void* sq, void* c, int M, int N, int K, void* stream) {
   if (int e = check_gemm_shape("w4a8_linear", M, N, K)) return e;
@@ -469,9 +513,9 @@ W4A8_API int w4a8_silu_mul_quant(const void* gate_up, void* q, float* scale, int
   if (!aligned(gate_up, 16) || !aligned(q, 8) || !aligned(scale, 4))
     return fail(W4A8_EINVAL,
                 "w4a8_silu_mul_quant: gate_up needs 16-byte alignment, q 8-byte, scale 4-byte");
-  const int dev = current_device();
-  void* part = dev >= 0 ? (void*)g_scratch[dev].partial : nullptr;
-  const size_t part_bytes = dev >= 0 ? g_scratch[dev].partial_bytes : 0;
+  const Scratch sc = registered_scratch(current_device());
+  void* part = sc.partial;
+  const size_t part_bytes = sc.partial_bytes;
   return hip_status(launch_silu_mul_quant(gate_up, (uint8_t*)q, scale, nullptr, M, N, part,
                                           part_bytes, (hipStream_t)stream),
                     "w4a8_silu_mul_quant");

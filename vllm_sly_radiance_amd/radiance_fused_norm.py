@@ -1,48 +1,60 @@
 """Fused norm / activation + per-token fp8 quant in front of the W4A8 MXFP4 GEMMs (gfx950).
 
-Mirrors sly/mxfp4/radiance_fused_norm.py: the same three custom ops, their fakes, the same gates and
-call-site helpers, and the same switches. Each op ends in the per-token e4m3 quantizer
+Interface of sly/mxfp4/radiance_fused_norm.py, kept so that the reference's model patch
+(sly/patch_fused_norm_quant.py) drives this module unchanged: the three custom ops with their
+fakes, the switch names, the gate names (mx_ok, input_ok, post_ok, mlp_ok, gdn_ok) and the
+call-site helper names and signatures. Each op ends in the per-token e4m3 quantizer that
 radiance::mxfp4_linear runs internally, so its (q, scale) pair goes straight to
 radiance::mxfp4_linear_pq (apply_weights' tuple branch) instead of a bf16 tensor that the op
 re-quantizes:
 
-  add_rms_quant   Gemma RMSNorm with residual (decoder input / post-attention layernorm): fp32 add,
-                  x * rsqrt(mean(x^2) + eps) * (w + 1) -> bf16 -> e4m3, plus the bf16 residual out.
-  silu_mul_quant  MLP act_fn: silu(gate) * up -> e4m3 for down_proj.
-  gdn_norm_quant  GatedDeltaNet output projection: per-head RMSNormGated (norm before gate, silu
-                  gate) -> e4m3 for out_proj; z may be a column slice of the fused projection.
+  add_rms_quant   Gemma RMSNorm with residual: fp32 add, x * rsqrt(mean(x^2) + eps) * (w + 1)
+                  -> bf16 -> e4m3, plus the bf16 residual out.
+  silu_mul_quant  silu(gate) * up -> e4m3.
+  gdn_norm_quant  per-head gated RMSNorm (norm before gate, silu gate) -> e4m3; z may be a column
+                  slice of a wider projection.
 
 The HIP library does the work (w4a8_add_rms_quant / w4a8_silu_mul_quant / w4a8_gdn_norm_quant);
 there is no torch fallback. Each op's result equals "the producer's bf16 output, then the plain
 quantizer" bit for bit (the quantizer divides by the scale, as _traced_quant does).
 
-Not carried over from the reference: the fragment-tiled q layout (the MI355X GEMM reads row-major
-activations through LDS at the same rate either way), the fp8 hi/lo activation split and the online
-Hadamard rotation (both belong to checkpoint variants outside this path).
+When a fusion is valid is data here, not code: SITES lists each place in a decoder where a
+producer can stand in for a bf16 activation (which module produces it, which linears consume it,
+what the host module must look like), and one function, site_ok, checks a site against a module.
+The gates are thin names over it. Everything they read is a plain attribute, so a tracing compiler
+folds each gate to a constant per layer.
 
-Switches (read once at import, as the reference does): RADIANCE_FUSED_NORM_QUANT=1 arms the fusions
-(default off), RADIANCE_FUSED_NORM_QUANT_ADD_RMS / _SILU / _GDN (default 1 each) pick them.
+Not carried over: the fragment-tiled q layout (the MI355X GEMM reads row-major activations through
+LDS at the same rate either way), the fp8 hi/lo activation split and the online Hadamard rotation
+(both belong to checkpoint variants outside this path).
+
+Switches, read once at import: RADIANCE_FUSED_NORM_QUANT=1 arms the fusions (default off);
+RADIANCE_FUSED_NORM_QUANT_ADD_RMS / _SILU / _GDN (default 1 each) then pick them.
 """
 from __future__ import annotations
 
 import os
+from dataclasses import dataclass, field
 
 import torch
 
 from . import _native
 
-
-def _flag(name: str, default: str) -> bool:
-    return os.environ.get(name, default) == "1"
+_MASTER = "RADIANCE_FUSED_NORM_QUANT"
 
 
-ENABLED = _flag("RADIANCE_FUSED_NORM_QUANT", "0")
-ADD_RMS = ENABLED and _flag("RADIANCE_FUSED_NORM_QUANT_ADD_RMS", "1")
-SILU = ENABLED and _flag("RADIANCE_FUSED_NORM_QUANT_SILU", "1")
-GDN = ENABLED and _flag("RADIANCE_FUSED_NORM_QUANT_GDN", "1")
+def _armed(fusion: str) -> bool:
+    """A fusion is on when the master switch is "1" and its own switch (default "1") is too."""
+    env = os.environ
+    return env.get(_MASTER, "0") == "1" and env.get(f"{_MASTER}_{fusion}", "1") == "1"
 
-# Launcher limits (sly/mxfp4/radiance_fused_norm.py:48-52): add_rms K <= 10240, silu N <= 18432,
-# gdn N <= 10240 with 128-wide heads; all 8-aligned.
+
+ENABLED = os.environ.get(_MASTER, "0") == "1"
+ADD_RMS, SILU, GDN = (_armed(f) for f in ("ADD_RMS", "SILU", "GDN"))
+
+# Widths the producer kernels accept (the entry points refuse anything else): add-RMSNorm rows up
+# to 10240, SiLU-mul outputs up to 18432, gated-norm rows up to 10240 in 128-wide heads; all
+# multiples of 8. The same limits as the reference's launchers.
 ADD_RMS_MAX_K = 10240
 SILU_MAX_N = 18432
 GDN_MAX_N = 10240
@@ -53,10 +65,22 @@ def _stream() -> int:
     return torch.cuda.current_stream().cuda_stream
 
 
-def _check_bf16(name: str, *ts: torch.Tensor) -> None:
-    for t in ts:
-        if t.dtype != torch.bfloat16:
-            raise RuntimeError(f"radiance::{name}: expected bfloat16, got {t.dtype}")
+def _need_bf16(op: str, **tensors: torch.Tensor) -> None:
+    bad = {k: t.dtype for k, t in tensors.items() if t.dtype != torch.bfloat16}
+    if bad:
+        raise RuntimeError(f"radiance::{op}: bfloat16 inputs required, got {bad}")
+
+
+def _row_runs(t: torch.Tensor, n: int):
+    """(t, row stride) such that every row of t is n contiguous elements starting 16-byte aligned,
+    one stride apart, which is all the gated-norm kernel needs of z. A column slice of a wider
+    bf16 projection qualifies as it is; anything else is copied to a contiguous tensor first."""
+    rows = t.shape[0]
+    stride = int(t.stride(0)) if rows > 1 else n
+    fits = t.stride(1) == 1 and t.data_ptr() % 16 == 0 and stride >= n and stride % 8 == 0
+    if not fits:
+        t, stride = t.contiguous(), n
+    return t, stride
 
 
 def _qs(M: int, K: int, device):
@@ -71,7 +95,7 @@ def add_rms_quant_op(y: torch.Tensor, residual: torch.Tensor, weight: torch.Tens
     """y, residual: [M, K] bf16; weight: [K] bf16 (Gemma convention, the kernel adds the 1).
     Returns (q [M, K] e4m3, scale [M] f32, residual_out [M, K] bf16)
     (sly/mxfp4/radiance_fused_norm.py:132-152)."""
-    _check_bf16("add_rms_quant", y, residual, weight)
+    _need_bf16("add_rms_quant", y=y, residual=residual, weight=weight)
     M, K = y.shape
     q, s = _qs(M, K, y.device)
     r = torch.empty((M, K), device=y.device, dtype=torch.bfloat16)
@@ -94,7 +118,7 @@ def _(y, residual, weight, eps):
 def silu_mul_quant_op(gate_up: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """gate_up: [M, 2N] bf16 -> (q [M, N] e4m3 of silu(gate) * up, scale [M] f32)
     (sly/mxfp4/radiance_fused_norm.py:163-180)."""
-    _check_bf16("silu_mul_quant", gate_up)
+    _need_bf16("silu_mul_quant", gate_up=gate_up)
     M, N2 = gate_up.shape
     N = N2 // 2
     q, s = _qs(M, N, gate_up.device)
@@ -117,19 +141,13 @@ def gdn_norm_quant_op(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor,
     """x: [M, N] bf16 (N = heads * 128); z: [M, N] bf16, any row stride as long as each row is a
     contiguous run; weight: [128] bf16. Returns (q [M, N] e4m3, scale [M] f32)
     (sly/mxfp4/radiance_fused_norm.py:189-213)."""
-    _check_bf16("gdn_norm_quant", x, z, weight)
+    _need_bf16("gdn_norm_quant", x=x, z=z, weight=weight)
     M, N = x.shape
     q, s = _qs(M, N, x.device)
     if M:
+        # every copy stays referenced until the launch is queued
         x, weight = x.contiguous(), weight.contiguous()
-        if M > 1 and (z.stride(1) != 1 or z.stride(0) < N or z.stride(0) % 8):
-            z = z.contiguous()
-        elif M == 1 and z.stride(1) != 1:
-            z = z.contiguous()
-        zs = int(z.stride(0)) if M > 1 else N
-        if z.data_ptr() % 16:
-            z = z.contiguous()
-            zs = N
+        z, zs = _row_runs(z, N)
         _native.gdn_norm_quant(x.data_ptr(), z.data_ptr(), zs, weight.data_ptr(), q.data_ptr(),
                                s.data_ptr(), M, N, float(eps), _stream())
     return q, s
@@ -142,92 +160,186 @@ def _(x, z, weight, eps):
             torch.empty((M,), device=x.device, dtype=torch.float32))
 
 
-# ---- gates (traced; plain attribute reads only) -------------------------------------------------
-# The reference tests isinstance against vLLM's GemmaRMSNorm / RMSNormGated / SiluAndMul; vLLM is
-# not a dependency here, so the gates compare class names, which is the same test when vLLM is
-# present (sly/mxfp4/radiance_fused_norm.py:226-299).
+# ---- where a fusion is valid ------------------------------------------------------------------
+_ABSENT = object()
+
+
+def _at(obj, path):
+    """The attribute at a dotted path ("mlp.gate_up_proj"), or _ABSENT when a link is missing."""
+    if path is None:
+        return None
+    for name in path.split("."):
+        obj = getattr(obj, name, _ABSENT)
+        if obj is _ABSENT:
+            break
+    return obj
+
+
 def _is(obj, name: str) -> bool:
+    """Class-name test against the MRO: vLLM is not a dependency here, and with vLLM present a
+    GemmaRMSNorm / SiluAndMul / RMSNormGated instance carries exactly that name."""
     return any(c.__name__ == name for c in type(obj).__mro__)
 
 
+# Predicates on one attribute value; an absent attribute fails all of them but `_unset`.
+def _eq(v):
+    return lambda x: x is not _ABSENT and x == v
+
+
+def _le(v):
+    return lambda x: x is not _ABSENT and x <= v
+
+
+def _one_of(*vs):
+    return lambda x: x is not _ABSENT and x in vs
+
+
+def _falsy(x):
+    return x is not _ABSENT and not x
+
+
+def _truthy(x):
+    return x is not _ABSENT and bool(x)
+
+
+def _none(x):
+    return x is None
+
+
+def _unset(x):
+    return x is None or x is _ABSENT
+
+
+def _bf16_vector(multiple_of=1, at_most=None, exactly=None):
+    """A bf16 tensor whose leading size fits the producer kernel."""
+    def ok(t):
+        if not isinstance(t, torch.Tensor) or t.dtype != torch.bfloat16:
+            return False
+        n = t.shape[0]
+        return n % multiple_of == 0 and (at_most is None or n <= at_most) \
+            and (exactly is None or n == exactly)
+    return ok
+
+
+def _k_of_descriptor(at_most):
+    """The K a radiance linear's (N, K, 0) layout descriptor records: 8-aligned and in range."""
+    def ok(ref):
+        return isinstance(ref, torch.Tensor) and ref.dim() == 3 \
+            and ref.shape[1] % 8 == 0 and ref.shape[1] <= at_most
+    return ok
+
+
+@dataclass(frozen=True)
+class Site:
+    """One place where a producer's (q, scale) output can stand in for a bf16 activation.
+
+    producer / producer_class: the module (a dotted path from the host module) whose output the
+        fused op replaces, and the class it must be.
+    consumers: host kind -> the linears that read the activation; every one of them must be a
+        radiance W4A8 linear (mx_ok), or the unfused chain stays. `kind_attr` names the host
+        attribute that picks the kind; without it the single entry under None applies.
+    requires: (path, predicate) pairs the host must satisfy, plus `by_kind` ones per kind.
+    """
+    producer: str
+    producer_class: str
+    consumers: dict
+    requires: tuple = ()
+    by_kind: dict = field(default_factory=dict)
+    kind_attr: str | None = None
+
+
+def _gemma(path):
+    return ((f"{path}.weight", _bf16_vector(multiple_of=8, at_most=ADD_RMS_MAX_K)),)
+
+
+# The reduce-scatter MoE path hands the norm output to a collective, not to the linears.
+_NO_REDUCE_SCATTER = (("use_attn_reduce_scatter_for_moe", _falsy),)
+
+SITES = {
+    # decoder input norm (with residual) -> the attention block's input projections
+    "input": Site(
+        producer="input_layernorm", producer_class="GemmaRMSNorm", kind_attr="layer_type",
+        consumers={"linear_attention": ("linear_attn.in_proj_qkvz", "linear_attn.in_proj_ba"),
+                   "full_attention": ("self_attn.qkv_proj",)},
+        requires=_NO_REDUCE_SCATTER + _gemma("input_layernorm"),
+        by_kind={"linear_attention": (("linear_attn.tp_size", _eq(1)),)}),
+    # post-attention norm -> a dense MLP's fused gate/up projection (a MoE block has an expert
+    # gate, which reads the bf16 activation itself)
+    "post": Site(
+        producer="post_attention_layernorm", producer_class="GemmaRMSNorm",
+        consumers={None: ("mlp.gate_up_proj",)},
+        requires=_NO_REDUCE_SCATTER + (("mlp.expert_gate", _none),)
+        + _gemma("post_attention_layernorm")),
+    # MLP activation -> down projection; the activation width is down's K
+    "mlp": Site(
+        producer="act_fn", producer_class="SiluAndMul", consumers={None: ("down_proj",)},
+        requires=(("down_proj.radiance_wref", _k_of_descriptor(SILU_MAX_N)),)),
+    # GatedDeltaNet output norm (per 128-wide head, norm before the silu gate) -> out_proj
+    "gdn": Site(
+        producer="norm", producer_class="RMSNormGated", consumers={None: ("out_proj",)},
+        requires=(("tp_size", _eq(1)), ("head_v_dim", _eq(GDN_HEAD)),
+                  ("value_dim", _le(GDN_MAX_N)), ("norm.group_size", _unset),
+                  ("norm.norm_before_gate", _truthy), ("norm.activation", _one_of("silu", "swish")),
+                  ("norm.weight", _bf16_vector(exactly=GDN_HEAD)))),
+}
+
+
 def mx_ok(lin) -> bool:
-    """A radiance W4A8 linear whose apply_weights takes the (q, scale) tuple branch."""
-    return (getattr(lin, "radiance_w4a8_ok", False)
-            and getattr(lin, "radiance_wref", None) is not None
-            and not getattr(lin, "_rad_ar_overlap", False)
+    """A radiance W4A8 linear whose apply_weights takes the (q, scale) tuple branch: repacked by
+    this plugin, not under the all-reduce overlap wrapper, not tensor-parallel."""
+    return (_truthy(_at(lin, "radiance_w4a8_ok"))
+            and _at(lin, "radiance_wref") not in (None, _ABSENT)
+            and not _truthy(_at(lin, "_rad_ar_overlap"))
             and getattr(lin, "tp_size", 1) == 1)
 
 
-def _gemma_ok(norm) -> bool:
-    w = getattr(norm, "weight", None)
-    return (norm is not None and _is(norm, "GemmaRMSNorm") and w is not None
-            and w.dtype == torch.bfloat16 and w.shape[0] % 8 == 0
-            and w.shape[0] <= ADD_RMS_MAX_K)
+def site_ok(site: Site, host) -> bool:
+    """Whether `host` (a decoder layer, MLP or attention module) matches `site`."""
+    kind = _at(host, site.kind_attr)
+    consumers = site.consumers.get(kind)
+    if consumers is None or not _is(_at(host, site.producer), site.producer_class):
+        return False
+    for path, ok in site.requires + site.by_kind.get(kind, ()):
+        if not ok(_at(host, path)):
+            return False
+    for path in consumers:
+        if not mx_ok(_at(host, path)):
+            return False
+    return True
 
 
+# ---- gates (names the model patch calls) --------------------------------------------------------
 def input_ok(layer) -> bool:
-    """Decoder input_layernorm (residual != None) -> the attention's projections."""
-    if getattr(layer, "use_attn_reduce_scatter_for_moe", True):
-        return False
-    if not _gemma_ok(getattr(layer, "input_layernorm", None)):
-        return False
-    kind = getattr(layer, "layer_type", None)
-    if kind == "linear_attention":
-        a = layer.linear_attn
-        return (getattr(a, "tp_size", 0) == 1 and mx_ok(getattr(a, "in_proj_qkvz", None))
-                and mx_ok(getattr(a, "in_proj_ba", None)))
-    if kind == "full_attention":
-        return mx_ok(getattr(layer.self_attn, "qkv_proj", None))
-    return False
+    return site_ok(SITES["input"], layer)
 
 
 def post_ok(layer) -> bool:
-    """Decoder post_attention_layernorm -> dense MLP gate_up_proj."""
-    if getattr(layer, "use_attn_reduce_scatter_for_moe", True):
-        return False
-    if not _gemma_ok(getattr(layer, "post_attention_layernorm", None)):
-        return False
-    mlp = getattr(layer, "mlp", None)
-    return getattr(mlp, "expert_gate", 1) is None and mx_ok(getattr(mlp, "gate_up_proj", None))
+    return site_ok(SITES["post"], layer)
 
 
 def mlp_ok(mlp) -> bool:
-    """MLP act_fn (SiluAndMul) -> down_proj."""
-    d = getattr(mlp, "down_proj", None)
-    if not (_is(getattr(mlp, "act_fn", None), "SiluAndMul") and mx_ok(d)):
-        return False
-    n = int(getattr(d, "radiance_wref").shape[1])        # down_proj's K = the act width N
-    return n % 8 == 0 and n <= SILU_MAX_N
+    return site_ok(SITES["mlp"], mlp)
 
 
 def gdn_ok(attn) -> bool:
-    """GatedDeltaNet _output_projection -> out_proj."""
-    n = getattr(attn, "norm", None)
-    if not (n is not None and _is(n, "RMSNormGated") and mx_ok(getattr(attn, "out_proj", None))):
-        return False
-    return (getattr(attn, "tp_size", 0) == 1 and getattr(attn, "head_v_dim", 0) == GDN_HEAD
-            and getattr(n, "group_size", None) is None and getattr(n, "norm_before_gate", False)
-            and getattr(n, "activation", None) in ("silu", "swish")
-            and n.weight.dtype == torch.bfloat16 and n.weight.shape[0] == GDN_HEAD
-            and getattr(attn, "value_dim", GDN_MAX_N + 1) <= GDN_MAX_N)
+    return site_ok(SITES["gdn"], attn)
 
 
-# ---- call sites (traced) ----------------------------------------------------------------------
+# ---- call-site helpers (names and signatures the model patch calls) -----------------------------
 def add_rms_quant(norm, hidden_states: torch.Tensor, residual: torch.Tensor):
-    """GemmaRMSNorm(hidden_states, residual) + quant -> ((q, scale), residual_out)."""
-    q, s, r = torch.ops.radiance.add_rms_quant(hidden_states, residual, norm.weight,
-                                               norm.variance_epsilon)
-    return (q, s), r
+    """Stands in for norm(hidden_states, residual): returns ((q, scale), new residual)."""
+    q, scale, new_residual = torch.ops.radiance.add_rms_quant(
+        hidden_states, residual, norm.weight, norm.variance_epsilon)
+    return (q, scale), new_residual
 
 
 def silu_mul_quant(gate_up: torch.Tensor):
-    q, s = torch.ops.radiance.silu_mul_quant(gate_up)
-    return (q, s)
+    """Stands in for act_fn(gate_up): returns (q, scale)."""
+    return tuple(torch.ops.radiance.silu_mul_quant(gate_up))
 
 
 def gdn_norm_quant(attn, core_attn_out: torch.Tensor, z: torch.Tensor):
-    """_output_projection's norm(core_attn_out, z) + flatten + quant -> (q, scale)."""
-    M = core_attn_out.shape[0]
-    q, s = torch.ops.radiance.gdn_norm_quant(core_attn_out.reshape(M, -1), z.reshape(M, -1),
-                                             attn.norm.weight, attn.norm.eps)
-    return (q, s)
+    """Stands in for attn.norm(core_attn_out, z) flattened to one row per token: (q, scale)."""
+    tokens = core_attn_out.shape[0]
+    return tuple(torch.ops.radiance.gdn_norm_quant(
+        core_attn_out.reshape(tokens, -1), z.reshape(tokens, -1), attn.norm.weight, attn.norm.eps))

@@ -27,9 +27,10 @@ import torch
 from . import _native
 
 ENABLED = os.environ.get("RADIANCE_MXFP4_W4A8", "0") == "1"
-# Largest N the registered split-K scratch covers, and the deepest split the plan may pick.
+# The registered split-K scratch covers every automatic plan up to these M and N (the decode band,
+# where the plan may split K across workgroups, ends at M = 64).
 SCRATCH_MAX_N = int(os.environ.get("RADIANCE_MXFP4_SCRATCH_MAX_N", "36864"))
-SCRATCH_MAX_SPLIT = 16
+SCRATCH_MAX_M = 64
 ACTIVATION_QUANT_KEY = "kMxfp4Dynamic"
 
 STATS = {"fast": 0, "refused": 0, "calls": 0, "calls_pq": 0}
@@ -84,14 +85,13 @@ def layout_ref(N: int, K: int, device) -> torch.Tensor:
 
 def ensure_scratch(device) -> None:
     """Allocate and register the split-K scratch once per process, at load time (outside graph
-    capture), torch-owned, as the reference does (sly/mxfp4/radiance_mxfp4.py:1054-1080)."""
+    capture), torch-owned, as the reference does (sly/mxfp4/radiance_mxfp4.py:1054-1080). Sized
+    by the library from its own plan: what any M <= SCRATCH_MAX_M, N <= SCRATCH_MAX_N may use."""
     if _scratch[0] is not None:
         return
-    # the widest plan: 4 m-fragments x 1 n-tile per workgroup x SCRATCH_MAX_SPLIT splits
-    tiles = -(-SCRATCH_MAX_N // 16)
-    partial = torch.empty(tiles * SCRATCH_MAX_SPLIT * 4 * 64 * 4, dtype=torch.float32,
-                          device=device)
-    counters = torch.zeros(tiles + 8, dtype=torch.int32, device=device)
+    part_bytes, cnt_bytes = _native.workspace_bytes(SCRATCH_MAX_M, SCRATCH_MAX_N)
+    partial = torch.empty(max(part_bytes, 16) // 4, dtype=torch.float32, device=device)
+    counters = torch.zeros(max(cnt_bytes, 4) // 4, dtype=torch.int32, device=device)
     _native.set_scratch(partial.data_ptr(), partial.numel() * 4, counters.data_ptr(),
                         counters.numel() * 4)
     _scratch[0], _scratch[1] = partial, counters
@@ -188,6 +188,18 @@ def layer_is_supported(layer, K: int) -> bool:
         return False
 
 
+def aiter_asm_fp4_enabled() -> bool:
+    """True when vLLM routes MXFP4 through AITER's asm fp4 GEMM, which keeps its weights shuffled
+    and its scales swizzled: a layer prepared for it is not a checkpoint layer this kernel can
+    repack, so can_implement declines (sly/mxfp4/radiance_mxfp4.py:995-1004, :1032-1036).
+    False when vLLM or its AITER hooks are absent."""
+    try:
+        from vllm._aiter_ops import rocm_aiter_ops
+        return bool(rocm_aiter_ops.is_asm_fp4_gemm_dynamic_quant_enabled())
+    except Exception:
+        return False
+
+
 def _base_classes():
     """vLLM's ABC and activation key when vLLM is importable, else local stand-ins with the same
     names (vllm.model_executor.kernels.linear.mxfp4.base, sly/mxfp4/radiance_mxfp4.py:1010-1014)."""
@@ -224,6 +236,8 @@ def _make_kernel_class():
         def can_implement(cls, config):
             if getattr(config, "activation_quant_key", None) != quant_key:
                 return False, "only supports MXFP4 dynamic activation"
+            if aiter_asm_fp4_enabled():
+                return False, "AITER's asm fp4 GEMM owns this layer's weight layout"
             return True, None
 
         def process_weights_after_loading(self, layer: torch.nn.Module) -> None:
@@ -286,16 +300,21 @@ def kernel_class():
     return _KERNEL_CLS
 
 
-def register_with_vllm(platform: str = "rocm") -> bool:
-    """Put the plugin at the head of vLLM's MXFP4 kernel priority list, the one thing
-    sly/patch_quark_mxfp4.py:76-103 patches in. Returns False when vLLM is not importable."""
+def register_with_vllm(platform=None) -> bool:
+    """Put the plugin at the head of vLLM's MXFP4 kernel priority list, the one change
+    sly/patch_quark_mxfp4.py:76-103 makes. The list is `_POSSIBLE_MXFP4_KERNELS[platform]` of
+    vllm.model_executor.kernels.linear (the module init_mxfp4_linear_kernel reads it from), keyed
+    by current_platform._enum unless `platform` is given. Idempotent: the class appears once, at
+    index 0. Returns False when vLLM is not importable."""
     try:
-        from vllm.model_executor.kernels.linear import mxfp4 as _m
+        import vllm.model_executor.kernels.linear as registry
+        if platform is None:
+            from vllm.platforms import current_platform
+            platform = current_platform._enum
     except Exception as e:  # noqa: BLE001
         sys.stderr.write(f"[radiance.mxfp4] vLLM not importable, plugin not registered: {e!r}\n")
         return False
-    lst = _m._POSSIBLE_MXFP4_KERNELS.setdefault(platform, [])
     cls = kernel_class()
-    if cls not in lst:
-        lst.insert(0, cls)
+    kernels = registry._POSSIBLE_MXFP4_KERNELS.setdefault(platform, [])
+    kernels[:] = [cls] + [k for k in kernels if k is not cls]
     return True
