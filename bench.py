@@ -17,6 +17,10 @@ GEMM's bytes in its launch shape (the HBM ceiling it is held against), and the C
 oracle's dequant + fp32 matmul, timed on this host). Prints ONE JSON line.
 
   python bench.py [--gpus 1] [--steps 1024] [--warmup 64]
+
+--steps K times exactly K verify-GEMM launches (one HIP graph of K launches between two events);
+--warmup W runs W untimed launches first. Before those, the same graph replays for one second to
+bring the clocks up; the line reports that separately (clock_warmup).
 """
 from __future__ import annotations
 
@@ -48,8 +52,10 @@ def gemm_bytes(M, N, K):
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=1024)
-    ap.add_argument("--warmup", type=int, default=64)
+    ap.add_argument("--steps", type=int, default=1024,
+                    help="verify-GEMM launches timed (exactly this many)")
+    ap.add_argument("--warmup", type=int, default=64,
+                    help="untimed verify-GEMM launches before them (after the clock warm-up)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only-verify", action="store_true", help="skip prefill and M=1 legs")
     ap.add_argument("--sweep", action="store_true",
@@ -74,8 +80,8 @@ class Gemm:
         self.M, self.N, self.K = M, N, K
         w, ws = synthetic.weights(N, K, seed)
         x = synthetic.activations(M, K, seed + 1)
-        xd = torch.from_numpy(x.view(np.int16)).cuda().view(torch.bfloat16)
-        self.q, self.s = R.quant_per_token(xd)
+        self.x = torch.from_numpy(x.view(np.int16)).cuda().view(torch.bfloat16)
+        self.q, self.s = R.quant_per_token(self.x)
         wq, sq = R.repack_weights(torch.from_numpy(w).cuda(), torch.from_numpy(ws).cuda())
         self.w = [wq] + [wq.clone() for _ in range(copies - 1)]
         self.ws = [sq] + [sq.clone() for _ in range(copies - 1)]
@@ -88,6 +94,16 @@ class Gemm:
         self._native.gemm(self.q.data_ptr(), self.s.data_ptr(), self.w[i].data_ptr(),
                           self.ws[i].data_ptr(), self.out.data_ptr(), self.M, self.N, self.K,
                           stream)
+
+
+class QuantGemm(Gemm):
+    """The linear as radiance::mxfp4_linear runs it: the per-token quantizer on bf16 activations,
+    then the GEMM (two launches per step)."""
+
+    def launch(self, i, stream):
+        self._native.quant_per_token(self.x.data_ptr(), self.K, self.q.data_ptr(),
+                                     self.s.data_ptr(), self.M, self.K, stream)
+        super().launch(i, stream)
 
 
 def per_launch_us(g, n, stream_obj):
@@ -110,72 +126,86 @@ WARM_SECONDS = 1.0
 
 
 def graph_timed(g, steps, warmup, warm_seconds=WARM_SECONDS):
-    """Capture one launch per weight copy into a HIP graph on a side stream, replay it on that same
-    stream (warmup, then the timed region) and return (steps run, warmup run, seconds, per-launch
-    event median/mean). The events bracket the timed replays on the stream the kernels run on.
-    Warmup runs at least `warmup` launches and at least `warm_seconds` of replays: MI355X raises
-    its clocks over the first few hundred milliseconds of load, and a cold GEMM reads up to 20 %
-    slow."""
+    """Time exactly `steps` launches after `warmup` untimed ones, on one side stream.
+
+    The timed launches are one HIP graph of `steps` launches (weight copies rotating), replayed
+    once between two events on the stream the kernels run on. Before the warmup launches the same
+    graph replays for at least `warm_seconds` (MI355X raises its clocks over the first few hundred
+    milliseconds of load; a cold GEMM reads up to 20 % slow), reported separately as the clock
+    warm-up. Its last four replays, the warmup launches, the first event and the timed replay are
+    queued without a synchronization in between, so the GPU never idles (and never drops its
+    clocks) before the timed launches start. Returns (seconds, clock warm-up dict, per-launch
+    event median, mean)."""
     import torch
     stream = torch.cuda.Stream()
     n = len(g.w)
     torch.cuda.synchronize()
     with torch.cuda.stream(stream):
-        for i in range(n):
-            g.launch(i, stream.cuda_stream)
+        g.launch(0, stream.cuda_stream)           # code objects loaded before capture
     stream.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
-        for i in range(n):
-            g.launch(i, stream.cuda_stream)
-    reps = max(1, -(-steps // n))
-    wreps = max(1, -(-warmup // n))
+        for i in range(steps):
+            g.launch(i % n, stream.cuda_stream)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
-        done, t_end = 0, time.perf_counter() + warm_seconds
-        while done < wreps or time.perf_counter() < t_end:
-            for _ in range(max(1, wreps)):
+        t0, replays = time.perf_counter(), 0
+        while True:
+            for _ in range(4):
                 graph.replay()
-            done += max(1, wreps)
-            torch.cuda.synchronize()
-        wreps = done
+            replays += 4
+            if time.perf_counter() - t0 >= warm_seconds:
+                break
+            stream.synchronize()
+        clock = dict(seconds=round(time.perf_counter() - t0, 3), launches=replays * steps)
+        for i in range(warmup):
+            g.launch(i % n, stream.cuda_stream)
         e0.record(stream)
-        for _ in range(reps):
-            graph.replay()
+        graph.replay()
         e1.record(stream)
     torch.cuda.synchronize()
     sec = e0.elapsed_time(e1) * 1e-3
     with torch.cuda.stream(stream):
         med_us, mean_us = per_launch_us(g, 64, stream)
     del graph
-    return reps * n, wreps * n, sec, med_us, mean_us
+    return sec, clock, med_us, mean_us
 
 
 def bench_verify(args):
     M, N, K = VERIFY["M"], VERIFY["N"], VERIFY["K"]
     g = Gemm(M, N, K, COPIES, seed=1)
-    steps, warm, sec, med_us, mean_us = graph_timed(g, args.steps, args.warmup)
+    sec, clock, med_us, mean_us = graph_timed(g, args.steps, args.warmup)
     nbytes = gemm_bytes(M, N, K)
-    us = sec / steps * 1e6
-    return dict(M=M, N=N, K=K, steps=steps, warmup=warm, ms_per_step=us * 1e-3,
-                gbs=nbytes / (us * 1e-6) / 1e9, bytes=nbytes, kernel_us=us,
-                event_pair_us_median=med_us, event_pair_us_mean=mean_us, plan=g.plan)
+    us = sec / args.steps * 1e6
+    return dict(M=M, N=N, K=K, steps=args.steps, warmup=args.warmup, clock_warmup=clock,
+                ms_per_step=us * 1e-3, gbs=nbytes / (us * 1e-6) / 1e9, bytes=nbytes,
+                kernel_us=us, event_pair_us_median=med_us, event_pair_us_mean=mean_us,
+                plan=g.plan)
 
 
 def bench_prefill():
+    """The M=4096 prefill GEMMs alone, and as config 4 states them: the per-token quantizer on
+    bf16 activations fused ahead of the GEMM (quant + GEMM per step, timed as one unit)."""
     import torch
     res = []
     for name, M, N, K in PREFILL:
         copies = max(2, -(-512 * 2 ** 20 // (N * K * 17 // 32)))
-        g = Gemm(M, N, K, copies, seed=7)
-        steps, _, sec, med_us, _ = graph_timed(g, 8 * copies, 2 * copies)
-        us = sec / steps * 1e6
         flop = 2.0 * M * N * K
-        tf = flop / (us * 1e-6) / 1e12
-        res.append(dict(name=name, M=M, N=N, K=K, us=round(us, 2), tflops=round(tf, 1),
-                        frac=round(tf / MFMA_PEAK_TFLOPS, 4), plan=g.plan))
-        del g
-        torch.cuda.empty_cache()
+        row = dict(name=name, M=M, N=N, K=K)
+        for key, cls in (("gemm", Gemm), ("quant_gemm", QuantGemm)):
+            g = cls(M, N, K, copies, seed=7)
+            sec, _, _, _ = graph_timed(g, 8 * copies, 2 * copies)
+            us = sec / (8 * copies) * 1e6
+            tf = flop / (us * 1e-6) / 1e12
+            if key == "gemm":
+                row.update(us=round(us, 2), tflops=round(tf, 1),
+                           frac=round(tf / MFMA_PEAK_TFLOPS, 4), plan=g.plan)
+            else:
+                row.update(quant_gemm_us=round(us, 2), quant_gemm_tflops=round(tf, 1),
+                           quant_gemm_frac=round(tf / MFMA_PEAK_TFLOPS, 4))
+            del g
+            torch.cuda.empty_cache()
+        res.append(row)
     return res
 
 
@@ -185,8 +215,8 @@ def bench_layer_m1():
     for name, N, K in LAYER_M1:
         copies = max(2, -(-512 * 2 ** 20 // (N * K * 17 // 32)))
         g = Gemm(1, N, K, copies, seed=3)
-        steps, _, sec, _, _ = graph_timed(g, 32 * copies, 4 * copies)
-        us = sec / steps * 1e6
+        sec, _, _, _ = graph_timed(g, 32 * copies, 4 * copies, warm_seconds=0.5)
+        us = sec / (32 * copies) * 1e6
         nb = gemm_bytes(1, N, K)
         tot_us += us
         tot_bytes += nb
@@ -275,8 +305,8 @@ def bench_quant():
     for M, K in QUANT_SHAPES:
         copies = max(2, min(16, -(-512 * 2 ** 20 // (2 * M * K))))
         g = Quant(M, K, copies, seed=31)
-        steps, _, sec, _, _ = graph_timed(g, 8 * copies, 2 * copies, warm_seconds=0.2)
-        us = sec / steps * 1e6
+        sec, _, _, _ = graph_timed(g, 8 * copies, 2 * copies, warm_seconds=0.2)
+        us = sec / (8 * copies) * 1e6
         gbs = g.bytes() / (us * 1e-6) / 1e9
         res.append(dict(M=M, K=K, us=round(us, 2), gbs=round(gbs, 1),
                         frac=round(gbs / HBM_PEAK_GBS, 4)))
@@ -301,8 +331,8 @@ def bench_producers():
             per_copy = 4 * M * N                         # bf16 input bytes per launch
             copies = max(2, min(16, -(-512 * 2 ** 20 // per_copy)))
             g = Producer(kind, M, N, copies, seed=21)
-            steps, _, sec, _, _ = graph_timed(g, 8 * copies, 2 * copies, warm_seconds=0.2)
-            us = sec / steps * 1e6
+            sec, _, _, _ = graph_timed(g, 8 * copies, 2 * copies, warm_seconds=0.2)
+            us = sec / (8 * copies) * 1e6
             gbs = g.bytes() / (us * 1e-6) / 1e9
             res.append(dict(op=kind, M=M, N=N, us=round(us, 2), gbs=round(gbs, 1),
                             frac=round(gbs / HBM_PEAK_GBS, 4)))
@@ -333,8 +363,8 @@ def bench_read_probe(steps, warmup):
     traffic, the same rotation over 16 copies and the same graph replay, nothing but reads."""
     import torch
     g = ReadProbe(gemm_bytes(VERIFY["M"], VERIFY["N"], VERIFY["K"]), COPIES)
-    n_steps, _, sec, _, _ = graph_timed(g, steps, warmup, warm_seconds=0.5)
-    us = sec / n_steps * 1e6
+    sec, _, _, _ = graph_timed(g, steps, warmup, warm_seconds=0.5)
+    us = sec / steps * 1e6
     gbs = g.n / (us * 1e-6) / 1e9
     del g
     torch.cuda.empty_cache()
@@ -388,6 +418,9 @@ def cpu_baseline():
 
 
 SWEEP_M = [1, 8, 16, 64, 512, 4096]
+# the default run's sweep: 16 layers keep each shape's weight set (0.27-0.76 GB) above the 256 MB
+# MALL, so no forward is served from the last-level cache; --sweep runs all 64
+SWEEP_LAYERS_DEFAULT = 16
 CROSSOVER_M = [8, 16, 17, 24, 32, 48, 64, 96, 128]
 
 
@@ -493,10 +526,11 @@ def bench_sweep(n_layers):
               f"({forward[-1]['per_shape_us_per_layer']} us per layer)", file=sys.stderr,
               flush=True)
 
-    # crossover: GEMM only (pre-quantized activations), 16 layers' weights rotating. The decode
-    # family is the streaming kernel where it serves (M <= 16), else the skinny kernel with the
-    # M-fragments covering M; the tile family is the macro-tile shape the plan picks at M.
-    skinny = _native.variants(_native.KERNEL_SKINNY)
+    # crossover: GEMM only (pre-quantized activations), up to 16 layers' weights rotating. The
+    # decode family is the streaming kernel where it serves (M <= 16), else the pipelined ring
+    # kernel with the fragments covering M (its first variant that serves the shape); the tile
+    # family is the macro tile the plan takes just above the ring's band (M = 21 .. 64), or at M.
+    ring = _native.variants(_native.KERNEL_RING)
     cross = {}
     for name, N, K in LAYER_M1:
         rows = []
@@ -504,6 +538,7 @@ def bench_sweep(n_layers):
             q, sc = R.quant_per_token(xs[(4096, K)][:M].contiguous())
             out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
             lins = layers[name][:16]
+            per = len(lins)
 
             def run(kernel, variant, split, q=q, sc=sc, out=out, lins=lins, M=M):
                 for lin in lins:
@@ -511,19 +546,23 @@ def bench_sweep(n_layers):
                                  lin.weight_scale.data_ptr(), out.data_ptr(), M, N, K,
                                  torch.cuda.current_stream().cuda_stream, kernel, variant, split)
 
-            tile_v = _native.plan(max(M, 24), N, K)[1]     # the tile plan's shape at M <= 32
-            row = dict(M=M, tile_us=round(_timed_graph(
-                lambda: run(_native.KERNEL_TILE, tile_v, 1), 5) * 1e3 / 16, 2))
             k, v, sp = _native.plan(M, N, K)
+            tile_v = v if k == _native.KERNEL_TILE else _native.plan(min(max(M, 21), 64), N, K)[1]
+            row = dict(M=M, tile_us=round(_timed_graph(
+                lambda: run(_native.KERNEL_TILE, tile_v, 1), 5) * 1e3 / per, 2))
             if k != _native.KERNEL_STREAM and M <= 64:
-                ntiles = -(-N // 16)
-                waves = 4 if ntiles >= 512 else 8 if ntiles >= 128 else 16
-                k, sp = _native.KERNEL_SKINNY, 1
-                v = next(i for i, c in enumerate(skinny)
-                         if c[0] == -(-M // 16) and c[1] == 1 and c[2] == waves)
-            if k != _native.KERNEL_TILE:
-                row["decode_us"] = round(_timed_graph(lambda: run(k, v, sp), 5) * 1e3 / 16, 2)
-                row["decode_kernel"] = "stream" if k == _native.KERNEL_STREAM else "skinny"
+                mf = -(-M // 16)
+                k, sp = _native.KERNEL_RING, 1
+                v = next((i for i, c in enumerate(ring) if c[0] == mf), None)
+                if k == _native.KERNEL_RING and M <= 20 and _native.plan(M, N, K)[0] == k:
+                    v = _native.plan(M, N, K)[1]
+            if k != _native.KERNEL_TILE and v is not None:
+                try:
+                    row["decode_us"] = round(_timed_graph(lambda: run(k, v, sp), 5) * 1e3 / per,
+                                             2)
+                    row["decode_kernel"] = "stream" if k == _native.KERNEL_STREAM else "ring"
+                except RuntimeError:
+                    pass
             rows.append(row)
         tile_wins = [r["M"] for r in rows if "decode_us" in r and r["tile_us"] <= r["decode_us"]]
         cross[name] = dict(rows=rows, tile_wins_from_M=min(tile_wins) if tile_wins else None)
@@ -531,7 +570,7 @@ def bench_sweep(n_layers):
     return dict(layers=n_layers, weight_gb=round(weight_bytes * n_layers / 1e9, 3),
                 repack_ms_per_layer_median=round(float(np.median(repack_ms)), 4),
                 repack_ms_total=round(float(np.sum(repack_ms)), 2), forward=forward,
-                crossover=cross, plan_stream_max_M=16)
+                crossover=cross, plan_stream_max_M=16, plan_ring_max_M=20)
 
 
 CALIBRATION_BYTES = 256 * 2 ** 20
@@ -621,7 +660,7 @@ def main():
     print(f"[bench] verify M=8: {v['kernel_us']:.2f} us/launch in the graph-timed region, "
           f"event pairs {v['event_pair_us_median']:.2f} us median, plan {v['plan']}",
           file=sys.stderr, flush=True)
-    prefill = layer = producers = quant = None
+    prefill = layer = producers = quant = sweep = None
     if not args.only_verify:
         prefill = bench_prefill()
         print(f"[bench] prefill: {prefill}", file=sys.stderr, flush=True)
@@ -631,6 +670,7 @@ def main():
         print(f"[bench] producers: {producers}", file=sys.stderr, flush=True)
         quant = bench_quant()
         print(f"[bench] quantizer: {quant}", file=sys.stderr, flush=True)
+        sweep = bench_sweep(SWEEP_LAYERS_DEFAULT)
     probe = mfma_probe()
     print(f"[bench] MFMA probe TFLOP/s: {probe}", file=sys.stderr, flush=True)
     rprobe = bench_read_probe(args.steps, args.warmup)
@@ -645,6 +685,7 @@ def main():
         "n_gpus": 1,
         "steps": v["steps"],
         "warmup": v["warmup"],
+        "clock_warmup": v["clock_warmup"],
         "ms_per_step": round(v["ms_per_step"], 6),
         "higher_is_better": True,
         "scaling": "weak",
@@ -668,6 +709,7 @@ def main():
         "decode_m1_layer": layer,
         "producers": producers,
         "quantizer": quant,
+        "sweep": sweep,
     }
     print(json.dumps(line), flush=True)
 

@@ -35,7 +35,13 @@ enum {
   W4A8_EHIP = 3       /* the HIP runtime reported an error at launch */
 };
 
-enum { W4A8_KERNEL_AUTO = 0, W4A8_KERNEL_SKINNY = 1, W4A8_KERNEL_TILE = 2, W4A8_KERNEL_STREAM = 3 };
+enum {
+  W4A8_KERNEL_AUTO = 0,
+  W4A8_KERNEL_SKINNY = 1,  /* split-K skinny kernel, any M <= 64 */
+  W4A8_KERNEL_TILE = 2,    /* LDS-pipelined macro tiles (prefill) */
+  W4A8_KERNEL_STREAM = 3,  /* whole k-range of every wave in flight at once, M <= 16 */
+  W4A8_KERNEL_RING = 4     /* per-wave pipeline of k-tile stages, M <= 64 */
+};
 
 /* ABI version of the loaded library (W4A8_ABI_VERSION). */
 int w4a8_abi_version(void);
@@ -103,7 +109,10 @@ int w4a8_gemm_planned(const void* a, const float* a_scale, const void* wq, const
  * stream: p = {NT (n-tiles per workgroup at most), KPW (k-tiles per wave at most), waves,
  *         NT * KPW (granules per wave at most)}. A stream variant serves (M, N, K) only when
  *         M <= 16, K % 512 == 0 and the shape's n-tiles per workgroup and k-tiles per wave fit it;
- *         forcing one that does not returns W4A8_EINVAL. */
+ *         forcing one that does not returns W4A8_EINVAL.
+ * ring:   p = {MF (16-token fragments), NT (n-tiles per workgroup at most), D (k-tile stages in
+ *         flight per wave), waves}. A ring variant serves (M, N, K) when M <= 16 * MF, the
+ *         shape's n-tiles per workgroup fit NT and every wave owns a k-tile. */
 int w4a8_variant_count(int kernel);
 int w4a8_variant_info(int kernel, int variant, int* p0, int* p1, int* p2, int* p3);
 

@@ -61,6 +61,35 @@ def gemm_errors(out_bits: np.ndarray, q, s, w, ws):
             float(np.mean(err <= ULP_MAX * ulp)))
 
 
+def parity_stats(out_bits: np.ndarray, q, s, w, ws):
+    """The figures of one parity-table cell: rel-L2 against bf16(ref), the worst ratio to the
+    per-element allowance, max error in bf16 ulp of ref and the fraction of outputs more than
+    ULP_MAX ulp from ref, for the kernel's output and, as the floor any implementation faces, for
+    the exact result rounded to bf16 (the products summed in float64 with no truncation). Outputs
+    that cancel far below their terms have bf16 ulps smaller than the fp32 reference's own
+    rounding error, so even the exact result misses the 2-ulp clause on some of them."""
+    ref = O.gemm_ref_f32(q, s, w, ws).astype(np.float64)
+    refb = O.bf16_to_f32(O.f32_to_bf16(ref.astype(np.float32))).astype(np.float64)
+    out = O.bf16_to_f32(out_bits).astype(np.float64)
+    terms = O.gemm_abs_terms(q, s, w, ws)
+    xr = O.e4m3fn_decode(q).astype(np.float64) * np.asarray(s, np.float64)[:, None]
+    exact = np.empty_like(ref)
+    for a in range(0, w.shape[0], 2048):
+        exact[:, a:a + 2048] = xr @ O.dequant_weight(w[a:a + 2048], ws[a:a + 2048]) \
+            .astype(np.float64).T
+    exactb = O.bf16_to_f32(O.f32_to_bf16(exact.astype(np.float32))).astype(np.float64)
+    ulp = O.bf16_ulp(ref)
+    err, err_x = np.abs(out - ref), np.abs(exactb - ref)
+    allow = ULP_MAX * ulp + HW_ACC_EPS * terms
+    return dict(rel_l2=float(np.linalg.norm(out - refb) / max(np.linalg.norm(refb), 1e-300)),
+                worst_over_allowance=float(np.max(err / allow)),
+                max_ulp=float(np.max(err / ulp)),
+                frac_beyond_2ulp=float(np.mean(err > ULP_MAX * ulp)),
+                exact_max_ulp=float(np.max(err_x / ulp)),
+                exact_frac_beyond_2ulp=float(np.mean(err_x > ULP_MAX * ulp)),
+                outputs=int(out.size))
+
+
 def assert_gemm_close(out_bits: np.ndarray, q, s, w, ws, what: str = ""):
     rel, ratio, ulps, within = gemm_errors(out_bits, q, s, w, ws)
     print(f"[parity] {what}: rel_l2={rel:.3e} worst/allowance={ratio:.3f} max_ulp={ulps:.2f} "

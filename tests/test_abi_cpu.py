@@ -107,14 +107,14 @@ def test_split_k_without_scratch_is_refused(lib):
 def test_plan_bands(lib):
     k, v, s = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     # M <= 16: the streaming family when a wave's run and the LDS staging fit, else skinny; above
-    # M = 16 the macro-tile family, except skinny up to M = 21 on N = 2048 .. 5120. N=17408 K=8704
-    # would need 43-granule runs, past the largest stream variant; K=640 has fewer k-tiles per
-    # n-tile than the smallest run.
+    # M = 16 the macro-tile family, except the ring kernel up to M = 20 on N up to 10240.
+    # N=17408 K=8704 would need 43-granule runs, past the largest stream variant; K=640 has fewer
+    # k-tiles per n-tile than the smallest run.
     for M, N, K, kernel in [(1, 17408, 5120, 3), (8, 17408, 5120, 3), (16, 17408, 5120, 3),
                             (8, 5120, 8704, 3), (8, 17408, 8704, 1), (8, 33, 640, 1),
                             (17, 17408, 5120, 2), (64, 17408, 5120, 2), (65, 17408, 5120, 2),
-                            (17, 5120, 6144, 1), (21, 5120, 8704, 1), (22, 5120, 8704, 2),
-                            (21, 10240, 5120, 2), (17, 1024, 6144, 2),
+                            (17, 5120, 6144, 4), (20, 5120, 8704, 4), (21, 5120, 8704, 2),
+                            (20, 10240, 5120, 4), (17, 1024, 6144, 4), (20, 10256, 5120, 2),
                             (4096, 17408, 5120, 2)]:
         assert lib.w4a8_plan(M, N, K, ctypes.byref(k), ctypes.byref(v), ctypes.byref(s)) == 0
         assert (M, N, K, k.value) == (M, N, K, kernel) and v.value >= 0 and s.value >= 1
@@ -122,10 +122,14 @@ def test_plan_bands(lib):
 
 
 @pytest.mark.parametrize("M,N,K,tile", [
-    # small M: the first tile (32x64, 64x64, 32x128, 64x128, 128x128, 128x256) whose workgroup
+    # decode band above 20 tokens: 32 (M <= 32) or 64 tokens tall, as narrow as keeps the
+    # workgroups within one per CU (256 CUs)
+    (24, 5120, 8704, (32, 32)), (32, 10240, 5120, (32, 64)), (32, 17408, 5120, (32, 96)),
+    (33, 5120, 6144, (64, 32)), (64, 17408, 5120, (64, 96)), (64, 5120, 8704, (64, 32)),
+    (64, 10240, 5120, (64, 64)), (64, 65536, 5120, (64, 128)),
+    # M > 64: the first tile (32x64, 64x64, 32x128, 64x128, 128x128, 128x256) whose workgroup
     # count stays within 5/8 of 256 CUs
-    (32, 10240, 5120, (32, 64)), (32, 17408, 5120, (32, 128)), (64, 17408, 5120, (64, 128)),
-    (64, 5120, 8704, (32, 64)), (64, 10240, 5120, (64, 64)), (128, 5120, 6144, (64, 64)),
+    (128, 5120, 6144, (64, 64)),
     (128, 17408, 5120, (128, 128)), (256, 10240, 5120, (128, 128)),
     (256, 17408, 5120, (128, 256)),
     # 256 < M < 1024: 256 x 160 when those tiles fill one round at least half, else 128 x 128

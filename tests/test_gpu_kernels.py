@@ -19,6 +19,7 @@ from vllm_sly_radiance_amd import _native, synthetic
 pytestmark = pytest.mark.gpu
 
 SKINNY, TILE, STREAM = _native.KERNEL_SKINNY, _native.KERNEL_TILE, _native.KERNEL_STREAM
+RING = _native.KERNEL_RING
 
 
 @pytest.fixture(scope="module")
@@ -348,6 +349,33 @@ def test_gemm_every_stream_variant(gpu_lib, N, K):
     assert (ran > 0) == served
 
 
+@pytest.mark.parametrize("N,K", [(17408, 5120), (5120, 8704), (1040, 2560), (33, 640),
+                                 (5120, 6144), (10240, 5120), (48, 1056), (2064, 4128)])
+def test_gemm_every_ring_variant(gpu_lib, N, K):
+    """The pipelined streaming family at every variant that serves (M, N, K): M up to each
+    variant's fragments (ragged), N ragged against the n-tile shares, K ending inside a k-tile
+    (1056) or a k-group (640, 4128), ranges whose last round is padded. A variant that does not
+    serve a shape (n-tiles per workgroup beyond NT, fewer k-tiles than waves) must refuse it."""
+    w, ws = cached_weights(N, K, N + 5 * K)
+    wq, sq = gpu_repack(w, ws)
+    ran = 0
+    for M in (1, 5, 16, 17, 33, 48, 64):
+        x = synthetic.activations(M, K, seed=3 * M + K)
+        q, s = O.quant_per_token(x)
+        for v, cfg in enumerate(_native.variants(RING)):
+            if M > 16 * cfg[0]:
+                continue
+            print(f"[ring] M={M} N={N} K={K} variant {v} {cfg}", flush=True)
+            try:
+                out = gpu_gemm(q, s, wq, sq, N, K, RING, v, 1)
+            except RuntimeError as e:
+                assert "does not serve" in str(e)
+                continue
+            ran += 1
+            assert_gemm_close(out, q, s, w, ws, f"M={M} N={N} K={K} ring variant {v} {cfg}")
+    assert ran > 0
+
+
 # K = 640, 96 and 1056 end inside a k-group: the k-loop runs whole k-groups over zero slabs
 @pytest.mark.parametrize("M,N,K", [(65, 544, 1024), (300, 1040, 2560), (1000, 17408 // 8, 5120),
                                    (129, 33, 640), (513, 5120, 8704), (70, 200, 96),
@@ -457,15 +485,16 @@ BASELINE_SHAPES = [(10240, 5120), (5120, 6144), (17408, 5120), (5120, 8704)]
 def test_plugin_scratch_covers_every_automatic_plan(gpu_lib):
     """The scratch the plugin registers (w4a8_workspace_bytes for M <= 64, N <= 36864) lets the
     automatic plan take every split it would take with unlimited room: the plans agree on the
-    Qwen3.8-27B linear shapes and on every N up to 2048 (where the decode band splits K), at
-    every M of the decode band and K of the model."""
+    Qwen3.8-27B linear shapes, and on every N up to 2048 at K = 1056 and 4128 (K not a multiple
+    of 512: the streaming kernel cannot serve them, so the decode band splits K across workgroups
+    when N is small), at every M of the decode band."""
     from vllm_sly_radiance_amd import radiance_mxfp4 as R
     R.ensure_scratch("cuda")
     part, cnt = R._scratch
     assert part.numel() * 4 < 8 << 20, "the plugin scratch should be a few MB at most"
     big_p = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
     big_c = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
-    shapes = BASELINE_SHAPES + [(n, k) for n in range(16, 2049, 16) for k in (5120, 8704)]
+    shapes = BASELINE_SHAPES + [(n, k) for n in range(16, 2049, 16) for k in (1056, 4128)]
     ms = list(range(1, 65))
     try:
         plans = {}

@@ -1,0 +1,70 @@
+"""GEMM parity at every cell of the benchmark configurations, through the automatic plan: the four
+Qwen3.8-27B linear shapes (qkv 10240x5120, o_proj 5120x6144, gate_up 17408x5120, down 5120x8704)
+at M = 1, 8, 16, 64, 512 and 4096 (192 sampled token rows at 4096, every column), plus the
+CPU-plumbing shape 5120x5120 at M = 8.
+
+Asserted per cell: rel-L2 <= 1e-3 against bf16 of the fp32-accumulated reference, and every output
+within 2 bf16 ulp of it plus the scaled MFMA's measured accumulation allowance (tests/_check.py).
+The strict 2-ulp clause alone is reported, not asserted: the exact result rounded to bf16 misses it
+too on outputs that cancel (their ulp is below the fp32 reference's own rounding error), so each
+cell prints the kernel's max ulp and fraction beyond 2 ulp next to the exact result's, and asserts
+that the kernel's fraction beyond 2 ulp stays under FRAC_BEYOND_2ULP_MAX."""
+import functools
+import json
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import mxfp4_oracle as O
+from tests._check import REL_L2_MAX, host_u16, parity_stats, stream, to_dev
+from vllm_sly_radiance_amd import _native, synthetic
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = {"qkv": (10240, 5120), "o_proj": (5120, 6144), "gate_up": (17408, 5120),
+          "down": (5120, 8704)}
+MS = [1, 8, 16, 64, 512, 4096]
+CELLS = [(name, M) for name in SHAPES for M in MS] + [("plumbing", 8)]
+SAMPLED_ROWS = 192
+# the measured fraction of outputs beyond 2 ulp is 0.03-0.1 % on these cells (the exact result's
+# own is 0-0.003 %); a layout or scale mistake puts most outputs beyond it
+FRAC_BEYOND_2ULP_MAX = 5e-3
+
+
+@functools.lru_cache(maxsize=2)
+def layer(name):
+    N, K = (5120, 5120) if name == "plumbing" else SHAPES[name]
+    w, ws = synthetic.weights(N, K, seed=N + 3 * K)
+    wb, sb = _native.packed_bytes(N, K)
+    wq = torch.empty(wb, dtype=torch.uint8, device="cuda")
+    sq = torch.empty(sb, dtype=torch.uint8, device="cuda")
+    wd, sd = to_dev(w), to_dev(ws)
+    _native.repack(wd.data_ptr(), sd.data_ptr(), wq.data_ptr(), sq.data_ptr(), N, K, stream())
+    torch.cuda.synchronize()
+    return N, K, w, ws, wq, sq
+
+
+@pytest.mark.parametrize("name,M", CELLS)
+def test_parity_cell(gpu_lib, name, M):
+    N, K, w, ws, wq, sq = layer(name)
+    plan = _native.plan(M, N, K)
+    print(f"[parity] {name} M={M} N={N} K={K} plan {plan}", flush=True)
+    q, s = O.quant_per_token(synthetic.activations(M, K, seed=7 * M + K))
+    out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    qd, sd = to_dev(q), to_dev(s)
+    _native.gemm(qd.data_ptr(), sd.data_ptr(), wq.data_ptr(), sq.data_ptr(), out.data_ptr(), M, N,
+                 K, stream())
+    torch.cuda.synchronize()
+    bits = host_u16(out)
+    rows = np.arange(M)
+    if M > 512:
+        rows = np.unique(np.concatenate([np.random.default_rng(M).choice(M, SAMPLED_ROWS - 2,
+                                                                         replace=False),
+                                         [0, M - 1]]))
+    st = parity_stats(bits[rows], q[rows], s[rows], w, ws)
+    st.update(cell=name, M=M, N=N, K=K, plan=list(plan), rows_checked=int(len(rows)))
+    print("[parity-table] " + json.dumps(st), flush=True)
+    assert st["rel_l2"] <= REL_L2_MAX, st
+    assert st["worst_over_allowance"] <= 1.0, st
+    assert st["frac_beyond_2ulp"] <= FRAC_BEYOND_2ULP_MAX, st

@@ -14,7 +14,7 @@ import threading
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libw4a8_mxfp4.so")
 ABI_VERSION = 1
-KERNEL_AUTO, KERNEL_SKINNY, KERNEL_TILE, KERNEL_STREAM = 0, 1, 2, 3
+KERNEL_AUTO, KERNEL_SKINNY, KERNEL_TILE, KERNEL_STREAM, KERNEL_RING = 0, 1, 2, 3, 4
 
 _c = ctypes
 _vp, _int, _long, _sz = _c.c_void_p, _c.c_int, _c.c_long, _c.c_size_t

@@ -33,9 +33,8 @@ int hip_status(hipError_t e, const char* what) {
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
-// Split-K scratch: fp32 partials and int counters. A view names one buffer; the registered one is
-// caller-owned (w4a8_set_scratch, once per device at load time), the static one belongs to the
-// allocation-free entry point (below).
+// Split-K scratch: fp32 partials and int counters. A view names one buffer: the registered one is
+// caller-owned (w4a8_set_scratch, once per device at load time).
 struct Scratch {
   float* partial = nullptr;
   size_t partial_bytes = 0;
@@ -133,6 +132,14 @@ bool scratch_fits(const Scratch& s, int variant, int N, int split_k) {
 
 Scratch registered_scratch(int dev) { return dev >= 0 ? g_scratch[dev] : Scratch{}; }
 
+int find_ring(int mf, int nt, int d, int waves) {
+  for (int v = 0; v < ring_variant_count(); ++v) {
+    const RingCfg c = ring_variant(v);
+    if (c.mf == mf && c.nt == nt && c.d == d && c.waves == waves) return v;
+  }
+  return -1;
+}
+
 // The stream variant that serves (M, N, K) with the fewest granules on its busiest wave, then the
 // fewest n-tile slots, then the fewest waves.
 int find_stream(int M, int N, int K, int dev) {
@@ -169,8 +176,7 @@ int small_m_tile(int M, int N, int cus) {
 // Decode / verify band: M <= 16 takes the streaming family when a variant fits (whole-K
 // workgroups, every weight load in flight at once), else the skinny family, whose workgroup count
 // should cover the 256 CUs several times over (for small N the K dimension is split across
-// workgroups too). Above M = 16 the macro-tile family wins on every Qwen3.8-27B shape, except up
-// to M = 21 on N = 2048 .. 5120 (below).
+// workgroups too). 16 < M <= 64: the ring kernel or narrow macro tiles (below).
 void plan_impl(int M, int N, int K, int dev, const Scratch& sc, int* kernel, int* variant,
                int* split_k) {
   if (M <= 16) {
@@ -195,19 +201,35 @@ void plan_impl(int M, int N, int K, int dev, const Scratch& sc, int* kernel, int
     *split_k = ks;
     return;
   }
-  // Just above the streaming band on N = 2048 .. 5120: the skinny kernel with two 16-row
-  // M-fragments (one n-tile per wave, 8 waves) beats the smallest macro tile up to M = 21 (N = 5120,
-  // K = 6144: 11.2-12.1 against 12.3 us; K = 8704: 14.5-15.9 against 16.9 us); from M = 22 the tile
-  // wins, and on wider N it wins from M = 17.
-  if (M <= 21) {
+  // Decode band above 16 tokens (measured on MI355X, every ring and every tile variant up to
+  // 64 x 128 on the four Qwen3.8-27B linear shapes at M = 17 .. 64):
+  //  * up to M = 20 on N up to 10240 the pipelined ring kernel with two fragments (3 n-tiles per
+  //    workgroup, 7 stages, 4 waves) is fastest (M = 17: qkv 10.95, o_proj 9.85, down 13.16 us
+  //    against 11.30, 10.23, 13.55 on the best tile);
+  //  * otherwise a macro tile BM = 32 (M <= 32) or 64 tokens tall and as narrow as keeps the
+  //    workgroups within one per CU: the weight stream then runs on as many CUs as the shape has
+  //    columns for (N = 5120: 32-column tiles, 160 workgroups; 10240: 64; 17408: 96 columns, 182
+  //    workgroups). gate_up M = 64: 16.3 us against 17.6 on 64 x 128; down M = 32: 13.6 against
+  //    17.0 on 32 x 64.
+  if (M <= 64) {
     const int ntiles = padded_n(N) / kNTile;
-    const int v = find_skinny(2, 1, 8);
-    if (ntiles >= 128 && ntiles <= 320 && v >= 0) {
-      *kernel = W4A8_KERNEL_SKINNY;
-      *variant = v;
-      *split_k = 1;
-      return;
+    const DeviceInfo d = device_info(dev);
+    if (M <= 20 && ntiles <= 640) {
+      const int v = find_ring(2, 3, 7, 4);
+      if (v >= 0 && ring_fits(v, M, N, K, d.cus, d.lds)) {
+        *kernel = W4A8_KERNEL_RING;
+        *variant = v;
+        *split_k = 1;
+        return;
+      }
     }
+    const int wm = M <= 32 ? 1 : 2, bm = 32 * wm;
+    int wn = 1;
+    while (wn < 4 && (long)ceil_div(M, bm) * ceil_div(N, 32 * wn) > d.cus) ++wn;
+    *kernel = W4A8_KERNEL_TILE;
+    *variant = find_tile(wm, wn, 4, wm == 2 && wn == 2 ? 5 : 0);   // 64 x 64: 5 stages
+    *split_k = 1;
+    return;
   }
   // Prefill band (measured on MI355X, every tile variant on the four Qwen3.8-27B linear shapes at
   // M = 32 .. 2048): 8-wave 256 x 256 tiles for wide N (the automatic path splits N so the last
@@ -299,6 +321,15 @@ int gemm_dispatch(const void* a, const float* as, const void* wq, const void* sq
       return fail(W4A8_EINVAL, "%s: M=%d K=%d exceeds the tile kernel's 32-bit offsets", who,
                   M, K);
     return hip_status(launch_tile(g, variant, st), who);
+  }
+  if (kernel == W4A8_KERNEL_RING) {
+    if (variant < 0 || variant >= ring_variant_count())
+      return fail(W4A8_EINVAL, "%s: ring variant %d out of range", who, variant);
+    const DeviceInfo d = device_info(current_device());
+    if (!ring_fits(variant, M, N, K, d.cus, d.lds))
+      return fail(W4A8_EINVAL, "%s: ring variant %d does not serve M=%d N=%d K=%d", who, variant,
+                  M, N, K);
+    return hip_status(launch_ring(g, variant, d.cus, st), who);
   }
   if (kernel == W4A8_KERNEL_STREAM) {
     if (variant < 0 || variant >= stream_variant_count())
@@ -416,6 +447,7 @@ W4A8_API int w4a8_variant_count(int kernel) {
   if (kernel == W4A8_KERNEL_SKINNY) return skinny_variant_count();
   if (kernel == W4A8_KERNEL_TILE) return tile_variant_count();
   if (kernel == W4A8_KERNEL_STREAM) return stream_variant_count();
+  if (kernel == W4A8_KERNEL_RING) return ring_variant_count();
   fail(W4A8_EINVAL, "w4a8_variant_count: unknown kernel %d", kernel);
   return -1;
 }
@@ -431,6 +463,9 @@ W4A8_API int w4a8_variant_info(int kernel, int variant, int* p0, int* p1, int* p
   } else if (kernel == W4A8_KERNEL_STREAM && variant >= 0 && variant < stream_variant_count()) {
     const StreamCfg c = stream_variant(variant);
     v[0] = c.nt; v[1] = c.kpw; v[2] = c.waves; v[3] = c.u;
+  } else if (kernel == W4A8_KERNEL_RING && variant >= 0 && variant < ring_variant_count()) {
+    const RingCfg c = ring_variant(variant);
+    v[0] = c.mf; v[1] = c.nt; v[2] = c.d; v[3] = c.waves;
   } else {
     return fail(W4A8_EINVAL, "w4a8_variant_info: no variant %d of kernel %d", variant, kernel);
   }

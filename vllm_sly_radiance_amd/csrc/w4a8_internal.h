@@ -147,6 +147,17 @@ int stream_granules(int variant, int N, int K, int cus);
 bool stream_fits(int variant, int M, int N, int K, int cus, size_t lds_limit);
 hipError_t launch_stream(const GemmArgs& g, int variant, int cus, hipStream_t stream);
 
+// Pipelined streaming family (M <= 16 * MF): grid = at most one workgroup per CU, each with the
+// same number of n-tiles (at most nt) and all of K; each of the `waves` waves streams a contiguous
+// k-range with d k-tile stages in flight. variant indexes the instantiated table.
+struct RingCfg { int mf, nt, d, waves; };
+int ring_variant_count();
+RingCfg ring_variant(int v);
+int ring_grid(int variant, int N, int cus);
+size_t ring_lds_bytes(int variant, int K);
+bool ring_fits(int variant, int M, int N, int K, int cus, size_t lds_limit);
+hipError_t launch_ring(const GemmArgs& g, int variant, int cus, hipStream_t stream);
+
 // Macro-tile family (M > 16). variant indexes the instantiated (WM, WN, NS, NW) table: nw waves of
 // wm x wn 16 x 16 MFMA tiles, a bm x bn workgroup tile.
 struct TileCfg { int wm, wn, bm, bn, nw, lds, ns; };
