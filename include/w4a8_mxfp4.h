@@ -103,6 +103,18 @@ int w4a8_plan(int M, int N, int K, int* kernel, int* variant, int* split_k);
 int w4a8_gemm_planned(const void* a, const float* a_scale, const void* wq, const void* sq, void* c,
                       int M, int N, int K, int kernel, int variant, int split_k, void* stream);
 
+/* w4a8_gemm_planned that allocates nothing and needs no registered scratch, for callers that
+ * cannot allocate or register device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. Split-K partials and counters
+ * live in a static device array of the library (4 MiB + 16 KiB per device, held until the process
+ * ends); the automatic plan takes only splits that fit it, and a forced plan needing more returns
+ * W4A8_ESCRATCH. The first call on a device finds the array's address and queues the clearing of
+ * its counters on `stream`. Every call on a device shares the array: calls that overlap on one
+ * device race and must be ordered by the caller (one stream, or events). Same kernels, plans and
+ * results as w4a8_gemm_planned with enough registered scratch. */
+int w4a8_gemm_noalloc(const void* a, const float* a_scale, const void* wq, const void* sq, void* c,
+                      int M, int N, int K, int kernel, int variant, int split_k, void* stream);
+
 /* Number of instantiated variants of a kernel family, and their parameters:
  * skinny: p = {MT (16-token fragments), NT (n-tiles per workgroup), waves, unroll};
  * tile:   p = {WM, WN (MFMA tiles per wave), BM, BN (workgroup tile)};

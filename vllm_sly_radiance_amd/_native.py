@@ -33,6 +33,8 @@ SIGNATURES = {
     "w4a8_plan": (_int, [_int, _int, _int, _pint, _pint, _pint]),
     "w4a8_gemm_planned": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _int, _int,
                                  _vp]),
+    "w4a8_gemm_noalloc": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _int, _int,
+                                 _vp]),
     "w4a8_variant_count": (_int, [_int]),
     "w4a8_variant_info": (_int, [_int, _int, _pint, _pint, _pint, _pint]),
     "w4a8_scratch_bytes": (_int, [_int, _int, _int, _psz, _psz]),
@@ -92,6 +94,13 @@ def repack(w_ptr, ws_ptr, wq_ptr, sq_ptr, N, K, stream):
 def gemm(a_ptr, as_ptr, wq_ptr, sq_ptr, c_ptr, M, N, K, stream, kernel=KERNEL_AUTO, variant=-1,
          split_k=0):
     check(lib().w4a8_gemm_planned(a_ptr, as_ptr, wq_ptr, sq_ptr, c_ptr, M, N, K, kernel, variant,
+                                  split_k, stream))
+
+
+def gemm_noalloc(a_ptr, as_ptr, wq_ptr, sq_ptr, c_ptr, M, N, K, stream, kernel=KERNEL_AUTO,
+                 variant=-1, split_k=0):
+    """gemm() on the library's static scratch: allocates nothing, needs no set_scratch."""
+    check(lib().w4a8_gemm_noalloc(a_ptr, as_ptr, wq_ptr, sq_ptr, c_ptr, M, N, K, kernel, variant,
                                   split_k, stream))
 
 

@@ -11,6 +11,14 @@
 
 #define W4A8_API extern "C" __attribute__((visibility("default")))
 
+// ---- scratch of the allocation-free entry point (w4a8_gemm_noalloc) -----------------------------
+// One copy per device in the code object's static data, held until the process ends: split-K
+// partials first, then the counters. Every call on a device shares it; the counters start at
+// zero (cleared at set-up) and each split reduction's last workgroup resets the ones it used.
+constexpr size_t kStaticPartialBytes = 4u << 20;
+constexpr size_t kStaticCounterBytes = 16u << 10;
+static __device__ __align__(256) uint8_t scratch[kStaticPartialBytes + kStaticCounterBytes];
+
 namespace {
 
 using namespace w4a8;
@@ -33,8 +41,9 @@ int hip_status(hipError_t e, const char* what) {
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
-// Split-K scratch: fp32 partials and int counters. A view names one buffer: the registered one is
-// caller-owned (w4a8_set_scratch, once per device at load time).
+// Split-K scratch: fp32 partials and int counters. A view names one buffer; the registered one is
+// caller-owned (w4a8_set_scratch, once per device at load time), the static one belongs to the
+// allocation-free entry point (below).
 struct Scratch {
   float* partial = nullptr;
   size_t partial_bytes = 0;
@@ -486,6 +495,46 @@ W4A8_API int w4a8_scratch_bytes(int variant, int N, int split_k, size_t* partial
   return W4A8_OK;
 }
 
+namespace {
+
+__global__ void clear_words(int* p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
+}
+
+// The device address of this device's static scratch, found once per device (with the device
+// current) by hipGetSymbolAddress; the host-side name `scratch` is not a device address. The first
+// call on a device also queues the counters' clear on its stream, ahead of its own launches.
+std::mutex g_static_fill;
+uint8_t* g_static_addr[kMaxDevices];
+std::atomic<bool> g_static_set[kMaxDevices];
+
+int static_scratch(int dev, hipStream_t st, Scratch* out) {
+  if (dev < 0) return fail(W4A8_EHIP, "w4a8_gemm_noalloc: no current HIP device");
+  if (!g_static_set[dev].load(std::memory_order_acquire)) {
+    std::lock_guard<std::mutex> lock(g_static_fill);
+    if (!g_static_set[dev].load(std::memory_order_relaxed)) {
+      void* p = nullptr;
+      if (int e = hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)),
+                             "w4a8_gemm_noalloc: hipGetSymbolAddress(scratch)"))
+        return e;
+      if (!p || !aligned(p, 256))
+        return fail(W4A8_EHIP, "w4a8_gemm_noalloc: static scratch has no usable address");
+      const int words = (int)(kStaticCounterBytes / sizeof(int));
+      hipLaunchKernelGGL(clear_words, dim3(16), dim3(256), 0, st,
+                         (int*)((uint8_t*)p + kStaticPartialBytes), words);
+      if (int e = hip_status(hipGetLastError(), "w4a8_gemm_noalloc: counter clear")) return e;
+      g_static_addr[dev] = (uint8_t*)p;
+      g_static_set[dev].store(true, std::memory_order_release);
+    }
+  }
+  uint8_t* base = g_static_addr[dev];
+  *out = Scratch{(float*)base, kStaticPartialBytes, (int*)(base + kStaticPartialBytes),
+                 kStaticCounterBytes, "the allocation-free entry point's static scratch"};
+  return W4A8_OK;
+}
+
+}  // namespace
+
 W4A8_API int w4a8_workspace_bytes(int max_m, int max_n, size_t* partial_bytes,
                                   size_t* counter_bytes) {
   if (max_m < 1 || max_n < 1 || max_n > (1 << 22))
@@ -616,4 +665,14 @@ W4A8_API int w4a8_mfma_tile(const void* a, const void* b, const void* sa, const 
   return hip_status(launch_mfma_tiles((const int*)a, (const int*)b, (const int*)sa,
                                       (const int*)sb, d, count, (hipStream_t)stream),
                     "w4a8_mfma_tile");
+}
+
+W4A8_API int w4a8_gemm_noalloc(const void* a, const float* a_scale, const void* wq,
+                               const void* sq, void* c, int M, int N, int K, int kernel,
+                               int variant, int split_k, void* stream) {
+  if (int e = check_gemm_shape("w4a8_gemm_noalloc", M, N, K)) return e;
+  Scratch sc;
+  if (int e = static_scratch(current_device(), (hipStream_t)stream, &sc)) return e;
+  return gemm_run(a, a_scale, wq, sq, c, M, N, K, kernel, variant, split_k, sc,
+                  "w4a8_gemm_noalloc", stream);
 }
