@@ -574,12 +574,15 @@ def bench_sweep(n_layers):
 
 
 CALIBRATION_BYTES = 256 * 2 ** 20
+# decode-band GEMMs in the counter runs: gate_up and down at M = 32 and 64
+BAND_PROFILE = [(32, 17408, 5120), (64, 17408, 5120), (32, 5120, 8704), (64, 5120, 8704)]
 
 
 def profile_workload():
     """The launches the committed rocprofv3 summaries are taken on: the verify GEMM (the bench's
     graph replay: one second of warmup replays, then 64 timed launches over 16 weight copies,
-    plus 64 event-bracketed single launches), each prefill GEMM (4 launches), each fused
+    plus 64 event-bracketed single launches), each prefill GEMM (4 launches), gate_up and down
+    at M = 32 and 64 (8 launches over 4 weight copies each), each fused
     producer and the quantizer at M = 4096 (4 launches over 2 input copies each) and a plain
     256 MiB device copy
     (torch's copy kernel), whose FETCH_SIZE / WRITE_SIZE readings calibrate the counters: a copy
@@ -596,6 +599,12 @@ def profile_workload():
         g = Gemm(M, N, K, 2, seed=7)
         for i in range(4):
             g.launch(i % 2, st.cuda_stream)
+        torch.cuda.synchronize()
+        del g
+    for M, N, K in BAND_PROFILE:                   # the decode band above 16 tokens
+        g = Gemm(M, N, K, 4, seed=9)
+        for i in range(8):
+            g.launch(i % 4, st.cuda_stream)
         torch.cuda.synchronize()
         del g
     for kind, N in PRODUCERS:                      # the fused producers at M = 4096

@@ -12,7 +12,8 @@
 // q = fma(r, y, q0) with the sign of x: three operations instead of a full division. Over every
 // finite row amax and every bf16 x with |x| <= amax (both signs, 1.07e9 pairs) the result equals
 // the IEEE quotient except for quotients below 2^-12, where both round to the same signed zero in
-// e4m3 (tests/test_markstein_cpu.py runs that exhaustive check).
+// e4m3 (tests/fp_identities.c, run by tests/test_fp_identities_cpu.py, makes that exhaustive
+// check).
 #pragma once
 #include "w4a8_internal.h"
 
