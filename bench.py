@@ -183,17 +183,29 @@ def bench_verify(args):
                 plan=g.plan)
 
 
+# the fused producer that makes each prefill GEMM's input in the model
+PREFILL_PRODUCER = {"gate_up": "add_rms", "down": "silu"}
+
+
 def bench_prefill():
     """The M=4096 prefill GEMMs alone, and as config 4 states them: the per-token quantizer on
-    bf16 activations fused ahead of the GEMM (quant + GEMM per step, timed as one unit)."""
+    bf16 activations fused ahead of the GEMM (quant + GEMM per step, timed as one unit); then
+    the model's own chain, the fused producer + GEMM, with q row-major and fragment-tiled."""
     import torch
+    from vllm_sly_radiance_amd import _native
     res = []
     for name, M, N, K in PREFILL:
         copies = max(2, -(-512 * 2 ** 20 // (N * K * 17 // 32)))
         flop = 2.0 * M * N * K
         row = dict(name=name, M=M, N=N, K=K)
-        for key, cls in (("gemm", Gemm), ("quant_gemm", QuantGemm)):
-            g = cls(M, N, K, copies, seed=7)
+        legs = (("gemm", lambda: Gemm(M, N, K, copies, seed=7)),
+                ("quant_gemm", lambda: QuantGemm(M, N, K, copies, seed=7)),
+                ("producer_gemm", lambda: ProducerGemm(PREFILL_PRODUCER[name], M, N, K, copies,
+                                                       7, _native.Q_ROWS)),
+                ("producer_gemm_tiled", lambda: ProducerGemm(PREFILL_PRODUCER[name], M, N, K,
+                                                             copies, 7, _native.Q_TILED)))
+        for key, make in legs:
+            g = make()
             sec, _, _, _ = graph_timed(g, 8 * copies, 2 * copies)
             us = sec / (8 * copies) * 1e6
             tf = flop / (us * 1e-6) / 1e12
@@ -201,10 +213,11 @@ def bench_prefill():
                 row.update(us=round(us, 2), tflops=round(tf, 1),
                            frac=round(tf / MFMA_PEAK_TFLOPS, 4), plan=g.plan)
             else:
-                row.update(quant_gemm_us=round(us, 2), quant_gemm_tflops=round(tf, 1),
-                           quant_gemm_frac=round(tf / MFMA_PEAK_TFLOPS, 4))
+                row.update({f"{key}_us": round(us, 2), f"{key}_tflops": round(tf, 1),
+                            f"{key}_frac": round(tf / MFMA_PEAK_TFLOPS, 4)})
             del g
             torch.cuda.empty_cache()
+        row["producer"] = PREFILL_PRODUCER[name]
         res.append(row)
     return res
 
@@ -232,10 +245,11 @@ class Producer:
     """Device operands of one fused producer (radiance::add_rms_quant / silu_mul_quant /
     gdn_norm_quant) with `copies` distinct input sets."""
 
-    def __init__(self, kind, M, N, copies, seed):
+    def __init__(self, kind, M, N, copies, seed, q_layout=0):
         import torch
         from vllm_sly_radiance_amd import _native, synthetic
         self.kind, self.M, self.N, self._native = kind, M, N, _native
+        self.q_layout = q_layout
 
         def dev(bits):
             return torch.from_numpy(bits.view(np.int16)).cuda().view(torch.bfloat16)
@@ -245,7 +259,8 @@ class Producer:
             if kind in ("add_rms", "gdn") else None
         nw = 128 if kind == "gdn" else N
         self.weight = dev(synthetic.activations(1, nw, seed + 200)[0])
-        self.q = torch.empty((M, N), dtype=torch.uint8, device="cuda")
+        qbytes = _native.tiled_bytes(M, N) if q_layout == _native.Q_TILED else M * N
+        self.q = torch.empty((qbytes,), dtype=torch.uint8, device="cuda")
         self.s = torch.empty((M,), dtype=torch.float32, device="cuda")
         self.r = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
         torch.cuda.synchronize()
@@ -263,14 +278,32 @@ class Producer:
         if self.kind == "add_rms":
             n.add_rms_quant(self.w[i].data_ptr(), self.w2[i].data_ptr(), self.weight.data_ptr(),
                             self.q.data_ptr(), self.s.data_ptr(), self.r.data_ptr(), self.M,
-                            self.N, 1e-6, stream)
+                            self.N, 1e-6, stream, self.q_layout)
         elif self.kind == "silu":
             n.silu_mul_quant(self.w[i].data_ptr(), self.q.data_ptr(), self.s.data_ptr(), self.M,
-                             self.N, stream)
+                             self.N, stream, self.q_layout)
         else:
             n.gdn_norm_quant(self.w[i].data_ptr(), self.w2[i].data_ptr(), self.N,
                              self.weight.data_ptr(), self.q.data_ptr(), self.s.data_ptr(), self.M,
-                             self.N, 1e-6, stream)
+                             self.N, 1e-6, stream, self.q_layout)
+
+
+class ProducerGemm(Gemm):
+    """The linear as the model runs it at prefill: the fused producer that makes its input
+    (add_rms_quant in front of gate_up, silu_mul_quant in front of down) writes (q, scale) and the
+    GEMM reads them, one producer input set per weight copy. q_layout 1 writes q fragment-tiled
+    and runs w4a8_gemm_at on it."""
+
+    def __init__(self, kind, M, N, K, copies, seed, q_layout):
+        super().__init__(M, N, K, copies, seed)
+        self.prod = Producer(kind, M, K, copies, seed + 50, q_layout)
+
+    def launch(self, i, stream):
+        p = self.prod
+        p.launch(i, stream)
+        gemm = self._native.gemm_at if p.q_layout else self._native.gemm
+        gemm(p.q.data_ptr(), p.s.data_ptr(), self.w[i].data_ptr(), self.ws[i].data_ptr(),
+             self.out.data_ptr(), self.M, self.N, self.K, stream)
 
 
 class Quant:
@@ -581,7 +614,8 @@ BAND_PROFILE = [(32, 17408, 5120), (64, 17408, 5120), (32, 5120, 8704), (64, 512
 def profile_workload():
     """The launches the committed rocprofv3 summaries are taken on: the verify GEMM (the bench's
     graph replay: one second of warmup replays, then 64 timed launches over 16 weight copies,
-    plus 64 event-bracketed single launches), each prefill GEMM (4 launches), gate_up and down
+    plus 64 event-bracketed single launches), each prefill GEMM (4 launches, then 4 more on
+    fragment-tiled q behind its fused producer), gate_up and down
     at M = 32 and 64 (8 launches over 4 weight copies each), each fused
     producer and the quantizer at M = 4096 (4 launches over 2 input copies each) and a plain
     256 MiB device copy
@@ -597,6 +631,13 @@ def profile_workload():
     del g
     for _, M, N, K in PREFILL:
         g = Gemm(M, N, K, 2, seed=7)
+        for i in range(4):
+            g.launch(i % 2, st.cuda_stream)
+        torch.cuda.synchronize()
+        del g
+    from vllm_sly_radiance_amd import _native
+    for name, M, N, K in PREFILL:                  # the same GEMMs on fragment-tiled q
+        g = ProducerGemm(PREFILL_PRODUCER[name], M, N, K, 2, 7, _native.Q_TILED)
         for i in range(4):
             g.launch(i % 2, st.cuda_stream)
         torch.cuda.synchronize()

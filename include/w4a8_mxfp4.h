@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define W4A8_ABI_VERSION 1
+#define W4A8_ABI_VERSION 2
 
 enum {
   W4A8_OK = 0,
@@ -40,8 +40,20 @@ enum {
   W4A8_KERNEL_SKINNY = 1,  /* split-K skinny kernel, any M <= 64 */
   W4A8_KERNEL_TILE = 2,    /* LDS-pipelined macro tiles (prefill) */
   W4A8_KERNEL_STREAM = 3,  /* whole k-range of every wave in flight at once, M <= 16 */
-  W4A8_KERNEL_RING = 4     /* per-wave pipeline of k-tile stages, M <= 64 */
+  W4A8_KERNEL_RING = 4,    /* per-wave pipeline of k-tile stages, M <= 64 */
+  W4A8_KERNEL_TILE_AT = 5  /* the macro tiles on fragment-tiled activations (same variants) */
 };
+
+/* Layouts of the producers' e4m3 output q (the q_layout argument).
+ * W4A8_Q_ROWS: row-major [M, K].
+ * W4A8_Q_TILED: fragment-tiled, the scaled MFMA's activation operand order. Tokens go in blocks
+ *   of 16 (the last block padded; w4a8_tiled_bytes gives the size), each block 16 x K bytes;
+ *   K % 128 == 0. In block b, k-tile t (128 k), half h (0, 1), lane l (0..63), the 16 bytes at
+ *   byte ((b * K / 128 + t) * 2 + h) * 1024 + 16 * l are token 16 b + l % 16, k-bytes
+ *   128 t + 16 (4 h + l / 16) .. + 15. Padding tokens are never written and never reach an output.
+ * The reference's WMMA-fragment-tiled layout (sly/mxfp4/tile_layout.py:1-32) is the RDNA4 form of
+ * the same idea; this one is MI355X's operand order and is not byte-compatible with it. */
+enum { W4A8_Q_ROWS = 0, W4A8_Q_TILED = 1 };
 
 /* ABI version of the loaded library (W4A8_ABI_VERSION). */
 int w4a8_abi_version(void);
@@ -97,9 +109,22 @@ int w4a8_gemm(const void* a, const float* a_scale, const void* wq, const void* s
  * w4a8_gemm_planned with the returned triple always makes one launch. */
 int w4a8_plan(int M, int N, int K, int* kernel, int* variant, int* split_k);
 
+/* The GEMM on fragment-tiled activations (W4A8_Q_TILED, as the producers write them; K % 128 == 0):
+ * the macro-tile kernel with the plan w4a8_gemm would take for a macro tile at this (M, N) (the
+ * decode-band tiles at M <= 64). Same bits as w4a8_gemm on the row-major activations through the
+ * same tile variant. Replaces launch_at (sly/mxfp4/radiance_mxfp4_fp8.hip:2236-2368). */
+int w4a8_gemm_at(const void* a_tiled, const float* a_scale, const void* wq, const void* sq, void* c,
+                 int M, int N, int K, void* stream);
+
+/* Bytes of a fragment-tiled q of M tokens of K (whole 16-token blocks); K % 128 == 0. The
+ * reference's producers allocate the same padded storage (sly/mxfp4/radiance_fused_norm.py:
+ * 116-128). */
+int w4a8_tiled_bytes(int M, int K, size_t* bytes);
+
 /* w4a8_gemm with an explicit plan, for sweeps and tests (the reference forces cells through the
  * RADIANCE_MXFP4_DECODE_KS / _BK environment knobs, sly/mxfp4/radiance_mxfp4_fp8.hip:1464-1475).
- * split_k > 1 needs registered scratch of w4a8_scratch_bytes(); kernel 2 ignores split_k. */
+ * split_k > 1 needs registered scratch of w4a8_scratch_bytes(); kernels 2 and 5 ignore split_k;
+ * kernel 5 reads fragment-tiled activations. */
 int w4a8_gemm_planned(const void* a, const float* a_scale, const void* wq, const void* sq, void* c,
                       int M, int N, int K, int kernel, int variant, int split_k, void* stream);
 
@@ -146,7 +171,9 @@ int w4a8_linear(const void* x, long ldx, void* q, float* scale, const void* wq, 
 
 /* (4) Fused fp8 activation producers. Each writes the (q [M, K] e4m3fn, scale [M] fp32) pair of
  * entry point (1) for its bf16 result, so the pair can feed w4a8_gemm directly (the tuple branch of
- * apply_weights, radiance::mxfp4_linear_pq). One workgroup per row; every floating-point step is
+ * apply_weights, radiance::mxfp4_linear_pq); q_layout W4A8_Q_TILED writes q fragment-tiled for
+ * w4a8_gemm_at instead (the reference's `tiled` argument, sly/mxfp4/radiance_mxfp4_fp8.hip:2020,
+ * :2161, :2198), same bytes in another order. One workgroup per row; every floating-point step is
  * fixed (no fused multiply-add, fixed summation order, correctly rounded 1/sqrt, a self-contained
  * exp), so the results are reproducible bit for bit. Rows are contiguous and 16-byte aligned. */
 
@@ -156,7 +183,8 @@ int w4a8_linear(const void* x, long ldx, void* q, float* scale, const void* wq, 
  * (sly/mxfp4/radiance_mxfp4_fp8.hip:2196-2234; kernel :1834-1933), behind the reference's
  * radiance::add_rms_quant op (sly/mxfp4/radiance_fused_norm.py:132-160). */
 int w4a8_add_rms_quant(const void* y, const void* residual, const void* weight, void* q,
-                       float* scale, void* residual_out, int M, int K, float eps, void* stream);
+                       float* scale, void* residual_out, int M, int K, float eps, void* stream,
+                       int q_layout);
 
 /* SiLU-and-mul, then quant: gate_up bf16 [M, 2N] (gate = columns 0..N-1, up = N..2N-1) ->
  * x = bf16(bf16(silu(gate)) * up), q [M, N]; N % 8 == 0, N <= 18432. Replaces
@@ -165,7 +193,8 @@ int w4a8_add_rms_quant(const void* y, const void* residual, const void* weight, 
  * N > 16384 with scratch registered by w4a8_set_scratch (M * ceil(N / 512) * 4 bytes of
  * partials), rows are split over several workgroups in two launches; the results are the same
  * bits either way. */
-int w4a8_silu_mul_quant(const void* gate_up, void* q, float* scale, int M, int N, void* stream);
+int w4a8_silu_mul_quant(const void* gate_up, void* q, float* scale, int M, int N, void* stream,
+                        int q_layout);
 
 /* The bf16 stage of w4a8_silu_mul_quant without the quantization: out bf16 [M, N] =
  * bf16(bf16(silu(gate)) * up), the same bits the fused op quantizes; gate_up and out 16-byte
@@ -181,7 +210,7 @@ int w4a8_silu_mul(const void* gate_up, void* out, int M, int N, void* stream);
  * launch_gdn_norm_quant (sly/mxfp4/radiance_mxfp4_fp8.hip:2159-2195; kernel :2068-2156), behind
  * radiance::gdn_norm_quant (sly/mxfp4/radiance_fused_norm.py:189-220). */
 int w4a8_gdn_norm_quant(const void* x, const void* z, long z_stride, const void* weight, void* q,
-                        float* scale, int M, int N, float eps, void* stream);
+                        float* scale, int M, int N, float eps, void* stream, int q_layout);
 
 /* Diagnostic: register-resident throughput probe of the scaled MFMA (fp4 A x fp8 B) the GEMMs
  * issue; shape 0 = 16x16x128, 1 = 32x32x64. Launches `blocks` workgroups of 4 waves that write

@@ -22,6 +22,9 @@ Pins (what checks each function against something other than itself; see tests/t
   gemm_ref_f32      gemm_exact_f64, an exact integer-domain brute force, on small shapes.
   repack/unrepack   round trip, one-hot bijectivity, and the MFMA fragment model
                     (oracle/mfma_model.py) reproducing gemm_ref_f32 from the repacked bytes.
+  tile_q/untile_q   round trip on ragged M; every byte against the fp8 operand lane map of the
+  tiled_offset      MFMA model (itself pinned to the layout measured on MI355X); the scalar offset
+                    against the array form at every element.
 """
 from __future__ import annotations
 
@@ -250,6 +253,41 @@ def repack(w: np.ndarray, ws: np.ndarray):
     # sp[n, kb] with kb = (g*4 + j)*4 + h  ->  sq[nt, g, h*16 + r, j]
     sq = sp.reshape(NT, 16, KG, 4, 4).transpose(0, 2, 4, 1, 3)
     return np.ascontiguousarray(wq).reshape(-1), np.ascontiguousarray(sq).reshape(-1)
+
+
+def tile_q(q: np.ndarray) -> np.ndarray:
+    """Row-major e4m3 codes q [M, K] (K % 128 == 0) -> the fragment-tiled bytes the producers
+    write with q_layout 1 and the tile GEMM reads (flat, ceil(M/16)*16*K; padding tokens zero).
+    Block b of 16 tokens, k-tile t, half h, lane l: 16 bytes = token 16b + l%16, k-bytes
+    128t + 16(4h + l//16) .. +15, i.e. the scaled MFMA's fp8 operand order (mfma_model.b_lane_map)
+    laid out lane after lane. The reference's tile() (sly/mxfp4/tile_layout.py:10-18) does the same
+    for gfx1201's 16x16x16 WMMA fragments."""
+    q = np.asarray(q, np.uint8)
+    M, K = q.shape
+    if K % 128:
+        raise ValueError(f"tile_q: K={K} is not a multiple of 128")
+    Mp = -(-M // 16) * 16
+    p = np.zeros((Mp, K), np.uint8)
+    p[:M] = q
+    # p[16b + r, 128t + 64h + 16c + e] -> [b, t, h, c * 16 + r, e]
+    t = p.reshape(Mp // 16, 16, K // 128, 2, 4, 16).transpose(0, 2, 3, 4, 1, 5)
+    return np.ascontiguousarray(t).reshape(-1)
+
+
+def untile_q(t: np.ndarray, M: int, K: int) -> np.ndarray:
+    """Inverse of tile_q: flat fragment-tiled bytes -> row-major q [M, K] (padding dropped).
+    Counterpart of the reference's untile() (sly/mxfp4/tile_layout.py:21-25)."""
+    Mp = -(-M // 16) * 16
+    r = np.asarray(t, np.uint8).reshape(-1)[:Mp * K].reshape(Mp // 16, K // 128, 2, 4, 16, 16)
+    return np.ascontiguousarray(r.transpose(0, 4, 1, 2, 3, 5)).reshape(Mp, K)[:M].copy()
+
+
+def tiled_offset(row: int, col: int, K: int) -> int:
+    """Byte offset of q[row, col] in the fragment-tiled layout: the scalar form of the producers'
+    store address (the reference's kernel_offset, sly/mxfp4/tile_layout.py:28-32, for its own
+    layout)."""
+    b, r, t, h, c, e = row >> 4, row & 15, col >> 7, (col >> 6) & 1, (col >> 4) & 3, col & 15
+    return ((b * (K >> 7) + t) * 2 + h) * 1024 + 16 * (r + 16 * c) + e
 
 
 def unrepack(wq: np.ndarray, sq: np.ndarray, N: int, K: int):

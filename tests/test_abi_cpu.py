@@ -165,31 +165,73 @@ def test_quant_and_repack_validate(lib):
 @pytest.mark.parametrize("K,msg", [(12, b"8-aligned"), (10248, b"<= 10240"), (0, b"8-aligned")])
 def test_add_rms_quant_validates_before_launch(lib, K, msg):
     p = 4096
-    assert lib.w4a8_add_rms_quant(p, p, p, p, p, p, 4, K, 1e-6, None) == 1
+    assert lib.w4a8_add_rms_quant(p, p, p, p, p, p, 4, K, 1e-6, None, 0) == 1
     assert msg in lib.w4a8_last_error()
 
 
 def test_producers_validate_before_launch(lib):
     p = 4096
-    assert lib.w4a8_add_rms_quant(None, None, None, None, None, None, 0, 8, 1e-6, None) == 0
-    assert lib.w4a8_add_rms_quant(None, p, p, p, p, p, 4, 8, 1e-6, None) == 1       # null y
-    assert lib.w4a8_add_rms_quant(p + 2, p, p, p, p, p, 4, 8, 1e-6, None) == 1      # misaligned
-    assert lib.w4a8_silu_mul_quant(p, p, p, 4, 12, None) == 1
+    assert lib.w4a8_add_rms_quant(None, None, None, None, None, None, 0, 8, 1e-6, None, 0) == 0
+    assert lib.w4a8_add_rms_quant(None, p, p, p, p, p, 4, 8, 1e-6, None, 0) == 1       # null y
+    assert lib.w4a8_add_rms_quant(p + 2, p, p, p, p, p, 4, 8, 1e-6, None, 0) == 1      # misaligned
+    assert lib.w4a8_silu_mul_quant(p, p, p, 4, 12, None, 0) == 1
     assert b"8-aligned" in lib.w4a8_last_error()
-    assert lib.w4a8_silu_mul_quant(p, p, p, 4, 18440, None) == 1
-    assert lib.w4a8_silu_mul_quant(p, p + 4, p, 4, 16, None) == 1                  # q misaligned
-    assert lib.w4a8_silu_mul_quant(None, None, None, 0, 16, None) == 0
+    assert lib.w4a8_silu_mul_quant(p, p, p, 4, 18440, None, 0) == 1
+    assert lib.w4a8_silu_mul_quant(p, p + 4, p, 4, 16, None, 0) == 1                  # q misaligned
+    assert lib.w4a8_silu_mul_quant(None, None, None, 0, 16, None, 0) == 0
     assert lib.w4a8_silu_mul(p, p, 4, 12, None) == 1
     assert b"w4a8_silu_mul: N must be 8-aligned" in lib.w4a8_last_error()
     assert lib.w4a8_silu_mul(p, p + 8, 4, 16, None) == 1                           # out misaligned
     assert lib.w4a8_silu_mul(p, None, 4, 16, None) == 1
     assert lib.w4a8_silu_mul(None, None, 0, 16, None) == 0
-    assert lib.w4a8_gdn_norm_quant(p, p, 256, p, p, p, 4, 200, 1e-6, None) == 1
+    assert lib.w4a8_gdn_norm_quant(p, p, 256, p, p, p, 4, 200, 1e-6, None, 0) == 1
     assert b"multiple of 128" in lib.w4a8_last_error()
-    assert lib.w4a8_gdn_norm_quant(p, p, 100, p, p, p, 4, 128, 1e-6, None) == 1     # stride < N
-    assert lib.w4a8_gdn_norm_quant(p, p, 132, p, p, p, 4, 128, 1e-6, None) == 1     # stride % 8
+    assert lib.w4a8_gdn_norm_quant(p, p, 100, p, p, p, 4, 128, 1e-6, None, 0) == 1     # stride < N
+    assert lib.w4a8_gdn_norm_quant(p, p, 132, p, p, p, 4, 128, 1e-6, None, 0) == 1     # stride % 8
     assert b"stride" in lib.w4a8_last_error()
-    assert lib.w4a8_gdn_norm_quant(p, p + 8, 256, p, p, p, 4, 128, 1e-6, None) == 1  # z misaligned
+    assert lib.w4a8_gdn_norm_quant(p, p + 8, 256, p, p, p, 4, 128, 1e-6, None, 0) == 1  # z misaligned
+
+
+def test_q_layout_is_validated(lib):
+    p = 4096
+    assert lib.w4a8_add_rms_quant(p, p, p, p, p, p, 4, 256, 1e-6, None, 2) == 1
+    assert b"unknown q layout 2" in lib.w4a8_last_error()
+    assert lib.w4a8_add_rms_quant(p, p, p, p, p, p, 4, 200, 1e-6, None, 1) == 1
+    assert b"multiple of 128" in lib.w4a8_last_error()
+    assert lib.w4a8_silu_mul_quant(p, p, p, 4, 8704 + 8, None, 1) == 1
+    assert b"fragment-tiled" in lib.w4a8_last_error()
+    assert lib.w4a8_gdn_norm_quant(p, p, 256, p, p, p, 4, 128, 1e-6, None, -1) == 1
+    assert b"unknown q layout" in lib.w4a8_last_error()
+    # M = 0 with a valid tiled layout is a no-op
+    assert lib.w4a8_silu_mul_quant(None, None, None, 0, 8704, None, 1) == 0
+
+
+def test_tiled_gemm_validates_before_launch(lib):
+    p = 4096
+    assert lib.w4a8_gemm_at(p, p, p, p, p, 64, 256, 5120 + 32, None) == 1
+    assert b"K % 128" in lib.w4a8_last_error()
+    assert lib.w4a8_gemm_at(None, p, p, p, p, 64, 256, 5120, None) == 1          # null a
+    assert lib.w4a8_gemm_at(None, None, None, None, None, 0, 256, 5120, None) == 0
+    # fragment-tiled activations go to the tile kernel only
+    assert lib.w4a8_gemm_planned(p, p, p, p, p, 8, 256, 512, _native.KERNEL_TILE_AT, 99, 1,
+                                 None) == 1
+    assert b"tile variant 99 out of range" in lib.w4a8_last_error()
+    assert lib.w4a8_variant_count(_native.KERNEL_TILE_AT) == \
+        lib.w4a8_variant_count(_native.KERNEL_TILE)
+
+
+@pytest.mark.parametrize("M,K,want", [(0, 128, 0), (1, 128, 2048), (16, 5120, 16 * 5120),
+                                      (17, 8704, 32 * 8704), (4096, 5120, 4096 * 5120)])
+def test_tiled_bytes(lib, M, K, want):
+    n = ctypes.c_size_t()
+    assert lib.w4a8_tiled_bytes(M, K, ctypes.byref(n)) == 0
+    assert n.value == want
+
+
+def test_tiled_bytes_refuses_ragged_k(lib):
+    n = ctypes.c_size_t()
+    assert lib.w4a8_tiled_bytes(4, 96, ctypes.byref(n)) == 1
+    assert lib.w4a8_tiled_bytes(4, 128, None) == 1
 
 
 def test_read_probe_validates_before_launch(lib):

@@ -13,8 +13,9 @@ import os
 import threading
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libw4a8_mxfp4.so")
-ABI_VERSION = 1
-KERNEL_AUTO, KERNEL_SKINNY, KERNEL_TILE, KERNEL_STREAM, KERNEL_RING = 0, 1, 2, 3, 4
+ABI_VERSION = 2
+KERNEL_AUTO, KERNEL_SKINNY, KERNEL_TILE, KERNEL_STREAM, KERNEL_RING, KERNEL_TILE_AT = range(6)
+Q_ROWS, Q_TILED = 0, 1          # layouts of a producer's q
 
 _c = ctypes
 _vp, _int, _long, _sz = _c.c_void_p, _c.c_int, _c.c_long, _c.c_size_t
@@ -30,6 +31,8 @@ SIGNATURES = {
     "w4a8_repack": (_int, [_vp, _vp, _vp, _vp, _int, _int, _vp]),
     "w4a8_set_scratch": (_int, [_vp, _sz, _vp, _sz]),
     "w4a8_gemm": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _int, _int, _vp]),
+    "w4a8_gemm_at": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _int, _int, _vp]),
+    "w4a8_tiled_bytes": (_int, [_int, _int, _psz]),
     "w4a8_plan": (_int, [_int, _int, _int, _pint, _pint, _pint]),
     "w4a8_gemm_planned": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _int, _int,
                                  _vp]),
@@ -40,10 +43,12 @@ SIGNATURES = {
     "w4a8_scratch_bytes": (_int, [_int, _int, _int, _psz, _psz]),
     "w4a8_workspace_bytes": (_int, [_int, _int, _psz, _psz]),
     "w4a8_linear": (_int, [_vp, _long, _vp, _vp, _vp, _vp, _vp, _int, _int, _int, _vp]),
-    "w4a8_add_rms_quant": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _int, _int, _c.c_float, _vp]),
-    "w4a8_silu_mul_quant": (_int, [_vp, _vp, _vp, _int, _int, _vp]),
+    "w4a8_add_rms_quant": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _int, _int, _c.c_float, _vp,
+                                  _int]),
+    "w4a8_silu_mul_quant": (_int, [_vp, _vp, _vp, _int, _int, _vp, _int]),
     "w4a8_silu_mul": (_int, [_vp, _vp, _int, _int, _vp]),
-    "w4a8_gdn_norm_quant": (_int, [_vp, _vp, _long, _vp, _vp, _vp, _int, _int, _c.c_float, _vp]),
+    "w4a8_gdn_norm_quant": (_int, [_vp, _vp, _long, _vp, _vp, _vp, _int, _int, _c.c_float, _vp,
+                                   _int]),
     "w4a8_mfma_probe": (_int, [_int, _vp, _int, _int, _c.POINTER(_c.c_double), _vp]),
     "w4a8_read_probe": (_int, [_vp, _long, _vp, _vp]),
     "w4a8_mfma_tile": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _vp]),
@@ -104,26 +109,39 @@ def gemm_noalloc(a_ptr, as_ptr, wq_ptr, sq_ptr, c_ptr, M, N, K, stream, kernel=K
                                   split_k, stream))
 
 
+def gemm_at(a_ptr, as_ptr, wq_ptr, sq_ptr, c_ptr, M, N, K, stream):
+    """The GEMM on fragment-tiled activations (a producer's q written with Q_TILED)."""
+    check(lib().w4a8_gemm_at(a_ptr, as_ptr, wq_ptr, sq_ptr, c_ptr, M, N, K, stream))
+
+
+def tiled_bytes(M: int, K: int) -> int:
+    n = _sz()
+    check(lib().w4a8_tiled_bytes(M, K, _c.byref(n)))
+    return n.value
+
+
 def linear(x_ptr, ldx, q_ptr, s_ptr, wq_ptr, sq_ptr, c_ptr, M, N, K, stream):
     check(lib().w4a8_linear(x_ptr, ldx, q_ptr, s_ptr, wq_ptr, sq_ptr, c_ptr, M, N, K, stream))
 
 
-def add_rms_quant(y_ptr, res_ptr, w_ptr, q_ptr, s_ptr, res_out_ptr, M, K, eps, stream):
+def add_rms_quant(y_ptr, res_ptr, w_ptr, q_ptr, s_ptr, res_out_ptr, M, K, eps, stream,
+                  q_layout=Q_ROWS):
     check(lib().w4a8_add_rms_quant(y_ptr, res_ptr, w_ptr, q_ptr, s_ptr, res_out_ptr, M, K, eps,
-                                   stream))
+                                   stream, q_layout))
 
 
-def silu_mul_quant(gu_ptr, q_ptr, s_ptr, M, N, stream):
-    check(lib().w4a8_silu_mul_quant(gu_ptr, q_ptr, s_ptr, M, N, stream))
+def silu_mul_quant(gu_ptr, q_ptr, s_ptr, M, N, stream, q_layout=Q_ROWS):
+    check(lib().w4a8_silu_mul_quant(gu_ptr, q_ptr, s_ptr, M, N, stream, q_layout))
 
 
 def silu_mul(gu_ptr, out_ptr, M, N, stream):
     check(lib().w4a8_silu_mul(gu_ptr, out_ptr, M, N, stream))
 
 
-def gdn_norm_quant(x_ptr, z_ptr, z_stride, w_ptr, q_ptr, s_ptr, M, N, eps, stream):
+def gdn_norm_quant(x_ptr, z_ptr, z_stride, w_ptr, q_ptr, s_ptr, M, N, eps, stream,
+                   q_layout=Q_ROWS):
     check(lib().w4a8_gdn_norm_quant(x_ptr, z_ptr, z_stride, w_ptr, q_ptr, s_ptr, M, N, eps,
-                                    stream))
+                                    stream, q_layout))
 
 
 def set_scratch(partial_ptr, partial_bytes, counter_ptr, counter_bytes):

@@ -186,6 +186,8 @@ int small_m_tile(int M, int N, int cus) {
 // workgroups, every weight load in flight at once), else the skinny family, whose workgroup count
 // should cover the 256 CUs several times over (for small N the K dimension is split across
 // workgroups too). 16 < M <= 64: the ring kernel or narrow macro tiles (below).
+int plan_tile(int M, int N, int dev);
+
 void plan_impl(int M, int N, int K, int dev, const Scratch& sc, int* kernel, int* variant,
                int* split_k) {
   if (M <= 16) {
@@ -232,13 +234,21 @@ void plan_impl(int M, int N, int K, int dev, const Scratch& sc, int* kernel, int
         return;
       }
     }
+  }
+  *kernel = W4A8_KERNEL_TILE;
+  *variant = plan_tile(M, N, dev);
+  *split_k = 1;
+}
+
+// The macro-tile variant for an M x N GEMM: the decode-band rule above for M <= 64, the prefill
+// rule below otherwise. Fragment-tiled activations always take this plan.
+int plan_tile(int M, int N, int dev) {
+  const int cus = device_info(dev).cus;
+  if (M <= 64) {
     const int wm = M <= 32 ? 1 : 2, bm = 32 * wm;
     int wn = 1;
-    while (wn < 4 && (long)ceil_div(M, bm) * ceil_div(N, 32 * wn) > d.cus) ++wn;
-    *kernel = W4A8_KERNEL_TILE;
-    *variant = find_tile(wm, wn, 4, wm == 2 && wn == 2 ? 5 : 0);   // 64 x 64: 5 stages
-    *split_k = 1;
-    return;
+    while (wn < 4 && (long)ceil_div(M, bm) * ceil_div(N, 32 * wn) > cus) ++wn;
+    return find_tile(wm, wn, 4, wm == 2 && wn == 2 ? 5 : 0);   // 64 x 64: 5 stages
   }
   // Prefill band (measured on MI355X, every tile variant on the four Qwen3.8-27B linear shapes at
   // M = 32 .. 2048): 8-wave 256 x 256 tiles for wide N (the automatic path splits N so the last
@@ -248,16 +258,13 @@ void plan_impl(int M, int N, int K, int dev, const Scratch& sc, int* kernel, int
   // one round at least half (N = 17408 at M = 512: 218 tiles, 43 against 58 us), and the small-M
   // rule below that. 128 x 128 tiles run 4 stages when they fit one round (N = 5120 at M = 512:
   // 24 against 26 us for o_proj, 32 against 35 us for down), 3 when they take several rounds.
-  *kernel = W4A8_KERNEL_TILE;
-  const int cus = device_info(dev).cus;
   const long t160 = (long)ceil_div(M, 256) * ceil_div(N, 160);
   const long t128 = (long)ceil_div(M, 128) * ceil_div(N, 128);
-  if (M >= 1024 && N % 160 == 0) *variant = find_tile(4, 5, 8);
-  else if (M >= 1024) *variant = find_tile(4, 8, 8);
-  else if (M > 256 && 2 * t160 >= cus && t160 <= cus) *variant = find_tile(4, 5, 8);
-  else if (M > 256) *variant = find_tile(4, 4, 4, t128 <= cus ? 4 : 3);
-  else *variant = small_m_tile(M, N, cus);
-  *split_k = 1;
+  if (M >= 1024 && N % 160 == 0) return find_tile(4, 5, 8);
+  if (M >= 1024) return find_tile(4, 8, 8);
+  if (M > 256 && 2 * t160 >= cus && t160 <= cus) return find_tile(4, 5, 8);
+  if (M > 256) return find_tile(4, 4, 4, t128 <= cus ? 4 : 3);
+  return small_m_tile(M, N, cus);
 }
 
 // A tile variant whose workgroup fills a CU's LDS runs in rounds of one workgroup per CU. When the
@@ -285,12 +292,13 @@ int tile_split(int M, int N, int variant, int dev, int* tail_variant) {
 // Output columns [n0, n0 + n) of an M x N GEMM on one tile variant: the weights, scales and
 // output are offset by n0 / 16 n-tiles; the output keeps its row stride N.
 int tile_columns(const void* a, const float* as, const void* wq, const void* sq, void* c, int M,
-                 int N, int K, int n0, int n, int variant, const char* who, hipStream_t st) {
+                 int N, int K, int n0, int n, int variant, bool a_tiled, const char* who,
+                 hipStream_t st) {
   const size_t kt = padded_k(K) / kKTile, nt0 = n0 / kNTile;
   const GemmArgs g{(const uint8_t*)a, as, (const uint8_t*)wq + nt0 * kt * kGranuleBytes,
                    (const uint32_t*)sq + nt0 * (kt / kKGroup) * 64, (uint16_t*)c + n0, M, n, K,
                    N};
-  return hip_status(launch_tile(g, variant, st), who);
+  return hip_status(launch_tile(g, variant, a_tiled, st), who);
 }
 
 int gemm_dispatch(const void* a, const float* as, const void* wq, const void* sq, void* c, int M,
@@ -323,13 +331,13 @@ int gemm_dispatch(const void* a, const float* as, const void* wq, const void* sq
     }
     return hip_status(launch_skinny(g, variant, split_k, partial, counters, st), who);
   }
-  if (kernel == W4A8_KERNEL_TILE) {
+  if (kernel == W4A8_KERNEL_TILE || kernel == W4A8_KERNEL_TILE_AT) {
     if (variant < 0 || variant >= tile_variant_count())
       return fail(W4A8_EINVAL, "%s: tile variant %d out of range", who, variant);
     if (!tile_fits(M, N, K))
       return fail(W4A8_EINVAL, "%s: M=%d K=%d exceeds the tile kernel's 32-bit offsets", who,
                   M, K);
-    return hip_status(launch_tile(g, variant, st), who);
+    return hip_status(launch_tile(g, variant, kernel == W4A8_KERNEL_TILE_AT, st), who);
   }
   if (kernel == W4A8_KERNEL_RING) {
     if (variant < 0 || variant >= ring_variant_count())
@@ -353,24 +361,40 @@ int gemm_dispatch(const void* a, const float* as, const void* wq, const void* sq
 }
 
 // The GEMM on one scratch view: validation, the automatic plan (kernel == W4A8_KERNEL_AUTO) or
-// the forced one, and the launch(es) on `stream`.
+// the forced one, and the launch(es) on `stream`. a_tiled: the activations are fragment-tiled,
+// which the tile kernel alone reads (the automatic plan is then plan_tile's).
 int gemm_run(const void* a, const float* as, const void* wq, const void* sq, void* c, int M, int N,
-             int K, int kernel, int variant, int split_k, const Scratch& sc, const char* who,
-             void* stream) {
+             int K, int kernel, int variant, int split_k, bool a_tiled, const Scratch& sc,
+             const char* who, void* stream) {
   if (int e = check_gemm_shape(who, M, N, K)) return e;
+  a_tiled = a_tiled || kernel == W4A8_KERNEL_TILE_AT;
+  if (a_tiled && kernel != W4A8_KERNEL_AUTO && kernel != W4A8_KERNEL_TILE_AT)
+    return fail(W4A8_EINVAL, "%s: fragment-tiled activations are read by the tile kernel only "
+                "(kernel %d)", who, kernel);
+  if (a_tiled && K % kKTile)
+    return fail(W4A8_EINVAL, "%s: fragment-tiled activations need K %% %d == 0, got K=%d", who,
+                kKTile, K);
   if (M == 0) return W4A8_OK;
   if (int e = check_gemm_ptrs(who, a, as, wq, sq, c)) return e;
   if (kernel == W4A8_KERNEL_AUTO) {
     const int dev = current_device();
-    plan_impl(M, N, K, dev, sc, &kernel, &variant, &split_k);
+    if (a_tiled) {
+      kernel = W4A8_KERNEL_TILE_AT;
+      variant = plan_tile(M, N, dev);
+      split_k = 1;
+    } else {
+      plan_impl(M, N, K, dev, sc, &kernel, &variant, &split_k);
+    }
     int tail = -1;
-    const int n_main = kernel == W4A8_KERNEL_TILE && tile_fits(M, N, K)
+    const int n_main = (kernel == W4A8_KERNEL_TILE || kernel == W4A8_KERNEL_TILE_AT) &&
+                               tile_fits(M, N, K)
                            ? tile_split(M, N, variant, dev, &tail)
                            : 0;
     if (n_main > 0 && n_main < N && n_main % kNTile == 0) {
       const hipStream_t st = (hipStream_t)stream;
-      if (int e = tile_columns(a, as, wq, sq, c, M, N, K, 0, n_main, variant, who, st)) return e;
-      return tile_columns(a, as, wq, sq, c, M, N, K, n_main, N - n_main, tail, who, st);
+      if (int e = tile_columns(a, as, wq, sq, c, M, N, K, 0, n_main, variant, a_tiled, who, st))
+        return e;
+      return tile_columns(a, as, wq, sq, c, M, N, K, n_main, N - n_main, tail, a_tiled, who, st);
     }
   }
   return gemm_dispatch(a, as, wq, sq, c, M, N, K, kernel, variant, split_k, sc, who, stream);
@@ -443,7 +467,7 @@ W4A8_API int w4a8_plan(int M, int N, int K, int* kernel, int* variant, int* spli
 W4A8_API int w4a8_gemm_planned(const void* a, const float* a_scale, const void* wq,
                                const void* sq, void* c, int M, int N, int K, int kernel,
                                int variant, int split_k, void* stream) {
-  return gemm_run(a, a_scale, wq, sq, c, M, N, K, kernel, variant, split_k,
+  return gemm_run(a, a_scale, wq, sq, c, M, N, K, kernel, variant, split_k, false,
                   registered_scratch(current_device()), "w4a8_gemm", stream);
 }
 
@@ -452,9 +476,23 @@ W4A8_API int w4a8_gemm(const void* a, const float* a_scale, const void* wq, cons
   return w4a8_gemm_planned(a, a_scale, wq, sq, c, M, N, K, W4A8_KERNEL_AUTO, -1, 0, stream);
 }
 
+W4A8_API int w4a8_gemm_at(const void* a_tiled, const float* a_scale, const void* wq,
+                          const void* sq, void* c, int M, int N, int K, void* stream) {
+  return gemm_run(a_tiled, a_scale, wq, sq, c, M, N, K, W4A8_KERNEL_AUTO, -1, 0, true,
+                  registered_scratch(current_device()), "w4a8_gemm_at", stream);
+}
+
+W4A8_API int w4a8_tiled_bytes(int M, int K, size_t* bytes) {
+  if (M < 0 || K <= 0 || K % kKTile || !bytes)
+    return fail(W4A8_EINVAL, "w4a8_tiled_bytes: need M >= 0, K a positive multiple of %d and an "
+                "output (M=%d K=%d)", kKTile, M, K);
+  *bytes = (size_t)ceil_div(M, 16) * 16 * K;
+  return W4A8_OK;
+}
+
 W4A8_API int w4a8_variant_count(int kernel) {
   if (kernel == W4A8_KERNEL_SKINNY) return skinny_variant_count();
-  if (kernel == W4A8_KERNEL_TILE) return tile_variant_count();
+  if (kernel == W4A8_KERNEL_TILE || kernel == W4A8_KERNEL_TILE_AT) return tile_variant_count();
   if (kernel == W4A8_KERNEL_STREAM) return stream_variant_count();
   if (kernel == W4A8_KERNEL_RING) return ring_variant_count();
   fail(W4A8_EINVAL, "w4a8_variant_count: unknown kernel %d", kernel);
@@ -466,7 +504,8 @@ W4A8_API int w4a8_variant_info(int kernel, int variant, int* p0, int* p1, int* p
   if (kernel == W4A8_KERNEL_SKINNY && variant >= 0 && variant < skinny_variant_count()) {
     const SkinnyCfg c = skinny_variant(variant);
     v[0] = c.mt; v[1] = c.nt; v[2] = c.waves; v[3] = c.unroll;
-  } else if (kernel == W4A8_KERNEL_TILE && variant >= 0 && variant < tile_variant_count()) {
+  } else if ((kernel == W4A8_KERNEL_TILE || kernel == W4A8_KERNEL_TILE_AT) && variant >= 0 &&
+             variant < tile_variant_count()) {
     const TileCfg c = tile_variant(variant);
     v[0] = c.wm; v[1] = c.wn; v[2] = c.bm; v[3] = c.bn;
   } else if (kernel == W4A8_KERNEL_STREAM && variant >= 0 && variant < stream_variant_count()) {
@@ -568,12 +607,23 @@ W4A8_API int w4a8_linear(const void* x, long ldx, void* q, float* scale, const v
   return w4a8_gemm(q, scale, wq, sq, c, M, N, K, stream);
 }
 
+// q_layout: W4A8_Q_ROWS, or W4A8_Q_TILED when the row length is whole 128-byte k-tiles
+static int check_q_layout(const char* who, int q_layout, int K) {
+  if (q_layout != W4A8_Q_ROWS && q_layout != W4A8_Q_TILED)
+    return fail(W4A8_EINVAL, "%s: unknown q layout %d", who, q_layout);
+  if (q_layout == W4A8_Q_TILED && K % kKTile)
+    return fail(W4A8_EINVAL, "%s: the fragment-tiled layout needs a row length that is a "
+                "multiple of %d, got %d", who, kKTile, K);
+  return W4A8_OK;
+}
+
 W4A8_API int w4a8_add_rms_quant(const void* y, const void* residual, const void* weight, void* q,
                                 float* scale, void* residual_out, int M, int K, float eps,
-                                void* stream) {
+                                void* stream, int q_layout) {
   if (M < 0 || K <= 0 || K % 8 || K > 10240)
     return fail(W4A8_EINVAL, "w4a8_add_rms_quant: K must be 8-aligned and <= 10240 (M=%d K=%d)",
                 M, K);
+  if (int e = check_q_layout("w4a8_add_rms_quant", q_layout, K)) return e;
   if (M == 0) return W4A8_OK;
   if (!y || !residual || !weight || !q || !scale || !residual_out)
     return fail(W4A8_EINVAL, "w4a8_add_rms_quant: null pointer");
@@ -583,15 +633,16 @@ W4A8_API int w4a8_add_rms_quant(const void* y, const void* residual, const void*
                 "w4a8_add_rms_quant: y, residual, weight and residual_out need 16-byte alignment, "
                 "q 8-byte, scale 4-byte");
   return hip_status(launch_add_rms_quant(y, residual, weight, (uint8_t*)q, scale, residual_out, M,
-                                         K, eps, (hipStream_t)stream),
+                                         K, eps, q_layout == W4A8_Q_TILED, (hipStream_t)stream),
                     "w4a8_add_rms_quant");
 }
 
 W4A8_API int w4a8_silu_mul_quant(const void* gate_up, void* q, float* scale, int M, int N,
-                                 void* stream) {
+                                 void* stream, int q_layout) {
   if (M < 0 || N <= 0 || N % 8 || N > 18432)
     return fail(W4A8_EINVAL, "w4a8_silu_mul_quant: N must be 8-aligned and <= 18432 (M=%d N=%d)",
                 M, N);
+  if (int e = check_q_layout("w4a8_silu_mul_quant", q_layout, N)) return e;
   if (M == 0) return W4A8_OK;
   if (!gate_up || !q || !scale) return fail(W4A8_EINVAL, "w4a8_silu_mul_quant: null pointer");
   if (!aligned(gate_up, 16) || !aligned(q, 8) || !aligned(scale, 4))
@@ -601,7 +652,8 @@ W4A8_API int w4a8_silu_mul_quant(const void* gate_up, void* q, float* scale, int
   void* part = sc.partial;
   const size_t part_bytes = sc.partial_bytes;
   return hip_status(launch_silu_mul_quant(gate_up, (uint8_t*)q, scale, nullptr, M, N, part,
-                                          part_bytes, (hipStream_t)stream),
+                                          part_bytes, q_layout == W4A8_Q_TILED,
+                                          (hipStream_t)stream),
                     "w4a8_silu_mul_quant");
 }
 
@@ -613,15 +665,17 @@ W4A8_API int w4a8_silu_mul(const void* gate_up, void* out, int M, int N, void* s
   if (!aligned(gate_up, 16) || !aligned(out, 16))
     return fail(W4A8_EINVAL, "w4a8_silu_mul: gate_up and out need 16-byte alignment");
   return hip_status(launch_silu_mul_quant(gate_up, nullptr, nullptr, out, M, N, nullptr, 0,
-                                          (hipStream_t)stream),
+                                          false, (hipStream_t)stream),
                     "w4a8_silu_mul");
 }
 
 W4A8_API int w4a8_gdn_norm_quant(const void* x, const void* z, long z_stride, const void* weight,
-                                 void* q, float* scale, int M, int N, float eps, void* stream) {
+                                 void* q, float* scale, int M, int N, float eps, void* stream,
+                                 int q_layout) {
   if (M < 0 || N <= 0 || N % 128 || N > 10240)
     return fail(W4A8_EINVAL,
                 "w4a8_gdn_norm_quant: N must be a multiple of 128 and <= 10240 (M=%d N=%d)", M, N);
+  if (int e = check_q_layout("w4a8_gdn_norm_quant", q_layout, N)) return e;
   if (M == 0) return W4A8_OK;
   if (z_stride % 8 || (M > 1 && z_stride < N))
     return fail(W4A8_EINVAL, "w4a8_gdn_norm_quant: z row stride %ld must be 8-aligned and >= N",
@@ -634,7 +688,7 @@ W4A8_API int w4a8_gdn_norm_quant(const void* x, const void* z, long z_stride, co
                 "w4a8_gdn_norm_quant: x, z and weight need 16-byte alignment, q 8-byte, scale "
                 "4-byte");
   return hip_status(launch_gdn_norm_quant(x, z, z_stride, weight, (uint8_t*)q, scale, M, N, eps,
-                                          (hipStream_t)stream),
+                                          q_layout == W4A8_Q_TILED, (hipStream_t)stream),
                     "w4a8_gdn_norm_quant");
 }
 
@@ -673,6 +727,6 @@ W4A8_API int w4a8_gemm_noalloc(const void* a, const float* a_scale, const void* 
   if (int e = check_gemm_shape("w4a8_gemm_noalloc", M, N, K)) return e;
   Scratch sc;
   if (int e = static_scratch(current_device(), (hipStream_t)stream, &sc)) return e;
-  return gemm_run(a, a_scale, wq, sq, c, M, N, K, kernel, variant, split_k, sc,
+  return gemm_run(a, a_scale, wq, sq, c, M, N, K, kernel, variant, split_k, false, sc,
                   "w4a8_gemm_noalloc", stream);
 }

@@ -28,6 +28,11 @@
 //    and weight panels in its own L2.
 //  * Epilogue: a lane holds 4 consecutive columns of one token; scaled by the per-token fp32 scale,
 //    rounded to bf16 and stored 8 bytes at a time.
+//  * AT = true reads the activations in the fragment-tiled layout the producers can write (16-token
+//    blocks of 16 x K bytes; in block b, k-tile t, half h, lane l's 16 bytes at
+//    ((b KT + t) 2 + h) 1024 + 16 l are token 16 b + l % 16, k-bytes 128 t + 16 (4 h + l / 16)):
+//    each activation unit is then one contiguous KiB, copied to LDS as it is, and the fragment
+//    reads are lane-contiguous. Only the addresses differ, so both layouts give the same bits.
 #include "w4a8_internal.h"
 
 namespace w4a8 {
@@ -90,7 +95,7 @@ struct IntC {
   static constexpr int value = Q;
 };
 
-template <int WM, int WN, int NS, int NW>
+template <int WM, int WN, int NS, int NW, bool AT>
 __global__ __launch_bounds__(NW * 64) void gemm_tile(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
     const uint32_t* __restrict__ Sq, uint16_t* __restrict__ C, int M, int N, int K, int KTp,
@@ -119,8 +124,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;      // (NW / 2) x 2 waves
 
-  // buffer resources: activations (all M x K), this tile's weight granules and scale dwords
-  const auto a_src = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, M * K, kBufferWord3);
+  // buffer resources: activations (all M x K; tiled: whole 16-token blocks), this tile's weight
+  // granules and scale dwords
+  const int mblocks = ceil_div(M, 16);
+  const auto a_src =
+      __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, AT ? mblocks * 16 * K : M * K, kBufferWord3);
   const int ntiles_here = min(S::BN / 16, NTILES - nt_base);
   const auto w_src = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(Wq + (size_t)nt_base * KTp * kGranuleBytes), 0, ntiles_here * KTp * kGranuleBytes,
@@ -134,18 +142,29 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile(
   const int a_row = lane >> 3;                              // token within the 8-token unit
   const int a_chunk = (lane & 7) ^ (a_row >> 1);            // chunk for even units; odd: ^ 4
   // MFMA fragment of lane l: token l % 16, chunks l / 16 and 4 + l / 16 of the 16-token block
+  // (tiled: the block's two halves as they are)
   const int f_row = lane & 15;
-  const int f_lo = 1024 * (f_row >> 3) + 16 * (8 * (f_row & 7) + ((lane >> 4) ^ ((f_row >> 1) & 7)));
-  const int f_hi = f_lo ^ 64;                               // chunk + 4: slot bit 2 flips
+  const int f_lo =
+      AT ? 16 * lane
+         : 1024 * (f_row >> 3) + 16 * (8 * (f_row & 7) + ((lane >> 4) ^ ((f_row >> 1) & 7)));
+  const int f_hi = AT ? f_lo + 1024 : f_lo ^ 64;            // chunk + 4: slot bit 2 flips
 
   // Fill op o of slab kt into stage base: an activation unit (o < A_PER_WAVE) or a weight granule.
   auto fill_op = [&](int kt, uint8_t* base, int o) {
     const bool kin = kt < KTe;
     if (o < S::A_PER_WAVE) {
       const int unit = wave * S::A_PER_WAVE + o;
-      const int row = m0 + unit * 8 + a_row;
-      const int col = kt * kKTile + 16 * (a_chunk ^ ((unit & 1) << 2));
-      const int off = (kin & (col < K) & (row < M)) ? row * K + col : kOut;
+      int off;
+      if constexpr (AT) {
+        // unit = half (unit & 1) of the tile's 16-token block unit / 2; K is whole k-tiles
+        const int blk = (m0 >> 4) + (unit >> 1);
+        off = (kin & (blk < mblocks)) ? ((blk * KTe + kt) * 2 + (unit & 1)) * 1024 + lane * 16
+                                      : kOut;
+      } else {
+        const int row = m0 + unit * 8 + a_row;
+        const int col = kt * kKTile + 16 * (a_chunk ^ ((unit & 1) << 2));
+        off = (kin & (col < K) & (row < M)) ? row * K + col : kOut;
+      }
       __builtin_amdgcn_raw_ptr_buffer_load_lds(a_src, (lds_ptr_t)(base + unit * 1024), 16, off, 0,
                                                0, 0);
     } else if (o < S::A_PER_WAVE + S::W_PER_WAVE) {
@@ -435,12 +454,13 @@ int tile_variant_count() { return kTileCount; }
 TileCfg tile_variant(int v) { return kTile[v]; }
 
 bool tile_fits(int M, int N, int K) {
-  // 32-bit buffer offsets: the activations and one tile's weight stripe
-  return (long)M * K < (1L << 31) && (long)16 * padded_k(K) / 2 * 16 < (1L << 31) &&
-         (long)N < (1L << 24);
+  // 32-bit buffer offsets: the activations (tiled: whole 16-token blocks) and one tile's weight
+  // stripe
+  return (long)ceil_div(M, 16) * 16 * K < (1L << 31) &&
+         (long)16 * padded_k(K) / 2 * 16 < (1L << 31) && (long)N < (1L << 24);
 }
 
-hipError_t launch_tile(const GemmArgs& g, int variant, hipStream_t stream) {
+hipError_t launch_tile(const GemmArgs& g, int variant, bool a_tiled, hipStream_t stream) {
   const TileCfg c = kTile[variant];
   const int KTp = padded_k(g.K) / kKTile, KTe = ceil_div(g.K, kKTile), KG = KTp / kKGroup;
   const int NTILES = padded_n(g.N) / kNTile;
@@ -453,9 +473,14 @@ hipError_t launch_tile(const GemmArgs& g, int variant, hipStream_t stream) {
   int idx = 0;
 #define W4A8_TILE_LAUNCH(wm, wn, ns, nw)                                                       \
   if (idx++ == variant) {                                                                        \
-    hipLaunchKernelGGL((gemm_tile<wm, wn, ns, nw>), grid, block, 0, stream, g.a, g.a_scale, g.wq, \
-                       g.sq, g.c, g.M, g.N, g.K, KTp, KTe, KG, NTILES, grid_m, grid_n, g.ldc,     \
-                       vec_out);                                                                 \
+    if (a_tiled)                                                                                 \
+      hipLaunchKernelGGL((gemm_tile<wm, wn, ns, nw, true>), grid, block, 0, stream, g.a,         \
+                         g.a_scale, g.wq, g.sq, g.c, g.M, g.N, g.K, KTp, KTe, KG, NTILES, grid_m, \
+                         grid_n, g.ldc, vec_out);                                                \
+    else                                                                                         \
+      hipLaunchKernelGGL((gemm_tile<wm, wn, ns, nw, false>), grid, block, 0, stream, g.a,        \
+                         g.a_scale, g.wq, g.sq, g.c, g.M, g.N, g.K, KTp, KTe, KG, NTILES, grid_m, \
+                         grid_n, g.ldc, vec_out);                                                \
     return hipGetLastError();                                                                    \
   }
   W4A8_TILE_TABLE(W4A8_TILE_LAUNCH)

@@ -100,7 +100,7 @@ __device__ __forceinline__ void store_out4(uint16_t* C, int ldc, int m, int n, i
 
 // ---- host-side launchers (one per kernel family) ---------------------------------------------
 struct GemmArgs {
-  const uint8_t* a;      // e4m3 [M, K] row-major
+  const uint8_t* a;      // e4m3 [M, K] row-major (tile kernel: or fragment-tiled)
   const float* a_scale;  // [M]
   const uint8_t* wq;     // granules
   const uint32_t* sq;    // scale dwords
@@ -113,17 +113,20 @@ hipError_t launch_quant(const uint16_t* x, long ldx, uint8_t* q, float* s, int M
                         hipStream_t stream);
 hipError_t launch_repack(const uint8_t* w, const uint8_t* ws, uint8_t* wq, uint32_t* sq, int N,
                          int K, hipStream_t stream);
+// tiled: q is written fragment-tiled (K or N a multiple of 128) instead of row-major
 hipError_t launch_add_rms_quant(const void* y, const void* res, const void* w, uint8_t* q,
-                                float* scale, void* res_out, int M, int K, float eps,
+                                float* scale, void* res_out, int M, int K, float eps, bool tiled,
                                 hipStream_t stream);
 // silu_mul splits rows of small M over several workgroups when `part` (the registered scratch)
 // holds producer_split_bytes(M, N); otherwise one workgroup per row. Same bits either way. With
 // `out` set (bf16 [M, N]) it writes the bf16 stage instead of quantizing, one workgroup per row.
 size_t producer_split_bytes(int M, int N);
 hipError_t launch_silu_mul_quant(const void* gate_up, uint8_t* q, float* scale, void* out, int M,
-                                 int N, void* part, size_t part_bytes, hipStream_t stream);
+                                 int N, void* part, size_t part_bytes, bool tiled,
+                                 hipStream_t stream);
 hipError_t launch_gdn_norm_quant(const void* x, const void* z, long zs, const void* w, uint8_t* q,
-                                 float* scale, int M, int N, float eps, hipStream_t stream);
+                                 float* scale, int M, int N, float eps, bool tiled,
+                                 hipStream_t stream);
 
 // Skinny split-K family (M <= 64). variant indexes the instantiated (MT, NT, WAVES, U) table.
 struct SkinnyCfg { int mt, nt, waves, unroll; };
@@ -164,7 +167,8 @@ struct TileCfg { int wm, wn, bm, bn, nw, lds, ns; };
 int tile_variant_count();
 TileCfg tile_variant(int v);
 bool tile_fits(int M, int N, int K);
-hipError_t launch_tile(const GemmArgs& g, int variant, hipStream_t stream);
+// a_tiled: the activations are fragment-tiled (16-token blocks; K a multiple of 128)
+hipError_t launch_tile(const GemmArgs& g, int variant, bool a_tiled, hipStream_t stream);
 
 // Register-resident MFMA throughput probe (shape 0: 16x16x128, 1: 32x32x64).
 hipError_t launch_read_probe(const void* buf, int bytes, int* out, hipStream_t stream);

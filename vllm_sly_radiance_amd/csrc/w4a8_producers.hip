@@ -113,10 +113,20 @@ __device__ __forceinline__ uint32_t block_max_t(uint32_t v) {
   return m;
 }
 
+// Byte offset of 8-element group g of row `row` in q (nv groups per row): row-major, or the
+// fragment-tiled layout the tile GEMM reads (16-token blocks of 16 x K bytes; in block b, k-tile t,
+// half h, lane l's 16 bytes at ((b KT + t) 2 + h) 1024 + 16 l hold token 16 b + l % 16, k-bytes
+// 128 t + 16 (4 h + l / 16)). Group g is the low or high 8 bytes of 16-byte chunk g / 2.
+__device__ __forceinline__ size_t q_offset(int row, int g, int nv, bool tiled) {
+  if (!tiled) return ((size_t)row * nv + g) * 8;
+  const int t = g >> 4, h = (g >> 3) & 1, l = (row & 15) + 16 * ((g >> 1) & 3);
+  return (((size_t)(row >> 4) * (nv >> 4) + t) * 2 + h) * 1024 + 16 * l + 8 * (g & 1);
+}
+
 // The quantization tail: bf16 groups nb[] (group g = tid + i T) of this row -> scale[row], q row.
 template <int G, int T>
 __device__ __forceinline__ void quant_tail(const uint4 (&nb)[G], int nv, uint8_t* __restrict__ q,
-                                           float* __restrict__ scale, int row) {
+                                           float* __restrict__ scale, int row, bool tiled) {
   const int tid = threadIdx.x;
   uint32_t am = 0;
 #pragma unroll
@@ -125,11 +135,12 @@ __device__ __forceinline__ void quant_tail(const uint4 (&nb)[G], int nv, uint8_t
   const float sc = row_scale(block_max_t<T>(am));
   const float rcp = 1.0f / sc;
   if (tid == 0) scale[row] = sc;
-  uint2* qr = reinterpret_cast<uint2*>(q + (size_t)row * nv * 8);
 #pragma unroll
   for (int i = 0; i < G; ++i) {
     const int g = tid + i * T;
-    if (g < nv) qr[g] = quant8_any_scale(nb[i], sc, rcp);
+    if (g < nv)
+      *reinterpret_cast<uint2*>(q + q_offset(row, g, nv, tiled)) =
+          quant8_any_scale(nb[i], sc, rcp);
   }
 }
 
@@ -140,7 +151,7 @@ template <int G>
 __global__ __launch_bounds__(kThreads) void add_rms_quant(
     const uint4* __restrict__ y, const uint4* __restrict__ res, const uint4* __restrict__ w,
     uint8_t* __restrict__ q, float* __restrict__ scale, uint4* __restrict__ res_out, int K,
-    float eps) {
+    float eps, int tiled) {
   const int row = blockIdx.x, tid = threadIdx.x, nv = K >> 3;
   y += (size_t)row * nv;
   res += (size_t)row * nv;
@@ -175,7 +186,7 @@ __global__ __launch_bounds__(kThreads) void add_rms_quant(
       nb[i] = pack8<true>(n);
     }
   }
-  quant_tail<G, kThreads>(nb, nv, q, scale, row);
+  quant_tail<G, kThreads>(nb, nv, q, scale, row, tiled);
 }
 
 // SiLU-and-mul: gate_up [M, 2N] -> bf16(bf16(silu(gate)) * up). T threads per row: the only
@@ -196,7 +207,7 @@ template <int G, int T>
 __global__ __launch_bounds__(T) void silu_mul_quant(const uint4* __restrict__ gu,
                                                     uint8_t* __restrict__ q,
                                                     float* __restrict__ scale,
-                                                    uint4* __restrict__ out, int N) {
+                                                    uint4* __restrict__ out, int N, int tiled) {
   const int row = blockIdx.x, tid = threadIdx.x, nv = N >> 3;
   const uint4* gate = gu + (size_t)row * 2 * nv;
   const uint4* up = gate + nv;
@@ -214,7 +225,7 @@ __global__ __launch_bounds__(T) void silu_mul_quant(const uint4* __restrict__ gu
     }
     return;
   }
-  quant_tail<G, T>(nb, nv, q, scale, row);
+  quant_tail<G, T>(nb, nv, q, scale, row, tiled);
 }
 
 // One 8-element group of the per-head gated RMSNorm. All 16 lanes of a head call it together
@@ -247,7 +258,7 @@ template <int G, int T>
 __global__ __launch_bounds__(T) void gdn_norm_quant(
     const uint4* __restrict__ x, const uint16_t* __restrict__ z, long zs,
     const uint4* __restrict__ w, uint8_t* __restrict__ q, float* __restrict__ scale, int N,
-    float eps) {
+    float eps, int tiled) {
   const int row = blockIdx.x, tid = threadIdx.x, nv = N >> 3;
   x += (size_t)row * nv;
   const uint4* zr = reinterpret_cast<const uint4*>(z + (size_t)row * zs);
@@ -257,7 +268,7 @@ __global__ __launch_bounds__(T) void gdn_norm_quant(
     const int g = tid + i * T;
     nb[i] = gdn_group(x, zr, w, g, g < nv, eps);
   }
-  quant_tail<G, T>(nb, nv, q, scale, row);
+  quant_tail<G, T>(nb, nv, q, scale, row, tiled);
 }
 
 // ---- silu_mul at few rows: each row split over one-wave workgroups ------------------------------
@@ -275,7 +286,7 @@ __global__ __launch_bounds__(T) void gdn_norm_quant(
 template <bool kQuant>
 __device__ __forceinline__ void split_tail(const uint4 nb, bool in, uint8_t* __restrict__ q,
                                            float* __restrict__ scale, uint32_t* __restrict__ part,
-                                           int row, int chunk, int S, int nv) {
+                                           int row, int chunk, int S, int nv, bool tiled) {
   const int lane = threadIdx.x, g = chunk * 64 + lane;
   if constexpr (!kQuant) {
     const uint32_t am = wave_max(in ? abs_bits_max8(nb) : 0u);
@@ -283,8 +294,9 @@ __device__ __forceinline__ void split_tail(const uint4 nb, bool in, uint8_t* __r
   } else {
     const float sc = row_scale(wave_max(lane < S ? part[row * S + lane] : 0u));
     if (chunk == 0 && lane == 0) scale[row] = sc;
-    if (in) reinterpret_cast<uint2*>(q + (size_t)row * nv * 8)[g] =
-        quant8_any_scale(nb, sc, 1.0f / sc);
+    if (in)
+      *reinterpret_cast<uint2*>(q + q_offset(row, g, nv, tiled)) =
+          quant8_any_scale(nb, sc, 1.0f / sc);
   }
 }
 
@@ -293,12 +305,12 @@ __global__ __launch_bounds__(64) void silu_mul_quant_split(const uint4* __restri
                                                            uint8_t* __restrict__ q,
                                                            float* __restrict__ scale,
                                                            uint32_t* __restrict__ part, int N,
-                                                           int S) {
+                                                           int S, int tiled) {
   const int chunk = blockIdx.x, row = blockIdx.y, nv = N >> 3, g = chunk * 64 + threadIdx.x;
   const uint4* gate = gu + (size_t)row * 2 * nv;
   const bool in = g < nv;
   const uint4 nb = in ? silu_mul_group<true>(gate[g], gate[nv + g]) : make_uint4(0, 0, 0, 0);
-  split_tail<kQuant>(nb, in, q, scale, part, row, chunk, S, nv);
+  split_tail<kQuant>(nb, in, q, scale, part, row, chunk, S, nv, tiled);
 }
 
 }  // namespace
@@ -320,14 +332,15 @@ bool split_rows(int M, int N, const void* part, size_t part_bytes) {
 }
 
 hipError_t launch_add_rms_quant(const void* y, const void* res, const void* w, uint8_t* q,
-                                float* scale, void* res_out, int M, int K, float eps,
+                                float* scale, void* res_out, int M, int K, float eps, bool tiled,
                                 hipStream_t stream) {
   if (M == 0) return hipSuccess;
   const int G = ceil_div(K >> 3, kThreads);
 #define W4A8_ARQ(C)                                                                             \
   case C:                                                                                       \
     hipLaunchKernelGGL(add_rms_quant<C>, dim3(M), dim3(kThreads), 0, stream, (const uint4*)y,   \
-                       (const uint4*)res, (const uint4*)w, q, scale, (uint4*)res_out, K, eps);  \
+                       (const uint4*)res, (const uint4*)w, q, scale, (uint4*)res_out, K, eps,   \
+                       (int)tiled);                                                             \
     break;
   switch (G) {
     W4A8_ARQ(1) W4A8_ARQ(2) W4A8_ARQ(3) W4A8_ARQ(4) W4A8_ARQ(5)
@@ -341,14 +354,15 @@ hipError_t launch_add_rms_quant(const void* y, const void* res, const void* w, u
 constexpr int kWideRowsMax = 128;
 
 hipError_t launch_silu_mul_quant(const void* gate_up, uint8_t* q, float* scale, void* out, int M,
-                                 int N, void* part, size_t part_bytes, hipStream_t stream) {
+                                 int N, void* part, size_t part_bytes, bool tiled,
+                                 hipStream_t stream) {
   if (M == 0) return hipSuccess;
   if (!out && split_rows(M, N, part, part_bytes)) {
     const int S = ceil_div(N >> 3, 64);
     hipLaunchKernelGGL(silu_mul_quant_split<false>, dim3(S, M), dim3(64), 0, stream,
-                       (const uint4*)gate_up, q, scale, (uint32_t*)part, N, S);
+                       (const uint4*)gate_up, q, scale, (uint32_t*)part, N, S, (int)tiled);
     hipLaunchKernelGGL(silu_mul_quant_split<true>, dim3(S, M), dim3(64), 0, stream,
-                       (const uint4*)gate_up, q, scale, (uint32_t*)part, N, S);
+                       (const uint4*)gate_up, q, scale, (uint32_t*)part, N, S, (int)tiled);
     return hipGetLastError();
   }
   const bool wide = M <= kWideRowsMax;
@@ -357,7 +371,7 @@ hipError_t launch_silu_mul_quant(const void* gate_up, uint8_t* q, float* scale, 
 #define W4A8_SMQ(C, TT)                                                                         \
   case C:                                                                                       \
     hipLaunchKernelGGL((silu_mul_quant<C, TT>), dim3(M), dim3(TT), 0, stream,                   \
-                       (const uint4*)gate_up, q, scale, (uint4*)out, N);                        \
+                       (const uint4*)gate_up, q, scale, (uint4*)out, N, (int)tiled);            \
     break;
   if (wide) {
     switch (G) {
@@ -376,7 +390,8 @@ hipError_t launch_silu_mul_quant(const void* gate_up, uint8_t* q, float* scale, 
 }
 
 hipError_t launch_gdn_norm_quant(const void* x, const void* z, long zs, const void* w, uint8_t* q,
-                                 float* scale, int M, int N, float eps, hipStream_t stream) {
+                                 float* scale, int M, int N, float eps, bool tiled,
+                                 hipStream_t stream) {
   if (M == 0) return hipSuccess;
   const bool wide = M <= kWideRowsMax;
   const int T = wide ? 1024 : kThreads;
@@ -384,7 +399,7 @@ hipError_t launch_gdn_norm_quant(const void* x, const void* z, long zs, const vo
 #define W4A8_GNQ(C, TT)                                                                         \
   case C:                                                                                       \
     hipLaunchKernelGGL((gdn_norm_quant<C, TT>), dim3(M), dim3(TT), 0, stream, (const uint4*)x,  \
-                       (const uint16_t*)z, zs, (const uint4*)w, q, scale, N, eps);              \
+                       (const uint16_t*)z, zs, (const uint4*)w, q, scale, N, eps, (int)tiled);  \
     break;
   if (wide) {
     switch (G) {

@@ -24,12 +24,19 @@ what the host module must look like), and one function, site_ok, checks a site a
 The gates are thin names over it. Everything they read is a plain attribute, so a tracing compiler
 folds each gate to a constant per layer.
 
-Not carried over: the fragment-tiled q layout (the MI355X GEMM reads row-major activations through
-LDS at the same rate either way), the fp8 hi/lo activation split and the online Hadamard rotation
-(both belong to checkpoint variants outside this path).
+At M >= RADIANCE_MXFP4_A_TILED_MIN_M (radiance_mxfp4; default off) the add-RMSNorm and SiLU-mul
+producers write q fragment-tiled, in the order the tile GEMM reads (w4a8_gemm_at), and record it in
+radiance_mxfp4's TiledHandoff for mxfp4_linear_pq; the gated norm does too when
+RADIANCE_MXFP4_TILED_OPROJ=1. The codes and scales are the same bytes in either layout; the choice is
+made per call from eager ints inside the opaque op body.
+
+Not carried over: the fp8 hi/lo activation split and the online Hadamard rotation (both belong to
+checkpoint variants outside this path).
 
 Switches, read once at import: RADIANCE_FUSED_NORM_QUANT=1 arms the fusions (default off);
-RADIANCE_FUSED_NORM_QUANT_ADD_RMS / _SILU / _GDN (default 1 each) then pick them.
+RADIANCE_FUSED_NORM_QUANT_ADD_RMS / _SILU / _GDN (default 1 each) then pick them;
+RADIANCE_MXFP4_TILED_OPROJ=1 lets the gated norm write the tiled layout (default off, as in the
+reference, sly/mxfp4/radiance_fused_norm.py:40-42).
 """
 from __future__ import annotations
 
@@ -39,6 +46,7 @@ from dataclasses import dataclass, field
 import torch
 
 from . import _native
+from . import radiance_mxfp4 as _rmx
 
 _MASTER = "RADIANCE_FUSED_NORM_QUANT"
 
@@ -51,6 +59,7 @@ def _armed(fusion: str) -> bool:
 
 ENABLED = os.environ.get(_MASTER, "0") == "1"
 ADD_RMS, SILU, GDN = (_armed(f) for f in ("ADD_RMS", "SILU", "GDN"))
+TILED_OPROJ = os.environ.get("RADIANCE_MXFP4_TILED_OPROJ", "0") == "1"
 
 # Widths the producer kernels accept (the entry points refuse anything else): add-RMSNorm rows up
 # to 10240, SiLU-mul outputs up to 18432, gated-norm rows up to 10240 in 128-wide heads; all
@@ -83,9 +92,25 @@ def _row_runs(t: torch.Tensor, n: int):
     return t, stride
 
 
-def _qs(M: int, K: int, device):
-    return (torch.empty((M, K), device=device, dtype=torch.float8_e4m3fn),
-            torch.empty((M,), device=device, dtype=torch.float32))
+def _tiled(M: int, K: int) -> bool:
+    """Write this producer's q fragment-tiled: the consumer GEMM's M asks for it and the row is
+    whole 128-byte k-tiles."""
+    return _rmx.a_tiled_wanted(M) and K % 128 == 0
+
+
+def _qs(M: int, K: int, device, tiled: bool = False):
+    q = (_rmx.alloc_tiled_q(M, K, device) if tiled
+         else torch.empty((M, K), device=device, dtype=torch.float8_e4m3fn))
+    return q, torch.empty((M,), device=device, dtype=torch.float32)
+
+
+def _layout(q: torch.Tensor, M: int, K: int, tiled: bool) -> int:
+    """The q_layout argument; a tiled q is recorded for its consumers (queued before any of them
+    can run, since they take q from this op's return)."""
+    if not tiled:
+        return _native.Q_ROWS
+    _rmx.a_tiled_register(q, M, K)
+    return _native.Q_TILED
 
 
 # ---- custom ops -------------------------------------------------------------------------------
@@ -97,12 +122,14 @@ def add_rms_quant_op(y: torch.Tensor, residual: torch.Tensor, weight: torch.Tens
     (sly/mxfp4/radiance_fused_norm.py:132-152)."""
     _need_bf16("add_rms_quant", y=y, residual=residual, weight=weight)
     M, K = y.shape
-    q, s = _qs(M, K, y.device)
+    tiled = _tiled(M, K)
+    q, s = _qs(M, K, y.device, tiled)
     r = torch.empty((M, K), device=y.device, dtype=torch.bfloat16)
     if M:
         y, residual, weight = y.contiguous(), residual.contiguous(), weight.contiguous()
         _native.add_rms_quant(y.data_ptr(), residual.data_ptr(), weight.data_ptr(), q.data_ptr(),
-                              s.data_ptr(), r.data_ptr(), M, K, float(eps), _stream())
+                              s.data_ptr(), r.data_ptr(), M, K, float(eps), _stream(),
+                              _layout(q, M, K, tiled))
     return q, s, r
 
 
@@ -121,10 +148,12 @@ def silu_mul_quant_op(gate_up: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor
     _need_bf16("silu_mul_quant", gate_up=gate_up)
     M, N2 = gate_up.shape
     N = N2 // 2
-    q, s = _qs(M, N, gate_up.device)
+    tiled = _tiled(M, N)
+    q, s = _qs(M, N, gate_up.device, tiled)
     if M:
         gate_up = gate_up.contiguous()
-        _native.silu_mul_quant(gate_up.data_ptr(), q.data_ptr(), s.data_ptr(), M, N, _stream())
+        _native.silu_mul_quant(gate_up.data_ptr(), q.data_ptr(), s.data_ptr(), M, N, _stream(),
+                               _layout(q, M, N, tiled))
     return q, s
 
 
@@ -143,13 +172,14 @@ def gdn_norm_quant_op(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor,
     (sly/mxfp4/radiance_fused_norm.py:189-213)."""
     _need_bf16("gdn_norm_quant", x=x, z=z, weight=weight)
     M, N = x.shape
-    q, s = _qs(M, N, x.device)
+    tiled = TILED_OPROJ and _tiled(M, N)
+    q, s = _qs(M, N, x.device, tiled)
     if M:
         # every copy stays referenced until the launch is queued
         x, weight = x.contiguous(), weight.contiguous()
         z, zs = _row_runs(z, N)
         _native.gdn_norm_quant(x.data_ptr(), z.data_ptr(), zs, weight.data_ptr(), q.data_ptr(),
-                               s.data_ptr(), M, N, float(eps), _stream())
+                               s.data_ptr(), M, N, float(eps), _stream(), _layout(q, M, N, tiled))
     return q, s
 
 

@@ -21,6 +21,7 @@ from __future__ import annotations
 
 import os
 import sys
+from collections import OrderedDict
 
 import torch
 
@@ -33,7 +34,17 @@ SCRATCH_MAX_N = int(os.environ.get("RADIANCE_MXFP4_SCRATCH_MAX_N", "36864"))
 SCRATCH_MAX_M = 64
 ACTIVATION_QUANT_KEY = "kMxfp4Dynamic"
 
-STATS = {"fast": 0, "refused": 0, "calls": 0, "calls_pq": 0}
+# Fragment-tiled activations (sly/mxfp4/radiance_mxfp4.py:29-39): the producers of
+# radiance_fused_norm write q in the layout the tile GEMM reads as contiguous 1 KiB units
+# (w4a8_gemm_at) when M >= this; 0 = off. Below M = 65 the streaming and ring kernels, which read
+# row-major activations, are faster than any macro tile, so the threshold must lie above that band.
+A_TILED_MIN_M = int(os.environ.get("RADIANCE_MXFP4_A_TILED_MIN_M", "0"))
+DECODE_BAND_MAX_M = 64
+if A_TILED_MIN_M and A_TILED_MIN_M <= DECODE_BAND_MAX_M:
+    raise RuntimeError(f"RADIANCE_MXFP4_A_TILED_MIN_M must exceed {DECODE_BAND_MAX_M} (the decode "
+                       f"band reads row-major activations), got {A_TILED_MIN_M}")
+
+STATS = {"fast": 0, "refused": 0, "calls": 0, "calls_pq": 0, "calls_tiled": 0}
 _scratch = [None, None]          # [partials, counters]: torch-owned, alive for the process
 
 
@@ -76,6 +87,80 @@ def repack_weights(weight: torch.Tensor, weight_scale: torch.Tensor):
     assert wq.numel() == wq_bytes and sq.numel() == sq_bytes
     _native.repack(w.data_ptr(), ws.data_ptr(), wq.data_ptr(), sq.data_ptr(), N, K, _stream())
     return wq, sq
+
+
+# --------------------------------------------------------------------------------------------
+# Fragment-tiled handoff, producer -> consumer
+# --------------------------------------------------------------------------------------------
+def a_tiled_wanted(M: int) -> bool:
+    """Should a producer of M tokens write q fragment-tiled (sly/mxfp4/radiance_mxfp4.py:50-51)."""
+    return A_TILED_MIN_M > 0 and M >= A_TILED_MIN_M
+
+
+def alloc_tiled_q(M: int, K: int, device) -> torch.Tensor:
+    """An [M, K] e4m3 tensor over storage of whole 16-token blocks (w4a8_tiled_bytes) plus a
+    128-byte tail that nothing reads: the tail gives tiled storage a size no row-major [M', K]
+    tensor has, which TiledHandoff checks. Rows are a view, so real and fake shapes agree."""
+    mp = -(-M // 16) * 16
+    buf = torch.empty((mp * K + 128,), dtype=torch.float8_e4m3fn, device=device)
+    return buf[:mp * K].view(mp, K)[:M]
+
+
+class TiledHandoff:
+    """Which pre-quantized activations are fragment-tiled. A tensor's bytes do not say how they are
+    ordered, and the custom-op boundary carries tensors only, so the producer records the tensor
+    it wrote (data pointer -> M, K, storage bytes) and mxfp4_linear_pq looks its input up, as the
+    reference does through its data_ptr table (sly/mxfp4/radiance_mxfp4.py:54-80).
+
+    A record stays after a lookup (a gated-norm q feeds two linears), and goes when its address is
+    marked again, when a lookup finds another shape or storage size there, or when it is older than
+    the last `keep` marks. A lookup needs the same (M, K) and the tiled storage size (whole blocks
+    plus the 128-byte tail, which no row-major [M', K] allocation has), so a row-major tensor at a
+    recycled address reads as row-major unless it is a view into that same tiled storage; callers
+    that quantized row-major themselves pass allow_tiled=False and skip the lookup."""
+
+    def __init__(self, keep: int = 64):
+        self.keep = keep
+        self._rec: OrderedDict[int, tuple[int, int, int]] = OrderedDict()
+
+    @staticmethod
+    def _sig(q: torch.Tensor, M: int, K: int) -> tuple[int, int, int]:
+        return (M, K, q.untyped_storage().nbytes() - q.storage_offset() * q.element_size())
+
+    def mark(self, q: torch.Tensor, M: int, K: int) -> None:
+        ptr = q.data_ptr()
+        self._rec.pop(ptr, None)
+        self._rec[ptr] = self._sig(q, M, K)
+        while len(self._rec) > self.keep:
+            self._rec.popitem(last=False)
+
+    def claim(self, q: torch.Tensor, M: int, K: int) -> bool:
+        ptr = q.data_ptr()
+        rec = self._rec.get(ptr)
+        if rec is None:
+            return False
+        mp = -(-M // 16) * 16
+        if rec != self._sig(q, M, K) or rec[2] != mp * K + 128:
+            del self._rec[ptr]
+            return False
+        return True
+
+    def clear(self) -> None:
+        self._rec.clear()
+
+
+A_TILED = TiledHandoff()
+
+
+def a_tiled_register(q: torch.Tensor, M: int, K: int) -> None:
+    """Record q (written fragment-tiled by a producer) for its consumers
+    (sly/mxfp4/radiance_mxfp4.py:66-71)."""
+    A_TILED.mark(q, M, K)
+
+
+def a_tiled_take(q: torch.Tensor, M: int, K: int) -> bool:
+    """Is q a recorded fragment-tiled tensor of this shape (sly/mxfp4/radiance_mxfp4.py:74-81)."""
+    return A_TILED.claim(q, M, K)
 
 
 def layout_ref(N: int, K: int, device) -> torch.Tensor:
@@ -142,8 +227,9 @@ def mxfp4_linear_pq(x_fp8: torch.Tensor, x_scale: torch.Tensor, weight: torch.Te
                     weight_scale: torch.Tensor, weight_ref: torch.Tensor,
                     allow_tiled: bool = True) -> torch.Tensor:
     """Pre-quantized entry (sly/mxfp4/radiance_mxfp4.py:825-860): (e4m3 [M, K], fp32 [M]) -> bf16
-    [M, N]. Activations are row-major; allow_tiled is accepted for signature compatibility and
-    has no effect (no fragment-tiled producer feeds this path)."""
+    [M, N]. x_fp8 is row-major, or fragment-tiled when a producer recorded it so (TiledHandoff;
+    tiled M x K is an [M, K] view over padded storage, so the shape is M either way).
+    allow_tiled=False skips the lookup, for callers that quantized row-major themselves."""
     STATS["calls_pq"] += 1
     N, K = weight_ref.shape[0], weight_ref.shape[1]
     if x_fp8.dim() != 2 or x_fp8.shape[1] != K or not x_fp8.is_contiguous():
@@ -155,6 +241,12 @@ def mxfp4_linear_pq(x_fp8: torch.Tensor, x_scale: torch.Tensor, weight: torch.Te
     xs = x_scale.reshape(-1)
     if xs.numel() != M or xs.dtype != torch.float32 or not xs.is_contiguous():
         raise RuntimeError(f"[radiance.mxfp4] x_scale must be {M} contiguous fp32 values")
+    if allow_tiled and A_TILED_MIN_M and a_tiled_take(x_fp8, M, K):
+        STATS["calls_tiled"] += 1
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=x_fp8.device)
+        _native.gemm_at(x_fp8.data_ptr(), xs.data_ptr(), weight.data_ptr(),
+                        weight_scale.data_ptr(), out.data_ptr(), M, N, K, _stream())
+        return out
     return gemm(x_fp8, xs, weight, weight_scale, N, K)
 
 
