@@ -561,8 +561,9 @@ def bench_sweep(n_layers):
 
     # crossover: GEMM only (pre-quantized activations), up to 16 layers' weights rotating. The
     # decode family is the streaming kernel where it serves (M <= 16), else the pipelined ring
-    # kernel with the fragments covering M (its first variant that serves the shape); the tile
-    # family is the macro tile the plan takes just above the ring's band (M = 21 .. 64), or at M.
+    # kernel with the fragments covering M (its first variant that serves the shape; a forced
+    # plan, kept to show why the plan takes the tiles there); the tile family is the macro tile
+    # the plan takes at M, or at M = 17 below that.
     ring = _native.variants(_native.KERNEL_RING)
     cross = {}
     for name, N, K in LAYER_M1:
@@ -580,15 +581,13 @@ def bench_sweep(n_layers):
                                  torch.cuda.current_stream().cuda_stream, kernel, variant, split)
 
             k, v, sp = _native.plan(M, N, K)
-            tile_v = v if k == _native.KERNEL_TILE else _native.plan(min(max(M, 21), 64), N, K)[1]
+            tile_v = v if k == _native.KERNEL_TILE else _native.plan(max(M, 17), N, K)[1]
             row = dict(M=M, tile_us=round(_timed_graph(
                 lambda: run(_native.KERNEL_TILE, tile_v, 1), 5) * 1e3 / per, 2))
             if k != _native.KERNEL_STREAM and M <= 64:
                 mf = -(-M // 16)
                 k, sp = _native.KERNEL_RING, 1
                 v = next((i for i, c in enumerate(ring) if c[0] == mf), None)
-                if k == _native.KERNEL_RING and M <= 20 and _native.plan(M, N, K)[0] == k:
-                    v = _native.plan(M, N, K)[1]
             if k != _native.KERNEL_TILE and v is not None:
                 try:
                     row["decode_us"] = round(_timed_graph(lambda: run(k, v, sp), 5) * 1e3 / per,
@@ -603,7 +602,7 @@ def bench_sweep(n_layers):
     return dict(layers=n_layers, weight_gb=round(weight_bytes * n_layers / 1e9, 3),
                 repack_ms_per_layer_median=round(float(np.median(repack_ms)), 4),
                 repack_ms_total=round(float(np.sum(repack_ms)), 2), forward=forward,
-                crossover=cross, plan_stream_max_M=16, plan_ring_max_M=20)
+                crossover=cross, plan_stream_max_M=16)
 
 
 CALIBRATION_BYTES = 256 * 2 ** 20

@@ -38,9 +38,9 @@ enum {
 enum {
   W4A8_KERNEL_AUTO = 0,
   W4A8_KERNEL_SKINNY = 1,  /* split-K skinny kernel, any M <= 64 */
-  W4A8_KERNEL_TILE = 2,    /* LDS-pipelined macro tiles (prefill) */
+  W4A8_KERNEL_TILE = 2,    /* LDS-pipelined macro tiles (M > 16) */
   W4A8_KERNEL_STREAM = 3,  /* whole k-range of every wave in flight at once, M <= 16 */
-  W4A8_KERNEL_RING = 4,    /* per-wave pipeline of k-tile stages, M <= 64 */
+  W4A8_KERNEL_RING = 4,    /* per-wave pipeline of k-tile stages, M <= 64 (forced plans only) */
   W4A8_KERNEL_TILE_AT = 5  /* the macro tiles on fragment-tiled activations (same variants) */
 };
 
@@ -152,6 +152,11 @@ int w4a8_gemm_noalloc(const void* a, const float* a_scale, const void* wq, const
  *         shape's n-tiles per workgroup fit NT and every wave owns a k-tile. */
 int w4a8_variant_count(int kernel);
 int w4a8_variant_info(int kernel, int variant, int* p0, int* p1, int* p2, int* p3);
+
+/* Diagnostic: the macro-tile variant's workgroup tile (bm tokens x bn columns), LDS pipeline
+ * depth, waves per workgroup and static LDS bytes. No counterpart in the reference, whose tile
+ * shapes are compile-time constants of its kernels. */
+int w4a8_tile_config(int variant, int* bm, int* bn, int* stages, int* waves, int* lds_bytes);
 
 /* Scratch a (skinny variant, split_k) plan needs for N columns: partial bytes and counter bytes. */
 int w4a8_scratch_bytes(int variant, int N, int split_k, size_t* partial_bytes,

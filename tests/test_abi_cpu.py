@@ -107,14 +107,14 @@ def test_split_k_without_scratch_is_refused(lib):
 def test_plan_bands(lib):
     k, v, s = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     # M <= 16: the streaming family when a wave's run and the LDS staging fit, else skinny; above
-    # M = 16 the macro-tile family, except the ring kernel up to M = 20 on N up to 10240.
+    # M = 16 the macro-tile family (the ring kernel only when forced).
     # N=17408 K=8704 would need 43-granule runs, past the largest stream variant; K=640 has fewer
     # k-tiles per n-tile than the smallest run.
     for M, N, K, kernel in [(1, 17408, 5120, 3), (8, 17408, 5120, 3), (16, 17408, 5120, 3),
                             (8, 5120, 8704, 3), (8, 17408, 8704, 1), (8, 33, 640, 1),
                             (17, 17408, 5120, 2), (64, 17408, 5120, 2), (65, 17408, 5120, 2),
-                            (17, 5120, 6144, 4), (20, 5120, 8704, 4), (21, 5120, 8704, 2),
-                            (20, 10240, 5120, 4), (17, 1024, 6144, 4), (20, 10256, 5120, 2),
+                            (17, 5120, 6144, 2), (20, 5120, 8704, 2), (21, 5120, 8704, 2),
+                            (20, 10240, 5120, 2), (17, 1024, 6144, 2), (20, 10256, 5120, 2),
                             (4096, 17408, 5120, 2)]:
         assert lib.w4a8_plan(M, N, K, ctypes.byref(k), ctypes.byref(v), ctypes.byref(s)) == 0
         assert (M, N, K, k.value) == (M, N, K, kernel) and v.value >= 0 and s.value >= 1
@@ -122,10 +122,12 @@ def test_plan_bands(lib):
 
 
 @pytest.mark.parametrize("M,N,K,tile", [
-    # decode band above 20 tokens: 32 (M <= 32) or 64 tokens tall, as narrow as keeps the
-    # workgroups within one per CU (256 CUs)
-    (24, 5120, 8704, (32, 32)), (32, 10240, 5120, (32, 64)), (32, 17408, 5120, (32, 96)),
-    (33, 5120, 6144, (64, 32)), (64, 17408, 5120, (64, 96)), (64, 5120, 8704, (64, 32)),
+    # decode band above 16 tokens: 32 tokens tall and as narrow as keeps the workgroups within
+    # one per CU (256 CUs); above 32 tokens 32 x 64 over both halves when that fits, else 64 x 64,
+    # 64 x 96, 64 x 128
+    (17, 5120, 6144, (32, 32)), (24, 5120, 8704, (32, 32)), (32, 10240, 5120, (32, 64)),
+    (32, 17408, 5120, (32, 96)), (32, 65536, 5120, (32, 128)),
+    (33, 5120, 6144, (32, 64)), (64, 17408, 5120, (64, 96)), (64, 5120, 8704, (32, 64)),
     (64, 10240, 5120, (64, 64)), (64, 65536, 5120, (64, 128)),
     # M > 64: the first tile (32x64, 64x64, 32x128, 64x128, 128x128, 128x256) whose workgroup
     # count stays within 5/8 of 256 CUs
@@ -143,6 +145,16 @@ def test_plan_tile_shapes(lib, M, N, K, tile):
     assert lib.w4a8_plan(M, N, K, ctypes.byref(k), ctypes.byref(v), ctypes.byref(s)) == 0
     assert k.value == 2
     assert _native.variants(2)[v.value][2:] == tile
+
+
+@pytest.mark.parametrize("M,N,K,stages", [(17, 5120, 6144, 8), (32, 17408, 5120, 8),
+                                          (64, 5120, 8704, 8), (64, 10240, 5120, 5),
+                                          (64, 17408, 5120, 5), (4096, 17408, 5120, 3)])
+def test_plan_pipeline_depth(lib, M, N, K, stages):
+    """The decode band's narrow tiles run 8 stages deep (latency-bound); the prefill tiles 3."""
+    k, v, s = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    assert lib.w4a8_plan(M, N, K, ctypes.byref(k), ctypes.byref(v), ctypes.byref(s)) == 0
+    assert _native.tile_stages(v.value) == stages
 
 
 def test_variant_tables(lib):

@@ -40,6 +40,7 @@ SIGNATURES = {
                                  _vp]),
     "w4a8_variant_count": (_int, [_int]),
     "w4a8_variant_info": (_int, [_int, _int, _pint, _pint, _pint, _pint]),
+    "w4a8_tile_config": (_int, [_int, _pint, _pint, _pint, _pint, _pint]),
     "w4a8_scratch_bytes": (_int, [_int, _int, _int, _psz, _psz]),
     "w4a8_workspace_bytes": (_int, [_int, _int, _psz, _psz]),
     "w4a8_linear": (_int, [_vp, _long, _vp, _vp, _vp, _vp, _vp, _int, _int, _int, _vp]),
@@ -170,6 +171,17 @@ def variants(kernel: int):
         check(lib().w4a8_variant_info(kernel, v, *[_c.byref(x) for x in p]))
         out.append(tuple(x.value for x in p))
     return out
+
+
+def tile_config(variant: int) -> dict:
+    """A macro-tile variant's workgroup tile, pipeline depth, waves and LDS bytes."""
+    p = [_int() for _ in range(5)]
+    check(lib().w4a8_tile_config(variant, *[_c.byref(x) for x in p]))
+    return dict(zip(("bm", "bn", "stages", "waves", "lds"), (x.value for x in p)))
+
+
+def tile_stages(variant: int) -> int:
+    return tile_config(variant)["stages"]
 
 
 def scratch_bytes(variant: int, N: int, split_k: int):

@@ -141,14 +141,6 @@ bool scratch_fits(const Scratch& s, int variant, int N, int split_k) {
 
 Scratch registered_scratch(int dev) { return dev >= 0 ? g_scratch[dev] : Scratch{}; }
 
-int find_ring(int mf, int nt, int d, int waves) {
-  for (int v = 0; v < ring_variant_count(); ++v) {
-    const RingCfg c = ring_variant(v);
-    if (c.mf == mf && c.nt == nt && c.d == d && c.waves == waves) return v;
-  }
-  return -1;
-}
-
 // The stream variant that serves (M, N, K) with the fewest granules on its busiest wave, then the
 // fewest n-tile slots, then the fewest waves.
 int find_stream(int M, int N, int K, int dev) {
@@ -185,7 +177,9 @@ int small_m_tile(int M, int N, int cus) {
 // Decode / verify band: M <= 16 takes the streaming family when a variant fits (whole-K
 // workgroups, every weight load in flight at once), else the skinny family, whose workgroup count
 // should cover the 256 CUs several times over (for small N the K dimension is split across
-// workgroups too). 16 < M <= 64: the ring kernel or narrow macro tiles (below).
+// workgroups too). Above 16 tokens the macro tiles (plan_tile). The ring kernel is not in the
+// automatic plan: the 8-stage narrow tiles beat it at every M from 17 to 64 on the four
+// Qwen3.8-27B shapes (it stays available to a forced plan).
 int plan_tile(int M, int N, int dev);
 
 void plan_impl(int M, int N, int K, int dev, const Scratch& sc, int* kernel, int* variant,
@@ -212,43 +206,37 @@ void plan_impl(int M, int N, int K, int dev, const Scratch& sc, int* kernel, int
     *split_k = ks;
     return;
   }
-  // Decode band above 16 tokens (measured on MI355X, every ring and every tile variant up to
-  // 64 x 128 on the four Qwen3.8-27B linear shapes at M = 17 .. 64):
-  //  * up to M = 20 on N up to 10240 the pipelined ring kernel with two fragments (3 n-tiles per
-  //    workgroup, 7 stages, 4 waves) is fastest (M = 17: qkv 10.95, o_proj 9.85, down 13.16 us
-  //    against 11.30, 10.23, 13.55 on the best tile);
-  //  * otherwise a macro tile BM = 32 (M <= 32) or 64 tokens tall and as narrow as keeps the
-  //    workgroups within one per CU: the weight stream then runs on as many CUs as the shape has
-  //    columns for (N = 5120: 32-column tiles, 160 workgroups; 10240: 64; 17408: 96 columns, 182
-  //    workgroups). gate_up M = 64: 16.3 us against 17.6 on 64 x 128; down M = 32: 13.6 against
-  //    17.0 on 32 x 64.
-  if (M <= 64) {
-    const int ntiles = padded_n(N) / kNTile;
-    const DeviceInfo d = device_info(dev);
-    if (M <= 20 && ntiles <= 640) {
-      const int v = find_ring(2, 3, 7, 4);
-      if (v >= 0 && ring_fits(v, M, N, K, d.cus, d.lds)) {
-        *kernel = W4A8_KERNEL_RING;
-        *variant = v;
-        *split_k = 1;
-        return;
-      }
-    }
-  }
   *kernel = W4A8_KERNEL_TILE;
   *variant = plan_tile(M, N, dev);
   *split_k = 1;
 }
 
-// The macro-tile variant for an M x N GEMM: the decode-band rule above for M <= 64, the prefill
-// rule below otherwise. Fragment-tiled activations always take this plan.
+// The macro-tile variant for an M x N GEMM: the decode-band rule for M <= 64, the prefill rule
+// below otherwise. Fragment-tiled activations always take this plan.
+//
+// Decode band (measured on MI355X, every tile variant up to 64 x 96 and every ring variant on the
+// four Qwen3.8-27B linear shapes at M = 17 .. 64): the tiles are latency-bound here, so they run 8
+// stages deep, and the fastest keep the workgroups within one per CU while staying 32 tokens tall:
+//  * M <= 32: 32 tokens tall and as narrow as fits one round (N = 5120: 32 x 32, 160 workgroups;
+//    10240: 32 x 64; 17408: 32 x 96): o_proj 8.6, down 10.8-11.0, qkv 8.9-10.0, gate_up 11.6-12.9
+//    us, against 10.0-15.2 us for the 4-5 stage tiles and 9.5-12.3 us for the best ring kernel;
+//  * M = 33 .. 64: 32 x 64 tiles over both 32-token halves when they fit one round (N = 5120: 160
+//    workgroups; o_proj 9.6-9.9, down 12.1-13.2 us against 11.4-15.4 on 64-token tiles), else
+//    64 x 64 (qkv, 160 workgroups, 11.8-13.2 us), else 64 x 96 in 8 waves (gate_up, 182
+//    workgroups, 14.7-15.9 us).
 int plan_tile(int M, int N, int dev) {
   const int cus = device_info(dev).cus;
-  if (M <= 64) {
-    const int wm = M <= 32 ? 1 : 2, bm = 32 * wm;
+  auto tiles = [&](int bm, int bn) { return (long)ceil_div(M, bm) * ceil_div(N, bn); };
+  if (M <= 32) {
     int wn = 1;
-    while (wn < 4 && (long)ceil_div(M, bm) * ceil_div(N, 32 * wn) > cus) ++wn;
-    return find_tile(wm, wn, 4, wm == 2 && wn == 2 ? 5 : 0);   // 64 x 64: 5 stages
+    while (wn < 4 && tiles(32, 32 * wn) > cus) ++wn;
+    return wn < 4 ? find_tile(1, wn, 4, 8) : find_tile(1, 4, 4, 4);
+  }
+  if (M <= 64) {
+    if (tiles(32, 64) <= cus) return find_tile(1, 2, 4, 8);
+    if (tiles(64, 64) <= cus) return find_tile(2, 2, 4, 5);
+    if (tiles(64, 96) <= cus) return find_tile(1, 3, 8, 5);
+    return find_tile(2, 4, 4, 4);
   }
   // Prefill band (measured on MI355X, every tile variant on the four Qwen3.8-27B linear shapes at
   // M = 32 .. 2048): 8-wave 256 x 256 tiles for wide N (the automatic path splits N so the last
@@ -497,6 +485,19 @@ W4A8_API int w4a8_variant_count(int kernel) {
   if (kernel == W4A8_KERNEL_RING) return ring_variant_count();
   fail(W4A8_EINVAL, "w4a8_variant_count: unknown kernel %d", kernel);
   return -1;
+}
+
+W4A8_API int w4a8_tile_config(int variant, int* bm, int* bn, int* stages, int* waves,
+                              int* lds_bytes) {
+  if (variant < 0 || variant >= tile_variant_count())
+    return fail(W4A8_EINVAL, "w4a8_tile_config: tile variant %d out of range", variant);
+  const TileCfg c = tile_variant(variant);
+  if (bm) *bm = c.bm;
+  if (bn) *bn = c.bn;
+  if (stages) *stages = c.ns;
+  if (waves) *waves = c.nw;
+  if (lds_bytes) *lds_bytes = c.lds;
+  return W4A8_OK;
 }
 
 W4A8_API int w4a8_variant_info(int kernel, int variant, int* p0, int* p1, int* p2, int* p3) {

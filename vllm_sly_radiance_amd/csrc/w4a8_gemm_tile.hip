@@ -21,8 +21,9 @@
 //    would wait for the younger slabs' fills too.
 //  * Buffer resources bound every fill: the K tail, rows past M and n-tiles past N fill zeros.
 //  * The e8m0 scale dwords change every 4 slabs (one dword per lane per k-group), so they live in
-//    a ring of 3 k-groups outside the stages; each slab's fills carry a quarter of the next
-//    k-group's rows. The MFMA applies the scales, so no dequantisation happens anywhere.
+//    a ring of k-groups outside the stages (ring_slots(NS) of them: enough that no refill lands
+//    on a k-group some slab still reads); every fourth slab's fills carry the rows of a k-group
+//    ahead. The MFMA applies the scales, so no dequantisation happens anywhere.
 //  * Workgroups are renumbered so each XCD (hardware places workgroup b on XCD b % 8) gets a
 //    contiguous run of tiles, walked in groups of 8 row blocks, which keeps an XCD's activation
 //    and weight panels in its own L2.
@@ -95,17 +96,36 @@ struct IntC {
   static constexpr int value = Q;
 };
 
+// k-groups in the scale ring of an NS-stage pipeline. The refill issued during slab kt (after its
+// barrier) is slab kt + NS - 1 (kt + NS on the deep-tile path) and, when that slab starts a
+// k-group, carries the rows of the k-group after it, g' = (kt + NS - 1) / 4 + 1. It lands on the
+// slot of k-group g' - R, which slabs up to 4 (g' - R) + 3 read (the deep-tile path reads a
+// group's rows once, at slab 4 g - 1). Those reads must precede slab kt, so 4 (g' - R) + 3 < kt,
+// which holds for NS < 4 R - 6: R = 3 up to 5 stages, 4 up to 9, 5 up to 13, 6 up to 17.
+constexpr int ring_slots(int ns) { return ns + 6 < 12 ? 3 : (ns + 6) / 4 + 1; }
+// every depth the kernel accepts: enough slots (NS < 4 R - 6), and no more than that needs
+// (tests/test_tile_scale_ring_cpu.py checks the condition against a model of the schedule)
+constexpr bool ring_slots_hold() {
+  for (int ns = 2; ns <= 16; ++ns) {
+    const int r = ring_slots(ns);
+    if (ns >= 4 * r - 6 || (r > 3 && ns < 4 * (r - 1) - 6)) return false;
+  }
+  return true;
+}
+static_assert(ring_slots_hold(), "scale ring: NS < 4 R - 6");
+
 template <int WM, int WN, int NS, int NW, bool AT>
 __global__ __launch_bounds__(NW * 64) void gemm_tile(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
     const uint32_t* __restrict__ Sq, uint16_t* __restrict__ C, int M, int N, int K, int KTp,
     int KTe, int KG, int NTILES, int grid_m, int grid_n, int ldc, int vec_out) {
   using S = TileShape<WM, WN, NW>;
-  static_assert(NS >= 2 && NS <= 5 && (NS - 1) * (S::OPS + 1) < 64, "pipeline depth");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * S::STAGE + 3 * S::S_SLOT + 1024 +
+  static_assert(NS >= 2 && NS <= 16 && (NS - 1) * (S::OPS + 1) < 64, "pipeline depth");
+  constexpr int RING = ring_slots(NS);
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * S::STAGE + RING * S::S_SLOT + 1024 +
                                                          S::TSCALE];
   uint8_t* const sring = lds + NS * S::STAGE;
-  uint8_t* const junk = sring + 3 * S::S_SLOT;     // where the surplus scale fills land
+  uint8_t* const junk = sring + RING * S::S_SLOT;  // where the surplus scale fills land
   uint8_t* const tscale = junk + 1024;             // the tile's per-token fp32 scales
 
   // ---- tile order: XCD-contiguous runs, grouped by 8 row blocks ----
@@ -174,7 +194,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile(
                                                off, 0, 0, kBufferNT);
     }
   };
-  // Scale unit of k-group grp into ring slot grp % 3: wave w < S_OPS moves rows 4w .. 4w+3 (lanes
+  // Scale unit of k-group grp into ring slot grp % RING: wave w < S_OPS moves rows 4w .. 4w+3 (lanes
   // 16 r .. 16 r + 15 read row 4w + r's 256 bytes, which land contiguously); the other waves move
   // zeros into the junk unit. Rows past S_ROWS or k-groups past KG read zero.
   auto fill_scales = [&](int grp) {
@@ -183,7 +203,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile(
     const int off = (mine & (r < S::S_ROWS) & (grp < KG)) ? (r * KG + grp) * 256 + (lane & 15) * 16
                                                           : kOut;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        s_src, (lds_ptr_t)(mine ? sring + (grp % 3) * S::S_SLOT + wave * 1024 : junk), 16, off, 0,
+        s_src, (lds_ptr_t)(mine ? sring + (grp % RING) * S::S_SLOT + wave * 1024 : junk), 16, off, 0,
         0, 0);
   };
   // Fill op o < S::fills(kt) of slab kt: the slab's units, then (kt % 4 == 0) k-group kt/4 + 1's
@@ -210,7 +230,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile(
   // activation fragment i (tokens 16 (wm WM + i) ..) of the same stage.
   auto read_w = [&](int st, int kt, v4i* wf, uint32_t* sc) {
     const uint8_t* base = lds + st * S::STAGE;
-    const uint8_t* srow = sring + ((kt >> 2) % 3) * S::S_SLOT + lane * 4;
+    const uint8_t* srow = sring + ((kt >> 2) % RING) * S::S_SLOT + lane * 4;
 #pragma unroll
     for (int j = 0; j < WN; ++j) {
       wf[j] = *reinterpret_cast<const v4i*>(base + S::W_OFF + (wn * WN + j) * 1024 + lane * 16);
@@ -302,7 +322,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile(
         bare_barrier();
         __builtin_amdgcn_sched_barrier(0);
         const uint8_t* nbase = lds + nst * S::STAGE;
-        const uint8_t* srow = sring + (((kt + 1) >> 2) % 3) * S::S_SLOT + lane * 4;
+        const uint8_t* srow = sring + (((kt + 1) >> 2) % RING) * S::S_SLOT + lane * 4;
 #pragma unroll
         for (int m = 0; m < R * WN; ++m) {
           const int r = m / WN, j = m % WN;
@@ -432,16 +452,17 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile(
 }
 
 // (WM, WN, NS, NW): NW waves of 16 WM x 16 WN in an (NW / 2) x 2 arrangement, NS-stage LDS
-// pipeline (LDS = NS * STAGE + 3 scale slots + token scales <= 160 KiB)
+// pipeline (LDS = NS * STAGE + ring_slots(NS) scale slots + token scales <= 160 KiB)
 #define W4A8_TILE_TABLE(X)                                                                        \
   X(2, 4, 4, 4) X(4, 4, 3, 4) X(4, 4, 4, 4) X(8, 4, 3, 4) X(4, 8, 3, 4) X(8, 8, 3, 4)            \
   X(8, 5, 3, 4) X(4, 8, 4, 4) X(4, 2, 4, 4) X(1, 2, 4, 4) X(2, 2, 4, 4) X(1, 4, 4, 4)            \
   X(2, 2, 5, 4) X(4, 8, 3, 8) X(4, 5, 3, 8) X(2, 3, 4, 4) X(2, 1, 5, 4) X(1, 3, 4, 4)            \
-  X(1, 1, 5, 4)
+  X(1, 1, 5, 4) X(1, 1, 8, 4) X(1, 2, 8, 4) X(1, 3, 8, 4) X(1, 3, 5, 8)
 
 #define W4A8_TILE_CFG(wm, wn, ns, nw)                                                             \
   TileCfg{wm, wn, TileShape<wm, wn, nw>::BM, TileShape<wm, wn, nw>::BN, nw,                        \
-          ns * TileShape<wm, wn, nw>::STAGE + 3 * TileShape<wm, wn, nw>::S_SLOT + 1024 +         \
+          ns * TileShape<wm, wn, nw>::STAGE + ring_slots(ns) * TileShape<wm, wn, nw>::S_SLOT +   \
+              1024 +                                                                             \
               TileShape<wm, wn, nw>::TSCALE,                                                     \
           ns},
 constexpr TileCfg kTile[] = {W4A8_TILE_TABLE(W4A8_TILE_CFG)};
