@@ -129,17 +129,17 @@ def test_plan_bands(lib):
     (32, 17408, 5120, (32, 96)), (32, 65536, 5120, (32, 128)),
     (33, 5120, 6144, (32, 64)), (64, 17408, 5120, (64, 96)), (64, 5120, 8704, (32, 64)),
     (64, 10240, 5120, (64, 64)), (64, 65536, 5120, (64, 128)),
-    # M > 64: the first tile (32x64, 64x64, 32x128, 64x128, 128x128, 128x256) whose workgroup
-    # count stays within 5/8 of 256 CUs
-    (128, 5120, 6144, (64, 64)),
-    (128, 17408, 5120, (128, 128)), (256, 10240, 5120, (128, 128)),
-    (256, 17408, 5120, (128, 256)),
-    # 256 < M < 1024: 256 x 160 when those tiles fill one round at least half, else 128 x 128
-    (512, 17408, 5120, (256, 160)), (512, 10240, 5120, (256, 160)), (512, 5120, 8704, (128, 128)),
-    (768, 17408, 5120, (128, 128)),
+    # 64 < M <= 1024: the candidate with the least predicted time (tiles per CU x area / rate);
+    # these are the measured-fastest variants at those points on MI355X
+    (65, 10240, 5120, (32, 128)), (128, 10240, 5120, (64, 128)), (384, 10240, 5120, (128, 128)),
+    (512, 10240, 5120, (256, 128)), (1024, 10240, 5120, (256, 160)),
+    (128, 5120, 6144, (32, 128)), (384, 5120, 8704, (64, 128)), (768, 5120, 8704, (128, 128)),
+    (1024, 5120, 8704, (256, 128)),
+    (96, 17408, 5120, (128, 128)), (192, 17408, 5120, (64, 128)), (256, 17408, 5120, (256, 128)),
+    (512, 17408, 5120, (256, 160)), (768, 17408, 5120, (256, 256)), (1024, 17408, 5120, (256, 160)),
     # prefill: 256 x 256 (8 waves) for wide N, 256 x 160 when N splits into 160-column tiles
-    (1024, 17408, 5120, (256, 256)), (4096, 17408, 5120, (256, 256)),
-    (1024, 10240, 5120, (256, 160)), (4096, 5120, 8704, (256, 160))])
+    (2048, 17408, 5120, (256, 256)), (4096, 17408, 5120, (256, 256)),
+    (2048, 10240, 5120, (256, 160)), (4096, 5120, 8704, (256, 160))])
 def test_plan_tile_shapes(lib, M, N, K, tile):
     k, v, s = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     assert lib.w4a8_plan(M, N, K, ctypes.byref(k), ctypes.byref(v), ctypes.byref(s)) == 0
@@ -147,14 +147,16 @@ def test_plan_tile_shapes(lib, M, N, K, tile):
     assert _native.variants(2)[v.value][2:] == tile
 
 
-@pytest.mark.parametrize("M,N,K,stages", [(17, 5120, 6144, 8), (32, 17408, 5120, 8),
-                                          (64, 5120, 8704, 8), (64, 10240, 5120, 5),
-                                          (64, 17408, 5120, 5), (4096, 17408, 5120, 3)])
-def test_plan_pipeline_depth(lib, M, N, K, stages):
-    """The decode band's narrow tiles run 8 stages deep (latency-bound); the prefill tiles 3."""
+@pytest.mark.parametrize("M,N,K,stages,waves", [
+    (17, 5120, 6144, 8, 4), (32, 17408, 5120, 8, 4), (64, 5120, 8704, 8, 4),
+    (64, 10240, 5120, 5, 4), (64, 17408, 5120, 5, 8), (96, 5120, 8704, 8, 4),
+    (96, 17408, 5120, 4, 8), (4096, 17408, 5120, 3, 8)])
+def test_plan_pipeline_depth_and_waves(lib, M, N, K, stages, waves):
+    """Narrow tiles run 8 stages deep (latency-bound at these M); large tiles 3-5, in 8 waves."""
     k, v, s = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     assert lib.w4a8_plan(M, N, K, ctypes.byref(k), ctypes.byref(v), ctypes.byref(s)) == 0
-    assert _native.tile_stages(v.value) == stages
+    c = _native.tile_config(v.value)
+    assert (c["stages"], c["waves"]) == (stages, waves)
 
 
 def test_variant_tables(lib):

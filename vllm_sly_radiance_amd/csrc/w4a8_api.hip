@@ -155,23 +155,43 @@ int find_stream(int M, int N, int K, int dev) {
   return best;
 }
 
-// The first macro tile, in the order 32x64, 64x64 (5 stages), 32x128, 64x128, 128x128, 128x256
-// (4 stages), whose workgroup count stays within 5/8 of the CUs: at M <= 256 the tile GEMM
-// streams the weights once per row block, and on MI355X fewer, longer workgroups beat one
-// workgroup per CU (measured on the Qwen3.8-27B linear shapes at M = 24..256; 64x64 beats 32x128
-// at the same count, e.g. down at M = 128: 17.5 against 19.5 us). 128x128 runs 4 stages when it
-// fits one round.
-int small_m_tile(int M, int N, int cus) {
-  static const int cand[][3] = {{1, 2, 0}, {2, 2, 5}, {1, 4, 0}, {2, 4, 0}, {4, 4, 0}, {4, 8, 4}};
-  for (const auto& c : cand) {
-    const int bm = 32 * c[0], bn = 32 * c[1];
-    const long tiles = (long)ceil_div(M, bm) * ceil_div(N, bn);
-    if (tiles <= (long)cus * 5 / 8) {
-      const int ns = c[2] ? c[2] : (c[0] == 4 && c[1] == 4 ? (tiles <= cus ? 4 : 3) : 0);
-      return find_tile(c[0], c[1], 4, ns);
-    }
+// Macro-tile candidates above the decode band, each with its measured throughput per CU
+// (TFLOP/s) with one workgroup on the CU (r1) and with two workgroups' worth of tiles per CU (r2,
+// running together or in two rounds). Measured on MI355X, every variant on the four Qwen3.8-27B
+// linear shapes at M = 65, 96, 128, 192, 256, 384, 512, 768 and 1024 (medians over the cases with
+// that many tiles per CU).
+struct TileRate {
+  int wm, wn, nw, ns;
+  float r1, r2;
+};
+constexpr TileRate kMidTiles[] = {
+    {2, 2, 4, 5, 3.77f, 4.59f},    // 64 x 64
+    {1, 4, 4, 8, 3.79f, 3.74f},    // 32 x 128, 8 stages
+    {2, 4, 4, 4, 5.60f, 6.24f},    // 64 x 128
+    {2, 4, 8, 4, 8.09f, 7.83f},    // 128 x 128, 8 waves
+    {2, 8, 8, 4, 9.77f, 9.51f},    // 128 x 256, 8 waves
+    {4, 4, 8, 3, 11.53f, 9.96f},   // 256 x 128, 8 waves
+    {4, 5, 8, 3, 12.28f, 10.09f},  // 256 x 160, 8 waves
+    {4, 8, 8, 3, 13.65f, 12.41f},  // 256 x 256, 8 waves
+};
+
+// 64 < M <= 1024: the candidate with the least predicted time, tiles per CU x tile area / rate
+// (r2 when the tiles come two per CU). Against the fastest variant measured at each of the 36
+// points above, the pick is 0.5 % slower on average and 5.7 % at worst (gate_up M = 384); the
+// first-fit rule it replaces was up to 33 % slower (qkv M = 384: 35.7 against 23.7 us).
+int mid_tile(int M, int N, int cus) {
+  double best = 0;
+  int pick = -1;
+  for (const TileRate& t : kMidTiles) {
+    const int v = find_tile(t.wm, t.wn, t.nw, t.ns);
+    if (v < 0) continue;
+    const TileCfg c = tile_variant(v);
+    const long per = ceil_div((long)ceil_div(M, c.bm) * ceil_div(N, c.bn), (long)cus);
+    const double area = (double)c.bm * c.bn;
+    const double cost = per == 2 ? 2 * area / t.r2 : per * area / t.r1;
+    if (pick < 0 || cost < best) best = cost, pick = v;
   }
-  return find_tile(4, 4);
+  return pick;
 }
 
 // Decode / verify band: M <= 16 takes the streaming family when a variant fits (whole-K
@@ -238,21 +258,13 @@ int plan_tile(int M, int N, int dev) {
     if (tiles(64, 96) <= cus) return find_tile(1, 3, 8, 5);
     return find_tile(2, 4, 4, 4);
   }
-  // Prefill band (measured on MI355X, every tile variant on the four Qwen3.8-27B linear shapes at
-  // M = 32 .. 2048): 8-wave 256 x 256 tiles for wide N (the automatic path splits N so the last
-  // round of these one-per-CU workgroups is not mostly idle, see tile_split), 256 x 160 where N
-  // divides into 160-column tiles (N = 5120: 512 tiles at M = 4096; N = 10240 at M = 1024: 256
-  // tiles, 44 against 56 us on 256 x 256), 128 x 128 below M = 1024 unless 256 x 160 tiles fill
-  // one round at least half (N = 17408 at M = 512: 218 tiles, 43 against 58 us), and the small-M
-  // rule below that. 128 x 128 tiles run 4 stages when they fit one round (N = 5120 at M = 512:
-  // 24 against 26 us for o_proj, 32 against 35 us for down), 3 when they take several rounds.
-  const long t160 = (long)ceil_div(M, 256) * ceil_div(N, 160);
-  const long t128 = (long)ceil_div(M, 128) * ceil_div(N, 128);
-  if (M >= 1024 && N % 160 == 0) return find_tile(4, 5, 8);
-  if (M >= 1024) return find_tile(4, 8, 8);
-  if (M > 256 && 2 * t160 >= cus && t160 <= cus) return find_tile(4, 5, 8);
-  if (M > 256) return find_tile(4, 4, 4, t128 <= cus ? 4 : 3);
-  return small_m_tile(M, N, cus);
+  if (M <= 1024) return mid_tile(M, N, cus);
+  // Prefill band (measured on MI355X on the four Qwen3.8-27B linear shapes at M = 2048 and
+  // 4096): 8-wave 256 x 256 tiles for wide N (the automatic path splits N so the last round of
+  // these one-per-CU workgroups is not mostly idle, see tile_split), 256 x 160 where N divides
+  // into 160-column tiles (N = 5120: 512 tiles at M = 4096).
+  if (N % 160 == 0) return find_tile(4, 5, 8);
+  return find_tile(4, 8, 8);
 }
 
 // A tile variant whose workgroup fills a CU's LDS runs in rounds of one workgroup per CU. When the

@@ -457,7 +457,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile(
   X(2, 4, 4, 4) X(4, 4, 3, 4) X(4, 4, 4, 4) X(8, 4, 3, 4) X(4, 8, 3, 4) X(8, 8, 3, 4)            \
   X(8, 5, 3, 4) X(4, 8, 4, 4) X(4, 2, 4, 4) X(1, 2, 4, 4) X(2, 2, 4, 4) X(1, 4, 4, 4)            \
   X(2, 2, 5, 4) X(4, 8, 3, 8) X(4, 5, 3, 8) X(2, 3, 4, 4) X(2, 1, 5, 4) X(1, 3, 4, 4)            \
-  X(1, 1, 5, 4) X(1, 1, 8, 4) X(1, 2, 8, 4) X(1, 3, 8, 4) X(1, 3, 5, 8)
+  X(1, 1, 5, 4) X(1, 1, 8, 4) X(1, 2, 8, 4) X(1, 3, 8, 4) X(1, 3, 5, 8) X(1, 4, 8, 4)            \
+  X(2, 4, 4, 8) X(2, 8, 4, 8) X(4, 4, 3, 8)
 
 #define W4A8_TILE_CFG(wm, wn, ns, nw)                                                             \
   TileCfg{wm, wn, TileShape<wm, wn, nw>::BM, TileShape<wm, wn, nw>::BN, nw,                        \
