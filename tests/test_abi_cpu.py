@@ -137,9 +137,13 @@ def test_plan_bands(lib):
     (1024, 5120, 8704, (256, 128)),
     (96, 17408, 5120, (128, 128)), (192, 17408, 5120, (64, 128)), (256, 17408, 5120, (256, 128)),
     (512, 17408, 5120, (256, 160)), (768, 17408, 5120, (256, 256)), (1024, 17408, 5120, (256, 160)),
-    # prefill: 256 x 256 (8 waves) for wide N, 256 x 160 when N splits into 160-column tiles
+    # M > 1024: the candidate (256 x 128, 256 x 160, 256 x 256, 128 x 256) whose rounds of
+    # one-per-CU workgroups, with a ragged last round split off where the path splits it, take
+    # the least predicted time
+    (1280, 10240, 5120, (256, 256)), (1280, 5120, 6144, (256, 128)),
+    (2048, 5120, 6144, (256, 160)), (2560, 5120, 8704, (256, 256)),
     (2048, 17408, 5120, (256, 256)), (4096, 17408, 5120, (256, 256)),
-    (2048, 10240, 5120, (256, 160)), (4096, 5120, 8704, (256, 160))])
+    (4096, 10240, 5120, (256, 160)), (4096, 5120, 8704, (256, 256))])
 def test_plan_tile_shapes(lib, M, N, K, tile):
     k, v, s = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     assert lib.w4a8_plan(M, N, K, ctypes.byref(k), ctypes.byref(v), ctypes.byref(s)) == 0

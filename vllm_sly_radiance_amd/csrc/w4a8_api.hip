@@ -194,6 +194,53 @@ int mid_tile(int M, int N, int cus) {
   return pick;
 }
 
+// Prefill candidates (M > 1024), each with its measured throughput per CU (TFLOP/s) over one or
+// more full rounds of one workgroup per CU, and that of the 128 x 128 tiles the automatic path
+// gives the columns of a ragged last round (tile_split). Measured on MI355X, every candidate on
+// the four Qwen3.8-27B linear shapes at M = 1280, 1536, 2048, 2560, 3072 and 4096 with warm
+// clocks (medians).
+constexpr TileRate kBigTiles[] = {
+    {4, 4, 8, 3, 9.75f, 0.f},   // 256 x 128
+    {4, 5, 8, 3, 10.36f, 0.f},  // 256 x 160
+    {4, 8, 8, 3, 12.11f, 0.f},  // 256 x 256
+    {2, 8, 8, 4, 9.14f, 0.f},   // 128 x 256
+};
+constexpr float kSplitTailRate = 8.3f;
+
+int tile_split(int M, int N, int variant, int dev, int* tail_variant);
+
+// Rounds of one-per-CU workgroups for an M x N GEMM on tile c, times area / rate.
+double round_cost(int M, int N, const TileCfg& c, float rate, int cus) {
+  const long per = ceil_div((long)ceil_div(M, c.bm) * ceil_div(N, c.bn), (long)cus);
+  return per * ((double)c.bm * c.bn) / rate;
+}
+
+// M > 1024: the candidate with the least predicted time as the automatic path would run it (its
+// ragged last round split off to 128 x 128 tiles where tile_split does so). Rounds are what
+// matter here: at M = 1280 .. 3072 the best tile is the one whose tiles fill whole rounds (qkv
+// M = 1280: 256 x 256 in one round of 200 tiles, 56.9 us, against 80 us for 256 x 160 in 320
+// tiles; o_proj and down M = 2560, 3072: 256 x 256 at 66.5-92.9 us against 90.6-122 us). Over the
+// 21 measured points whose pick runs as one launch or whose split was timed, the pick is 0.1 %
+// slower than the fastest candidate on average and 1.7 % at worst.
+int big_tile(int M, int N, int dev) {
+  const int cus = device_info(dev).cus;
+  double best = 0;
+  int pick = -1;
+  for (const TileRate& t : kBigTiles) {
+    const int v = find_tile(t.wm, t.wn, t.nw, t.ns);
+    if (v < 0) continue;
+    const TileCfg c = tile_variant(v);
+    double cost = round_cost(M, N, c, t.r1, cus);
+    int tail = -1;
+    const int n_main = tile_split(M, N, v, dev, &tail);
+    if (n_main > 0 && n_main < N && n_main % kNTile == 0)
+      cost = round_cost(M, n_main, c, t.r1, cus) +
+             round_cost(M, N - n_main, tile_variant(tail), kSplitTailRate, cus);
+    if (pick < 0 || cost < best) best = cost, pick = v;
+  }
+  return pick;
+}
+
 // Decode / verify band: M <= 16 takes the streaming family when a variant fits (whole-K
 // workgroups, every weight load in flight at once), else the skinny family, whose workgroup count
 // should cover the 256 CUs several times over (for small N the K dimension is split across
@@ -259,12 +306,7 @@ int plan_tile(int M, int N, int dev) {
     return find_tile(2, 4, 4, 4);
   }
   if (M <= 1024) return mid_tile(M, N, cus);
-  // Prefill band (measured on MI355X on the four Qwen3.8-27B linear shapes at M = 2048 and
-  // 4096): 8-wave 256 x 256 tiles for wide N (the automatic path splits N so the last round of
-  // these one-per-CU workgroups is not mostly idle, see tile_split), 256 x 160 where N divides
-  // into 160-column tiles (N = 5120: 512 tiles at M = 4096).
-  if (N % 160 == 0) return find_tile(4, 5, 8);
-  return find_tile(4, 8, 8);
+  return big_tile(M, N, dev);
 }
 
 // A tile variant whose workgroup fills a CU's LDS runs in rounds of one workgroup per CU. When the
