@@ -168,11 +168,20 @@ int w4a8_scratch_bytes(int variant, int N, int split_k, size_t* partial_bytes,
  * scratch from its own band limits (sly/mxfp4/radiance_mxfp4.py:1064-1070). max_n <= 2^22. */
 int w4a8_workspace_bytes(int max_m, int max_n, size_t* partial_bytes, size_t* counter_bytes);
 
-/* Quantize + GEMM in one call (two launches on the stream): the body of radiance::mxfp4_linear
- * (sly/mxfp4/radiance_mxfp4.py:644-816) minus the output allocation, which stays with the caller
- * (torch.empty at sly/mxfp4/radiance_mxfp4.py:737). q [M, K] and scale [M] are caller workspace. */
+/* Quantize + GEMM in one call: the body of radiance::mxfp4_linear (sly/mxfp4/radiance_mxfp4.py:
+ * 644-816) minus the output allocation, which stays with the caller (torch.empty at
+ * sly/mxfp4/radiance_mxfp4.py:737). Where w4a8_linear_fused says so (M = 1, and M = 2 where the
+ * streaming kernel's waves hold 4 k-tiles; x 16-byte aligned, ldx % 8 == 0) it is one launch
+ * that quantizes inside the GEMM;
+ * otherwise the quantizer and the GEMM, two launches on the stream. The output is the same bits
+ * either way. q [M, K] and scale [M] are caller workspace (not written by the one-launch form). */
 int w4a8_linear(const void* x, long ldx, void* q, float* scale, const void* wq, const void* sq,
                 void* c, int M, int N, int K, void* stream);
+
+/* 1 when w4a8_linear runs this shape (with a 16-byte aligned x) as one launch, 0 when as the
+ * quantizer and the GEMM, -1 for a bad shape. No counterpart in the reference, whose op always
+ * quantizes in a separate launch. */
+int w4a8_linear_fused(int M, int N, int K, long ldx);
 
 /* (4) Fused fp8 activation producers. Each writes the (q [M, K] e4m3fn, scale [M] fp32) pair of
  * entry point (1) for its bf16 result, so the pair can feed w4a8_gemm directly (the tuple branch of

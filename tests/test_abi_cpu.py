@@ -121,6 +121,21 @@ def test_plan_bands(lib):
     assert lib.w4a8_plan(8, 17408, 5000, ctypes.byref(k), ctypes.byref(v), ctypes.byref(s)) == 1
 
 
+def test_one_launch_linear_where_it_pays(lib):
+    """w4a8_linear runs as one launch (the quantizer inside the streaming GEMM) only for rows x
+    k-tiles per wave <= 8: M = 1 on every stream shape, M = 2 where a wave holds 4 k-tiles (not on
+    down's 8); never above the streaming band, never for rows that are not 16-byte chunks."""
+    f = lib.w4a8_linear_fused
+    for N, K in [(17408, 5120), (10240, 5120), (5120, 6144), (2048, 1024), (1040, 512)]:
+        assert [f(M, N, K, K) for M in range(1, 10)] == [1, 1] + [0] * 7, (N, K)
+    assert [f(M, 5120, 8704, 8704) for M in (1, 2, 3)] == [1, 0, 0]
+    assert f(1, 17408, 5120, 5120 + 72) == 1
+    assert f(1, 17408, 5120, 5120 + 4) == 0                # rows not whole 16-byte chunks
+    assert f(1, 17408, 5000, 5000) == -1                   # K not a multiple of 32: an error
+    assert f(1, 17408, 8704, 8704) == 0                    # no stream plan (skinny)
+    assert f(0, 17408, 5120, 5120) == 0 and f(1, 17408, 5120, 5119) == 0
+
+
 @pytest.mark.parametrize("M,N,K,tile", [
     # decode band above 16 tokens: 32 tokens tall and as narrow as keeps the workgroups within
     # one per CU (256 CUs); above 32 tokens 32 x 64 over both halves when that fits, else 64 x 64,

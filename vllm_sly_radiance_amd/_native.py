@@ -44,6 +44,7 @@ SIGNATURES = {
     "w4a8_scratch_bytes": (_int, [_int, _int, _int, _psz, _psz]),
     "w4a8_workspace_bytes": (_int, [_int, _int, _psz, _psz]),
     "w4a8_linear": (_int, [_vp, _long, _vp, _vp, _vp, _vp, _vp, _int, _int, _int, _vp]),
+    "w4a8_linear_fused": (_int, [_int, _int, _int, _long]),
     "w4a8_add_rms_quant": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _int, _int, _c.c_float, _vp,
                                   _int]),
     "w4a8_silu_mul_quant": (_int, [_vp, _vp, _vp, _int, _int, _vp, _int]),
@@ -123,6 +124,14 @@ def tiled_bytes(M: int, K: int) -> int:
 
 def linear(x_ptr, ldx, q_ptr, s_ptr, wq_ptr, sq_ptr, c_ptr, M, N, K, stream):
     check(lib().w4a8_linear(x_ptr, ldx, q_ptr, s_ptr, wq_ptr, sq_ptr, c_ptr, M, N, K, stream))
+
+
+def linear_fused(M: int, N: int, K: int, ldx: int) -> bool:
+    """Does linear() run this shape as one launch (quantizer inside the streaming GEMM)."""
+    r = lib().w4a8_linear_fused(M, N, K, ldx)
+    if r < 0:
+        check(1)
+    return bool(r)
 
 
 def add_rms_quant(y_ptr, res_ptr, w_ptr, q_ptr, s_ptr, res_out_ptr, M, K, eps, stream,

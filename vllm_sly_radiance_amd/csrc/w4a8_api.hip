@@ -397,7 +397,7 @@ int gemm_dispatch(const void* a, const float* as, const void* wq, const void* sq
     if (!stream_fits(variant, M, N, K, d.cus, d.lds))
       return fail(W4A8_EINVAL, "%s: stream variant %d does not serve M=%d N=%d K=%d",
                   who, variant, M, N, K);
-    return hip_status(launch_stream(g, variant, d.cus, st), who);
+    return hip_status(launch_stream(g, variant, d.cus, false, 0, st), who);
   }
   return fail(W4A8_EINVAL, "%s: unknown kernel %d", who, kernel);
 }
@@ -653,11 +653,37 @@ W4A8_API int w4a8_workspace_bytes(int max_m, int max_n, size_t* partial_bytes,
   return W4A8_OK;
 }
 
+// The stream variant that runs the whole linear in one launch for this shape, or -1: the plan
+// takes the streaming family and stream_linear_fits holds (few rows, 16-byte rows, LDS).
+static int linear_fused_variant(int M, int N, int K, long ldx, bool x_aligned, int dev) {
+  if (!x_aligned || M < 1 || M > 8) return -1;
+  int kernel, variant, split_k;
+  plan_impl(M, N, K, dev, registered_scratch(dev), &kernel, &variant, &split_k);
+  if (kernel != W4A8_KERNEL_STREAM) return -1;
+  const DeviceInfo d = device_info(dev);
+  return stream_linear_fits(variant, M, N, K, ldx, d.cus, d.lds) ? variant : -1;
+}
+
+W4A8_API int w4a8_linear_fused(int M, int N, int K, long ldx) {
+  if (check_gemm_shape("w4a8_linear_fused", M, N, K)) return -1;
+  return linear_fused_variant(M, N, K, ldx, true, current_device()) >= 0 ? 1 : 0;
+}
+
 W4A8_API int w4a8_linear(const void* x, long ldx, void* q, float* scale, const void* wq,
                          const void* sq, void* c, int M, int N, int K, void* stream) {
   if (int e = check_gemm_shape("w4a8_linear", M, N, K)) return e;
   if (M == 0) return W4A8_OK;
   if (int e = check_gemm_ptrs("w4a8_linear", q, scale, wq, sq, c)) return e;
+  if (!x) return fail(W4A8_EINVAL, "w4a8_linear: null x");
+  if (ldx < K) return fail(W4A8_EINVAL, "w4a8_linear: ldx=%ld < K=%d", ldx, K);
+  const int dev = current_device();
+  const int v = linear_fused_variant(M, N, K, ldx, aligned(x, 16), dev);
+  if (v >= 0) {
+    const GemmArgs g{(const uint8_t*)x, nullptr, (const uint8_t*)wq, (const uint32_t*)sq,
+                     (uint16_t*)c, M, N, K, N};
+    return hip_status(launch_stream(g, v, device_info(dev).cus, true, ldx, (hipStream_t)stream),
+                      "w4a8_linear");
+  }
   if (int e = w4a8_quant_per_token(x, ldx, q, scale, M, K, stream)) return e;
   return w4a8_gemm(q, scale, wq, sq, c, M, N, K, stream);
 }

@@ -145,10 +145,15 @@ struct StreamCfg { int nt, kpw, waves, u; };
 int stream_variant_count();
 StreamCfg stream_variant(int v);
 int stream_grid(int N, int cus);
-size_t stream_lds_bytes(int variant, int M, int K);
+size_t stream_lds_bytes(int variant, int M, int K, bool fused);
 int stream_granules(int variant, int N, int K, int cus);
 bool stream_fits(int variant, int M, int N, int K, int cus, size_t lds_limit);
-hipError_t launch_stream(const GemmArgs& g, int variant, int cus, hipStream_t stream);
+// The variant can also run the whole linear (bf16 activations with row stride ldx elements,
+// quantized in the kernel) and it pays: M x KPW <= 8, 16-byte rows, the staging area fits the LDS.
+bool stream_linear_fits(int variant, int M, int N, int K, long ldx, int cus, size_t lds_limit);
+// fused: g.a is bf16 [M, K] with row stride lda elements and g.a_scale is unused
+hipError_t launch_stream(const GemmArgs& g, int variant, int cus, bool fused, long lda,
+                         hipStream_t stream);
 
 // Pipelined streaming family (M <= 16 * MF): grid = at most one workgroup per CU, each with the
 // same number of n-tiles (at most nt) and all of K; each of the `waves` waves streams a contiguous

@@ -199,8 +199,10 @@ def gemm(x_fp8: torch.Tensor, x_scale: torch.Tensor, weight: torch.Tensor,
 @torch.library.custom_op("radiance::mxfp4_linear", mutates_args=())
 def mxfp4_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
                  weight_ref: torch.Tensor) -> torch.Tensor:
-    """bf16 x [M, K] -> bf16 [M, N]: per-token e4m3 quant + W4A8 GEMM, two launches on the current
-    stream. N and K come from weight_ref's shape (see module docstring)."""
+    """bf16 x [M, K] -> bf16 [M, N]: per-token e4m3 quant + W4A8 GEMM on the current stream. At
+    M = 1 (and M = 2 on most shapes) one launch quantizes inside the streaming GEMM, else two
+    launches; the bits are the same either way. N and K come from weight_ref's shape (see module
+    docstring)."""
     STATS["calls"] += 1
     N, K = weight_ref.shape[0], weight_ref.shape[1]
     if x.dim() != 2 or x.shape[1] != K:
