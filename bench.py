@@ -106,6 +106,20 @@ class QuantGemm(Gemm):
         super().launch(i, stream)
 
 
+class Linear:
+    """A Gemm's operands run as radiance::mxfp4_linear runs them through w4a8_linear: bf16
+    activations in, one launch where the quantizer runs inside the streaming GEMM
+    (w4a8_linear_fused), else two."""
+
+    def __init__(self, g):
+        self.g, self.w = g, g.w
+
+    def launch(self, i, stream):
+        g = self.g
+        g._native.linear(g.x.data_ptr(), g.K, g.q.data_ptr(), g.s.data_ptr(), g.w[i].data_ptr(),
+                         g.ws[i].data_ptr(), g.out.data_ptr(), g.M, g.N, g.K, stream)
+
+
 def per_launch_us(g, n, stream_obj):
     """Median and mean duration of single launches, each bracketed by its own HIP event pair on the
     launch stream (includes the event overhead; a cross-check only)."""
@@ -223,22 +237,31 @@ def bench_prefill():
 
 
 def bench_layer_m1():
+    """The four linears of one layer at M = 1: the GEMM on pre-quantized activations (`us`), and
+    the linear on bf16 activations as the op runs it (`linear_us`: one launch with the quantizer
+    inside where `one_launch`, else quantizer + GEMM)."""
     import torch
-    out, tot_us, tot_bytes = [], 0.0, 0
+    out, tot_us, tot_lin, tot_bytes = [], 0.0, 0.0, 0
     for name, N, K in LAYER_M1:
         copies = max(2, -(-512 * 2 ** 20 // (N * K * 17 // 32)))
         g = Gemm(1, N, K, copies, seed=3)
         sec, _, _, _ = graph_timed(g, 32 * copies, 4 * copies, warm_seconds=0.5)
         us = sec / (32 * copies) * 1e6
+        sec, _, _, _ = graph_timed(Linear(g), 32 * copies, 4 * copies, warm_seconds=0.2)
+        lin = sec / (32 * copies) * 1e6
         nb = gemm_bytes(1, N, K)
         tot_us += us
+        tot_lin += lin
         tot_bytes += nb
         out.append(dict(name=name, N=N, K=K, us=round(us, 2),
-                        gbs=round(nb / (us * 1e-6) / 1e9, 1), plan=g.plan))
+                        gbs=round(nb / (us * 1e-6) / 1e9, 1), plan=g.plan,
+                        linear_us=round(lin, 2),
+                        one_launch=bool(g._native.linear_fused(1, N, K, K))))
         del g
         torch.cuda.empty_cache()
     return dict(layers=out, us_per_layer=round(tot_us, 2),
-                gbs=round(tot_bytes / (tot_us * 1e-6) / 1e9, 1))
+                gbs=round(tot_bytes / (tot_us * 1e-6) / 1e9, 1),
+                linear_us_per_layer=round(tot_lin, 2))
 
 
 class Producer:

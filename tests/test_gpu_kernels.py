@@ -349,6 +349,32 @@ def test_gemm_every_stream_variant(gpu_lib, N, K):
     assert (ran > 0) == served
 
 
+@pytest.mark.parametrize("N,K", [(17408, 5120), (10240, 5120), (5120, 8704), (1040, 2560)])
+def test_stream_eight_rows_equal_the_same_rows_of_sixteen(gpu_lib, N, K):
+    """At M <= 8 the streaming kernel loads each k-tile's activation fragment with one load (both
+    16-byte runs of the 8 live tokens, the second moved across lanes); above 8 with two. Every
+    output column depends on its own token only, with the same sums in the same order, so the
+    rows of an M <= 8 call equal the same rows inside an M = 9..16 call bit for bit, at every
+    variant that serves the shape."""
+    w, ws = cached_weights(N, K, N + 7 * K)
+    wq, sq = gpu_repack(w, ws)
+    big = synthetic.activations(16, K, seed=N + 1)
+    qb, sb = O.quant_per_token(big)
+    ran = 0
+    for v, cfg in enumerate(_native.variants(STREAM)):
+        for M, Mb in [(1, 9), (5, 13), (8, 16)]:
+            try:
+                ref = gpu_gemm(qb[:Mb], sb[:Mb], wq, sq, N, K, STREAM, v, 1)
+            except RuntimeError as e:
+                assert "does not serve" in str(e)
+                continue
+            out = gpu_gemm(qb[:M], sb[:M], wq, sq, N, K, STREAM, v, 1)
+            ran += 1
+            bad = np.argwhere(out != ref[:M])
+            assert bad.size == 0, f"variant {v} {cfg} M={M}: {len(bad)} differ, {bad[:3].tolist()}"
+    assert ran > 0
+
+
 @pytest.mark.parametrize("N,K", [(17408, 5120), (5120, 8704), (1040, 2560), (33, 640),
                                  (5120, 6144), (10240, 5120), (48, 1056), (2064, 4128)])
 def test_gemm_every_ring_variant(gpu_lib, N, K):

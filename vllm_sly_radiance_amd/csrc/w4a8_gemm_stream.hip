@@ -16,9 +16,10 @@
 //  * Wave w owns the k-groups [KG w / W, KG (w + 1) / W) (4 k-tiles each, so one scale dword per
 //    n-tile) of every n-tile of the workgroup. It loads its activation fragments for those
 //    k-tiles straight into registers (lane l: token l % 16, k 16 (l / 16).. and 64 + 16 (l / 16)..;
-//    tokens past M read as zero), then the scale dwords, then the granules k-tile by k-tile, and
-//    multiplies each fragment into all NT n-tiles as their granules land: no LDS staging, no
-//    barrier before the MFMAs, NT independent accumulator chains.
+//    tokens past M read as zero; at M <= 8 one load per k-tile, see H8), then the scale dwords,
+//    then the granules k-tile by k-tile, and multiplies each fragment into all NT n-tiles as
+//    their granules land: no LDS staging, no barrier before the MFMAs, NT independent
+//    accumulator chains.
 //  * Every global load goes through a buffer resource; loads past the workgroup's n-tiles or the
 //    wave's k-range return zero without a memory access, so the code has no branches around loads
 //    and the compiler counts outstanding loads exactly.
@@ -26,13 +27,14 @@
 //    (deterministic), scaled by the per-token fp32 scale and stored as bf16. Nothing crosses
 //    workgroups.
 //  * FQ = true takes bf16 activations (up to 8 rows; the host uses it for M x KPW <= 8) and
-//    quantizes them itself, the whole linear in one launch. The waves of a workgroup together cover all of K, so the per-token amax is a
-//    reduction inside the workgroup: each wave copies its k-range of the (at most 8) rows into
-//    LDS (buffer_load ... lds, chunks XOR-swizzled by token so the fragment reads are
-//    conflict-free), issues its scale and weight loads, takes the amax of its range, and after
-//    one barrier every lane has its token's row amax. The codes then come from the same steps as
-//    the plain quantizer's (w4a8_fp8.h), so the output equals quantizer + GEMM bit for bit. A
-//    second barrier frees the staging area, which the final reduction reuses.
+//    quantizes them itself, the whole linear in one launch. The waves of a workgroup together
+//    cover all of K, so the per-token amax is a reduction inside the workgroup: each wave copies
+//    its k-range of the (at most 8) rows into LDS (buffer_load ... lds, chunks XOR-swizzled by
+//    token so the fragment reads are conflict-free), issues its scale and weight loads, takes the
+//    amax of its range, and after one barrier every lane has its token's row amax. The codes then
+//    come from the same steps as the plain quantizer's (w4a8_fp8.h), so the output equals
+//    quantizer + GEMM bit for bit. A second barrier frees the staging area, which the final
+//    reduction reuses.
 #include "w4a8_fp8.h"
 
 namespace w4a8 {
@@ -64,15 +66,18 @@ __device__ __forceinline__ int stage_off(int seg, int t, int c) {
 }
 
 // NT: n-tiles per workgroup at most; KPW: k-tiles per wave at most (a multiple of 4); W: waves.
-// The host requires K % 512 == 0 (whole k-groups), M <= 16 (M <= 8 with FQ),
+// The host requires K % 512 == 0 (whole k-groups), M <= 16 (M <= 8 with FQ or H8),
 // 4 * ceil(KG / W) <= KPW. With FQ, A is the bf16 activation (row stride lda elements, 16-byte
-// aligned rows) and As is not read.
-template <int NT, int KPW, int W, bool FQ>
+// aligned rows) and As is not read. H8 (M <= 8, e4m3 A): one load per k-tile brings both 16-byte
+// runs of the 8 live tokens (lanes 8..15 of each row of 16 load the second run of token r - 8,
+// and a row rotation by 8 lanes hands it to lane r), half the activation loads; the MFMA columns
+// of tokens 8..15 then hold other tokens' bytes, and those columns are never stored.
+template <int NT, int KPW, int W, bool FQ, bool H8>
 __global__ __launch_bounds__(W * 64) void gemm_stream(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
     const uint32_t* __restrict__ Sq, uint16_t* __restrict__ C, int M, int N, int K, int KT,
     int KG, int NTILES, int vec_out, long lda) {
-  static_assert(KPW % 4 == 0 && NT >= 1 && W >= 1 && W <= 16, "stream variant");
+  static_assert(KPW % 4 == 0 && NT >= 1 && W >= 1 && W <= 16 && !(FQ && H8), "stream variant");
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   // Wave-uniform work selection in scalar registers; 32-bit products only (the host bounds them).
@@ -103,6 +108,14 @@ __global__ __launch_bounds__(W * 64) void gemm_stream(
     }
     __builtin_amdgcn_sched_barrier(0);           // the staging copies go out first: the wait
                                                  // below counts the loads issued after them
+  } else if constexpr (H8) {
+    const auto a_src = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, M * K, kBufferWord3);
+#pragma unroll
+    for (int u = 0; u < KPW; ++u) {
+      const int kt = min(kr0 + u, KT - 1);
+      xlo[u] = __builtin_amdgcn_raw_buffer_load_b128(
+          a_src, (m & 7) * K + kt * kKTile + 64 * (m >> 3) + 16 * g, 0, 0);
+    }
   } else {
     const auto a_src = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, M * K, kBufferWord3);
 #pragma unroll
@@ -213,6 +226,14 @@ __global__ __launch_bounds__(W * 64) void gemm_stream(
     tok_scale = __builtin_bit_cast(
         float, __builtin_amdgcn_raw_buffer_load_b32(as_src, (lane & 15) * 4, 0, 0));
     __builtin_amdgcn_sched_barrier(0);           // every load above is issued before any MFMA
+    if constexpr (H8) {
+      // DPP row_ror:8 (within each row of 16 lanes, lane r takes lane (r + 8) % 16's value)
+#pragma unroll
+      for (int u = 0; u < KPW; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          xhi[u][i] = __builtin_amdgcn_mov_dpp(xlo[u][i], 0x128, 0xF, 0xF, false);
+    }
   }
 
   // ---- 3. MFMAs, branch-free: loads past the k-range or the n-tiles are zero and add nothing ----
@@ -323,22 +344,23 @@ hipError_t launch_stream(const GemmArgs& g, int variant, int cus, bool fused, lo
   const dim3 grid(stream_grid(g.N, cus)), block(kStream[variant].waves * 64);
   const size_t lds = stream_lds_bytes(variant, g.M, g.K, fused);
   int idx = 0;
-#define W4A8_STREAM_GO(nt, kpw, w, fq)                                                           \
+#define W4A8_STREAM_GO(nt, kpw, w, fq, h8)                                                       \
   {                                                                                              \
     if (lds > 64 * 1024) {                                                                       \
-      const hipError_t e = hipFuncSetAttribute((const void*)gemm_stream<nt, kpw, w, fq>,         \
+      const hipError_t e = hipFuncSetAttribute((const void*)gemm_stream<nt, kpw, w, fq, h8>,     \
                                                hipFuncAttributeMaxDynamicSharedMemorySize,       \
                                                (int)lds);                                        \
       if (e != hipSuccess) return e;                                                             \
     }                                                                                            \
-    hipLaunchKernelGGL((gemm_stream<nt, kpw, w, fq>), grid, block, lds, stream, g.a, g.a_scale,  \
-                       g.wq, g.sq, g.c, g.M, g.N, g.K, KT, KG, NTILES, vec_out, lda);            \
+    hipLaunchKernelGGL((gemm_stream<nt, kpw, w, fq, h8>), grid, block, lds, stream, g.a,         \
+                       g.a_scale, g.wq, g.sq, g.c, g.M, g.N, g.K, KT, KG, NTILES, vec_out, lda); \
     return hipGetLastError();                                                                    \
   }
 #define W4A8_STREAM_LAUNCH(nt, kpw, w)                                                           \
   if (idx++ == variant) {                                                                        \
-    if (fused) W4A8_STREAM_GO(nt, kpw, w, true)                                                  \
-    W4A8_STREAM_GO(nt, kpw, w, false)                                                            \
+    if (fused) W4A8_STREAM_GO(nt, kpw, w, true, false)                                           \
+    if (g.M <= 8) W4A8_STREAM_GO(nt, kpw, w, false, true)                                        \
+    W4A8_STREAM_GO(nt, kpw, w, false, false)                                                     \
   }
   W4A8_STREAM_TABLE(W4A8_STREAM_LAUNCH)
 #undef W4A8_STREAM_LAUNCH
