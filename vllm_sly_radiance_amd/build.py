@@ -28,6 +28,11 @@ FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden",
     # keep the compiler from forming packed-fp32 VALU ops (v_pk_*_f32)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # the first 14 kernel-argument dwords arrive in SGPRs at wave launch instead of through a
+    # scalar load from the kernarg segment (the kernels order their arguments so that everything
+    # the first memory requests depend on comes first); the code object keeps a 256-byte prologue
+    # that loads them itself where the firmware does not preload
+    "-mllvm", "-amdgpu-kernarg-preload-count=14",
     "-Wall", "-Wno-unused-function",
 ]
 

@@ -75,14 +75,15 @@ __device__ __forceinline__ int stage_off(int seg, int t, int c) {
 template <int NT, int KPW, int W, bool FQ, bool H8>
 __global__ __launch_bounds__(W * 64) void gemm_stream(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
-    const uint32_t* __restrict__ Sq, uint16_t* __restrict__ C, int M, int N, int K, int KT,
-    int KG, int NTILES, int vec_out, long lda) {
+    const uint32_t* __restrict__ Sq, int M, int K, int NTILES, int G, int lda,
+    uint16_t* __restrict__ C, int N, int vec_out) {
   static_assert(KPW % 4 == 0 && NT >= 1 && W >= 1 && W <= 16 && !(FQ && H8), "stream variant");
+  const int KT = K / kKTile, KG = KT / kKGroup;  // K % 512 == 0
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   // Wave-uniform work selection in scalar registers; 32-bit products only (the host bounds them).
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int G = gridDim.x, b = blockIdx.x;
+  const int b = blockIdx.x;
   const int ntb0 = b * NTILES / G, nth = (b + 1) * NTILES / G - ntb0;
   const int kr0 = 4 * (KG * wave / W), kr1 = 4 * (KG * (wave + 1) / W);
 
@@ -102,7 +103,7 @@ __global__ __launch_bounds__(W * 64) void gemm_stream(
     for (int j = 0; j < 2 * KPW; ++j) {
       // segment j of the wave's range; k-tiles past K (a range shorter than KPW) read zero
       const int k = kr0 * kKTile + 64 * j + 8 * c;
-      const int off = k < K ? (int)(t * lda * 2) + 2 * k : 0x7FFFFFF0;
+      const int off = k < K ? t * lda * 2 + 2 * k : 0x7FFFFFF0;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(x_src, (lds_ptr_t)(stage + j * 1024), 16, off,
                                                0, 0, 0);
     }
@@ -330,7 +331,7 @@ bool stream_linear_fits(int variant, int M, int N, int K, long ldx, int cus, siz
   const StreamCfg c = kStream[variant];
   if (M * c.kpw > 8) return false;
   return stream_fits(variant, M, N, K, cus, lds_limit) && ldx >= K &&
-         ldx % 8 == 0 && (long)M * ldx * 2 < (1L << 31) &&
+         ldx % 8 == 0 && 16L * ldx < (1L << 31) &&   // row offsets of all 8 staged rows
          stream_lds_bytes(variant, M, K, true) <= lds_limit;
 }
 
@@ -338,7 +339,6 @@ bool stream_linear_fits(int variant, int M, int N, int K, long ldx, int cus, siz
 // kernel); otherwise g.a is e4m3 [M, K] and g.a_scale its per-token scales
 hipError_t launch_stream(const GemmArgs& g, int variant, int cus, bool fused, long lda,
                          hipStream_t stream) {
-  const int KT = g.K / kKTile, KG = KT / kKGroup;
   const int NTILES = padded_n(g.N) / kNTile;
   const int vec_out = (g.N % 4 == 0 && ((uintptr_t)g.c % 8) == 0) ? 1 : 0;
   const dim3 grid(stream_grid(g.N, cus)), block(kStream[variant].waves * 64);
@@ -353,7 +353,8 @@ hipError_t launch_stream(const GemmArgs& g, int variant, int cus, bool fused, lo
       if (e != hipSuccess) return e;                                                             \
     }                                                                                            \
     hipLaunchKernelGGL((gemm_stream<nt, kpw, w, fq, h8>), grid, block, lds, stream, g.a,         \
-                       g.a_scale, g.wq, g.sq, g.c, g.M, g.N, g.K, KT, KG, NTILES, vec_out, lda); \
+                       g.a_scale, g.wq, g.sq, g.M, g.K, NTILES, (int)grid.x, (int)lda, g.c, g.N, \
+                       vec_out);                                                                 \
     return hipGetLastError();                                                                    \
   }
 #define W4A8_STREAM_LAUNCH(nt, kpw, w)                                                           \
