@@ -51,16 +51,6 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
   return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
-// The same with a select instead of a branch: two more VALU operations, no exec-mask branching.
-// Cheaper where a SIMD runs one or two waves (nothing hides the scalar branch work); the branch
-// form is cheaper in VALU-bound code with many waves per SIMD.
-__device__ __forceinline__ uint32_t f32_to_bf16_sel(float f) {
-  const uint32_t u = __float_as_uint(f);
-  const uint32_t rne = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-  const uint32_t nan = ((u >> 16) & 0x8000u) | 0x7FC0u;
-  return (u & 0x7FFFFFFFu) > 0x7F800000u ? nan : rne;
-}
-
 // Word 3 of a raw (stride 0) buffer resource on gfx9-family GPUs: 32-bit data format, no swizzle.
 // Loads through such a resource return 0 for offsets at or past num_records, without a memory access.
 constexpr int kBufferWord3 = 0x00020000;

@@ -21,7 +21,11 @@
 //  * exp is exp_f32 below: Cody-Waite reduction by ln 2 (Cody and Waite, "Software Manual for the
 //    Elementary Functions", 1980; ln 2 split into a 16-bit head and a tail) and the degree-7
 //    Taylor polynomial of e^r on |r| <= ln2 / 2 by Horner, the reduction and each Horner step one
-//    fused multiply-add, then an exact scaling by 2^n.
+//    fused multiply-add, then an exact scaling by 2^n;
+//  * silu's division is the IEEE quotient (silu8: the reciprocal with one Markstein correction
+//    where that equals it, else the division);
+//  * rounding to bf16 is round to nearest even with NaN -> 0x7FC0 | sign (the hardware convert,
+//    with the software rounding for a group that holds a NaN).
 #pragma clang fp contract(off)
 
 #include "w4a8_fp8.h"
@@ -59,18 +63,39 @@ __device__ __forceinline__ float exp_f32(float y_in) {
   return y_in != y_in ? y_in : e;
 }
 
-__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + exp_f32(-x)); }
-
-// kSel: round to bf16 with a select rather than a branch (kernels with one wave per SIMD)
-template <bool kSel>
-__device__ __forceinline__ uint32_t to_bf16(float x) {
-  return kSel ? f32_to_bf16_sel(x) : f32_to_bf16(x);
+// silu of 8 values, x / (1 + exp_f32(-x)) with the IEEE quotient. Where every value of the group
+// has |x| <= 44 (1 <= d <= 2^64: the reciprocal is a normal number, nothing is infinite or NaN)
+// the quotient comes from the hardware reciprocal and one Markstein correction, y = rcp(d),
+// q = x y, r = fma(-d, q, x), q + r y, with x's sign (a -0 quotient would otherwise come out +0):
+// five operations instead of the division's ten. Any other group (rare) divides. Every bf16 x is
+// checked against the IEEE quotient on the GPU (the silu tests run all 65536 gate patterns).
+__device__ __forceinline__ void silu8(const float (&x)[8], float (&s)[8]) {
+  float d[8];
+  bool wide = false;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    d[j] = 1.0f + exp_f32(-x[j]);
+    const float y = __builtin_amdgcn_rcpf(d[j]);
+    const float q = x[j] * y;
+    const float r = __builtin_fmaf(-d[j], q, x[j]);
+    s[j] = __builtin_copysignf(__builtin_fmaf(r, y, q), x[j]);
+    wide |= !(__builtin_fabsf(x[j]) <= 44.0f);
+  }
+  if (__builtin_expect(wide, 0)) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s[j] = x[j] / d[j];
+  }
 }
 
-template <bool kSel>
-__device__ __forceinline__ float bf16_round(float x) {
-  return __uint_as_float(to_bf16<kSel>(x) << 16);
+// Round to bf16 with the hardware convert (v_cvt_pk_bf16_f32, round to nearest even, the same
+// bits as f32_to_bf16 for every non-NaN input, subnormals included); a NaN keeps its payload.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t cvt_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
 }
+// for an intermediate whose NaNs only ever reach the canonicalizing pack below
+__device__ __forceinline__ float bf16_round_hw(float x) { return (float)(__bf16)x; }
 
 __device__ __forceinline__ void unpack8(const uint4 v, float (&f)[8]) {
   f[0] = __uint_as_float(v.x << 16); f[1] = __uint_as_float(v.x & 0xFFFF0000u);
@@ -79,12 +104,23 @@ __device__ __forceinline__ void unpack8(const uint4 v, float (&f)[8]) {
   f[6] = __uint_as_float(v.w << 16); f[7] = __uint_as_float(v.w & 0xFFFF0000u);
 }
 
-template <bool kSel>
-__device__ __forceinline__ uint4 pack8(const float (&f)[8]) {
-  return make_uint4(to_bf16<kSel>(f[0]) | (to_bf16<kSel>(f[1]) << 16),
-                    to_bf16<kSel>(f[2]) | (to_bf16<kSel>(f[3]) << 16),
-                    to_bf16<kSel>(f[4]) | (to_bf16<kSel>(f[5]) << 16),
-                    to_bf16<kSel>(f[6]) | (to_bf16<kSel>(f[7]) << 16));
+// software rounding, NaN -> 0x7FC0 | sign
+__device__ __forceinline__ uint4 pack8_sw(const float (&f)[8]) {
+  return make_uint4(f32_to_bf16(f[0]) | (f32_to_bf16(f[1]) << 16),
+                    f32_to_bf16(f[2]) | (f32_to_bf16(f[3]) << 16),
+                    f32_to_bf16(f[4]) | (f32_to_bf16(f[5]) << 16),
+                    f32_to_bf16(f[6]) | (f32_to_bf16(f[7]) << 16));
+}
+
+// pack8 with the hardware convert: two values per operation. A group holding a NaN (rare) takes
+// the software rounding, whose NaNs are canonical (0x7FC0 | sign).
+__device__ __forceinline__ uint4 pack8_hw(const float (&f)[8]) {
+  bool nan = false;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) nan |= f[j] != f[j];
+  if (__builtin_expect(nan, 0)) return pack8_sw(f);
+  return make_uint4(cvt_bf16x2(f[0], f[1]), cvt_bf16x2(f[2], f[3]), cvt_bf16x2(f[4], f[5]),
+                    cvt_bf16x2(f[6], f[7]));
 }
 
 // Row sum over the workgroup in the fixed order (every thread gets the result).
@@ -170,7 +206,7 @@ __global__ __launch_bounds__(kThreads) void add_rms_quant(
         v[i][j] = a[j] + b[j];
         part = part + v[i][j] * v[i][j];
       }
-      res_out[g] = pack8<true>(v[i]);
+      res_out[g] = pack8_hw(v[i]);
     }
   }
   const float inv = 1.0f / sqrtf(block_sum_fixed(part) / (float)K + eps);
@@ -183,7 +219,7 @@ __global__ __launch_bounds__(kThreads) void add_rms_quant(
       unpack8(w[g], wf);
 #pragma unroll
       for (int j = 0; j < 8; ++j) n[j] = (v[i][j] * inv) * (wf[j] + 1.0f);
-      nb[i] = pack8<true>(n);
+      nb[i] = pack8_hw(n);
     }
   }
   quant_tail<G, kThreads>(nb, nv, q, scale, row, tiled);
@@ -191,14 +227,14 @@ __global__ __launch_bounds__(kThreads) void add_rms_quant(
 
 // SiLU-and-mul: gate_up [M, 2N] -> bf16(bf16(silu(gate)) * up). T threads per row: the only
 // reduction is the amax, so any T gives the same bits; short rows of work (small M) take 1024.
-template <bool kSel>
 __device__ __forceinline__ uint4 silu_mul_group(const uint4 gv, const uint4 uv) {
-  float a[8], b[8], p[8];
+  float a[8], b[8], sg[8], p[8];
   unpack8(gv, a);
   unpack8(uv, b);
+  silu8(a, sg);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) p[j] = bf16_round<kSel>(silu_f32(a[j])) * b[j];
-  return pack8<kSel>(p);
+  for (int j = 0; j < 8; ++j) p[j] = bf16_round_hw(sg[j]) * b[j];
+  return pack8_hw(p);
 }
 
 // One workgroup per row. With `out` set the bf16 stage is written there ([M, N]) and nothing is
@@ -215,7 +251,7 @@ __global__ __launch_bounds__(T) void silu_mul_quant(const uint4* __restrict__ gu
 #pragma unroll
   for (int i = 0; i < G; ++i) {
     const int g = tid + i * T;
-    if (g < nv) nb[i] = silu_mul_group<false>(gate[g], up[g]);
+    if (g < nv) nb[i] = silu_mul_group(gate[g], up[g]);
   }
   if (out) {
 #pragma unroll
@@ -242,12 +278,13 @@ __device__ __forceinline__ uint4 gdn_group(const uint4* __restrict__ x,
   for (int o = 8; o > 0; o >>= 1) part = part + __shfl_xor(part, o, 16);
   if (!in) return make_uint4(0, 0, 0, 0);
   const float inv = 1.0f / sqrtf(part * (1.0f / 128.0f) + eps);
-  float zz[8], wf[8], n[8];
+  float zz[8], sz[8], wf[8], n[8];
   unpack8(zr[g], zz);
   unpack8(w[g & 15], wf);
+  silu8(zz, sz);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) n[j] = ((v[j] * inv) * wf[j]) * silu_f32(zz[j]);
-  return pack8<false>(n);
+  for (int j = 0; j < 8; ++j) n[j] = ((v[j] * inv) * wf[j]) * sz[j];
+  return pack8_hw(n);
 }
 
 // Per-head gated RMSNorm (head = 128 = 16 groups; norm before the gate, weight without +1):
@@ -309,7 +346,7 @@ __global__ __launch_bounds__(64) void silu_mul_quant_split(const uint4* __restri
   const int chunk = blockIdx.x, row = blockIdx.y, nv = N >> 3, g = chunk * 64 + threadIdx.x;
   const uint4* gate = gu + (size_t)row * 2 * nv;
   const bool in = g < nv;
-  const uint4 nb = in ? silu_mul_group<true>(gate[g], gate[nv + g]) : make_uint4(0, 0, 0, 0);
+  const uint4 nb = in ? silu_mul_group(gate[g], gate[nv + g]) : make_uint4(0, 0, 0, 0);
   split_tail<kQuant>(nb, in, q, scale, part, row, chunk, S, nv, tiled);
 }
 
