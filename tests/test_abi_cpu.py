@@ -122,13 +122,14 @@ def test_plan_bands(lib):
 
 
 def test_one_launch_linear_where_it_pays(lib):
-    """w4a8_linear runs as one launch (the quantizer inside the streaming GEMM) only for rows x
-    k-tiles per wave <= 8: M = 1 on every stream shape, M = 2 where a wave holds 4 k-tiles (not on
-    down's 8); never above the streaming band, never for rows that are not 16-byte chunks."""
+    """w4a8_linear runs as one launch (quantizing waves beside the streaming GEMM's weight waves)
+    at M <= 2, and up to M = 4 where a workgroup holds 3 or more n-tiles; never on 16-wave
+    variants (no room for the quantizing waves), never for rows that are not 16-byte chunks."""
     f = lib.w4a8_linear_fused
-    for N, K in [(17408, 5120), (10240, 5120), (5120, 6144), (2048, 1024), (1040, 512)]:
-        assert [f(M, N, K, K) for M in range(1, 10)] == [1, 1] + [0] * 7, (N, K)
-    assert [f(M, 5120, 8704, 8704) for M in (1, 2, 3)] == [1, 0, 0]
+    for N, K, up_to in [(17408, 5120, 4), (10240, 5120, 4), (5120, 6144, 2), (5120, 8704, 2),
+                        (5120, 5120, 2), (2048, 1024, 0), (1040, 512, 0)]:
+        assert [f(M, N, K, K) for M in range(1, 10)] == [int(M <= up_to) for M in range(1, 10)], \
+            (N, K)
     assert f(1, 17408, 5120, 5120 + 72) == 1
     assert f(1, 17408, 5120, 5120 + 4) == 0                # rows not whole 16-byte chunks
     assert f(1, 17408, 5000, 5000) == -1                   # K not a multiple of 32: an error

@@ -26,15 +26,8 @@
 //  * The W partial sums of each n-tile meet once in LDS and are added in wave order
 //    (deterministic), scaled by the per-token fp32 scale and stored as bf16. Nothing crosses
 //    workgroups.
-//  * FQ = true takes bf16 activations (up to 8 rows; the host uses it for M x KPW <= 8) and
-//    quantizes them itself, the whole linear in one launch. The waves of a workgroup together
-//    cover all of K, so the per-token amax is a reduction inside the workgroup: each wave copies
-//    its k-range of the (at most 8) rows into LDS (buffer_load ... lds, chunks XOR-swizzled by
-//    token so the fragment reads are conflict-free), issues its scale and weight loads, takes the
-//    amax of its range, and after one barrier every lane has its token's row amax. The codes then
-//    come from the same steps as the plain quantizer's (w4a8_fp8.h), so the output equals
-//    quantizer + GEMM bit for bit. A second barrier frees the staging area, which the final
-//    reduction reuses.
+//  * gemm_stream_fq (below) is the whole linear in one launch: bf16 activations, the per-token
+//    quantizer run by extra waves of each workgroup while the weight waves stream.
 #include "w4a8_fp8.h"
 
 namespace w4a8 {
@@ -58,26 +51,18 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// Fused-quant staging, per wave: KPW k-tiles x 8 tokens x 128 bf16 = 2 KPW KiB. Segment j (64
-// elements of the wave's k-range, 1 KiB) holds token t's 16-byte chunk c at slot 8 t + (c ^ t).
-template <int KPW>
-__device__ __forceinline__ int stage_off(int seg, int t, int c) {
-  return seg * 1024 + 16 * (8 * t + (c ^ t));
-}
-
 // NT: n-tiles per workgroup at most; KPW: k-tiles per wave at most (a multiple of 4); W: waves.
-// The host requires K % 512 == 0 (whole k-groups), M <= 16 (M <= 8 with FQ or H8),
-// 4 * ceil(KG / W) <= KPW. With FQ, A is the bf16 activation (row stride lda elements, 16-byte
-// aligned rows) and As is not read. H8 (M <= 8, e4m3 A): one load per k-tile brings both 16-byte
-// runs of the 8 live tokens (lanes 8..15 of each row of 16 load the second run of token r - 8,
-// and a row rotation by 8 lanes hands it to lane r), half the activation loads; the MFMA columns
-// of tokens 8..15 then hold other tokens' bytes, and those columns are never stored.
-template <int NT, int KPW, int W, bool FQ, bool H8>
+// The host requires K % 512 == 0 (whole k-groups), M <= 16 (M <= 8 with H8),
+// 4 * ceil(KG / W) <= KPW. H8 (M <= 8): one load per k-tile brings both 16-byte runs of the 8
+// live tokens (lanes 8..15 of each row of 16 load the second run of token r - 8, and a row
+// rotation by 8 lanes hands it to lane r), half the activation loads; the MFMA columns of tokens
+// 8..15 then hold other tokens' bytes, and those columns are never stored.
+template <int NT, int KPW, int W, bool H8>
 __global__ __launch_bounds__(W * 64) void gemm_stream(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
-    const uint32_t* __restrict__ Sq, int M, int K, int NTILES, int G, int lda,
+    const uint32_t* __restrict__ Sq, int M, int K, int NTILES, int G,
     uint16_t* __restrict__ C, int N, int vec_out) {
-  static_assert(KPW % 4 == 0 && NT >= 1 && W >= 1 && W <= 16 && !(FQ && H8), "stream variant");
+  static_assert(KPW % 4 == 0 && NT >= 1 && W >= 1 && W <= 16, "stream variant");
   const int KT = K / kKTile, KG = KT / kKGroup;  // K % 512 == 0
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -90,26 +75,10 @@ __global__ __launch_bounds__(W * 64) void gemm_stream(
   // ---- 1. activation fragments of k-tiles kr0.. (L2): token lane % 16, two 16-byte runs.
   //         Tokens past M fall outside the buffer and read as zero; a k-tile past the wave's
   //         range re-reads the row's last k-tile (clamped in scalar arithmetic), which only ever
-  //         meets zero weights. FQ: the bf16 rows of the wave's k-range go to its LDS staging
-  //         area instead, 8 tokens x 64 elements per load; tokens past M read zero ----
+  //         meets zero weights ----
   const int m = lane & 15, g = lane >> 4;
   v4i xlo[KPW], xhi[KPW];
-  uint8_t* const stage = lds + wave * KPW * 2048;
-  if constexpr (FQ) {
-    const auto x_src = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, (long)M * lda * 2,
-                                                         kBufferWord3);
-    const int t = lane >> 3, slot = lane & 7, c = slot ^ t;
-#pragma unroll
-    for (int j = 0; j < 2 * KPW; ++j) {
-      // segment j of the wave's range; k-tiles past K (a range shorter than KPW) read zero
-      const int k = kr0 * kKTile + 64 * j + 8 * c;
-      const int off = k < K ? t * lda * 2 + 2 * k : 0x7FFFFFF0;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(x_src, (lds_ptr_t)(stage + j * 1024), 16, off,
-                                               0, 0, 0);
-    }
-    __builtin_amdgcn_sched_barrier(0);           // the staging copies go out first: the wait
-                                                 // below counts the loads issued after them
-  } else if constexpr (H8) {
+  if constexpr (H8) {
     const auto a_src = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, M * K, kBufferWord3);
 #pragma unroll
     for (int u = 0; u < KPW; ++u) {
@@ -158,70 +127,7 @@ __global__ __launch_bounds__(W * 64) void gemm_stream(
             w_src[t], (kr0 + u) * kGranuleBytes + lane * 16, 0, kBufferNT);
   }
   float tok_scale;
-  if constexpr (FQ) {
-    __builtin_amdgcn_sched_barrier(0);           // every load above is issued before any wait
-    // ---- 1b. amax of the wave's range per token (lanes 8 t .. 8 t + 7: token t), then the row
-    //          amax over the waves, the scale and the codes, as the plain quantizer computes
-    //          them ----
-    wait_vm<NT * KPW + NT * (KPW / 4)>();         // this wave's staging copies have landed
-    asm volatile("" ::: "memory");
-    uint32_t* const amax_w = reinterpret_cast<uint32_t*>(lds + W * KPW * 2048);
-    {
-      const int t = lane >> 3, slot = lane & 7;
-      uint32_t am = 0;
-#pragma unroll
-      for (int j = 0; j < 2 * KPW; ++j)
-        am = max(am, fp8::abs_bits_max8(
-                         *reinterpret_cast<const uint4*>(stage + j * 1024 + 16 * (8 * t + slot))));
-#pragma unroll
-      for (int o = 1; o < 8; o <<= 1) am = max(am, (uint32_t)__shfl_xor((int)am, o, 64));
-      if (slot == 0) amax_w[wave * 8 + t] = am;
-    }
-    lds_barrier();
-    // the scales: lanes 0..7 of every wave take token lane's row amax over the waves and write
-    // its scale and reciprocal next to the wave's maxima (read back by this wave only)
-    float* const sc_w = reinterpret_cast<float*>(amax_w + W * 8) + wave * 16;
-    if (lane < 8) {
-      uint32_t am = 0;
-#pragma unroll
-      for (int w = 0; w < W; ++w) am = max(am, amax_w[w * 8 + lane]);
-      const float sc = fp8::row_scale(am);
-      sc_w[lane] = sc;
-      sc_w[8 + lane] = 1.0f / sc;
-    }
-    __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0): the wave's scales are written
-    // Codes of the live chunks only (tokens < M; 16 KPW chunks a token), one 16-byte chunk per
-    // lane per step, written as the fragment reads want them: half h of k-tile u holds lane
-    // group g's 16 bytes of token t at ((2u + h) * 4 + g) * 8 + t (16-byte units). Step i reads
-    // staged segments >= 8 i / M and writes into segments < 8 (i + 1) / M, which every lane of
-    // the wave has read in earlier steps (or in this one, before it writes): the codes can
-    // overwrite the staging area in place.
-    const int live_chunks = M * 16 * KPW;
-    for (int ci = lane; ci < ((live_chunks + 63) & ~63); ci += 64) {
-      const bool in = ci < live_chunks;
-      const int t = in ? ci % M : 0, qq = in ? ci / M : 0;
-      const int seg = qq >> 3, c = qq & 7;
-      const uint4 v = *reinterpret_cast<const uint4*>(stage + stage_off<KPW>(seg, t, c));
-      const float sc = sc_w[t], rcp = sc_w[8 + t];
-      __builtin_amdgcn_s_waitcnt(0xC07F);        // every lane's chunk is read before any write
-      const uint2 q = fp8::quant8_any_scale(v, sc, rcp);
-      if (in)
-        *reinterpret_cast<uint2*>(stage + ((seg * 4 + (c >> 1)) * 8 + t) * 16 + 8 * (c & 1)) = q;
-    }
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    const int tm = m & 7;                        // lanes of tokens 8..15 mirror 0..7, then zero
-    const bool live = m < M;
-#pragma unroll
-    for (int u = 0; u < KPW; ++u) {
-      const v4i lo = *reinterpret_cast<const v4i*>(stage + (((2 * u) * 4 + g) * 8 + tm) * 16);
-      const v4i hi = *reinterpret_cast<const v4i*>(stage + (((2 * u + 1) * 4 + g) * 8 + tm) * 16);
-      xlo[u] = live ? lo : v4i{0, 0, 0, 0};
-      xhi[u] = live ? hi : v4i{0, 0, 0, 0};
-    }
-    const float sc = sc_w[tm];
-    tok_scale = sc;
-    lds_barrier();                               // the staging area is free for the reduction
-  } else {
+  {
     // the epilogue's per-token scale, last: it is needed last
     const auto as_src = __builtin_amdgcn_make_buffer_rsrc((void*)As, 0, M * 4, kBufferWord3);
     tok_scale = __builtin_bit_cast(
@@ -266,6 +172,185 @@ __global__ __launch_bounds__(W * 64) void gemm_stream(
   }
 }
 
+// The whole linear in one launch (bf16 activations, M <= 8): the W weight waves stream the GEMM
+// as gemm_stream does, without loading activations, while the other Q = 16 - W waves of the
+// workgroup quantize the bf16 rows into LDS, each a 1/Q column range of every row. Nothing
+// couples the weight waves to each other before the final reduction: each issues all its scale
+// and weight loads, then waits until the quantizing waves have all counted themselves done (long
+// before, the rows being small), reads its fragments from LDS and multiplies as its granules land.
+// The quantizing waves meet once, to take each row's amax over their partial maxima (a counter in
+// LDS). The codes come from the plain quantizer's steps (row amax, row_scale, the Markstein-
+// corrected quotient), so the output equals quantizer + GEMM bit for bit.
+// LDS: the codes [k-tile][half][lane group][8 tokens][16 B] (KT KiB), then 8 token scales, two
+// counters, Q x 8 partial maxima (512 B in all), then the partial sums. X is bf16 [M, ldx], 16-byte
+// aligned rows; the host requires M <= 8, W <= 12, K % 512 == 0 and 16 ldx < 2^31.
+constexpr int kFqWaves = 16;           // weight waves + quantizing waves
+constexpr int kFqSpin = 1 << 20;       // s_sleep(2) rounds a wave waits at most (~0.1 s)
+constexpr int kFqHeader = 512;         // scales, counters, partial maxima
+
+// the counter reaches `target` (a wave-uniform wait; bounded, so it always ends)
+__device__ __forceinline__ void fq_wait(int* counter, int target) {
+  for (int it = 0; it < kFqSpin; ++it) {
+    const int n = __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (__builtin_amdgcn_readfirstlane(n) >= target) break;
+    __builtin_amdgcn_s_sleep(2);
+  }
+  asm volatile("" ::: "memory");                 // the reads after the wait stay after it
+}
+
+// count this wave done after its LDS writes have landed: LDS serves one wave's operations in
+// order, so a wave that sees the count and then reads sees the writes (relaxed atomics and
+// compiler barriers: no fence, which would also wait for the weight loads in flight)
+__device__ __forceinline__ void fq_signal(int* counter) {
+  __builtin_amdgcn_s_waitcnt(0xC07F);            // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  if ((threadIdx.x & 63) == 0)
+    __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+template <int NT, int KPW, int W>
+__global__ __launch_bounds__(kFqWaves * 64) void gemm_stream_fq(
+    const uint8_t* __restrict__ X, const uint8_t* __restrict__ Wq, const uint32_t* __restrict__ Sq,
+    int M, int K, int NTILES, int G, int ldx, uint16_t* __restrict__ C, int N, int vec_out) {
+  constexpr int Q = kFqWaves - W;                // quantizing waves
+  static_assert(KPW % 4 == 0 && NT >= 1 && W >= 1 && Q >= 4 && Q <= 8, "fq variant");
+  const int KT = K / kKTile, KG = KT / kKGroup;  // K % 512 == 0
+  extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+  uint8_t* const codes = lds;
+  float* const tsc = reinterpret_cast<float*>(lds + KT * 1024);
+  int* const cnt = reinterpret_cast<int*>(tsc + 8);         // [0]: maxima posted, [1]: codes done
+  uint32_t* const pam = reinterpret_cast<uint32_t*>(cnt + 2);  // [Q][8] partial maxima
+  v4f* const red = reinterpret_cast<v4f*>(lds + KT * 1024 + kFqHeader);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int b = blockIdx.x;
+  const int ntb0 = b * NTILES / G, nth = (b + 1) * NTILES / G - ntb0;
+  if (wave >= W) {
+    // ---- quantizing wave q: chunk columns [c0, c1) of every row (a chunk: 8 elements, 16 B),
+    //      column c0 + lane + 64 i in register i. The row loads go out before the barrier below
+    //      lets the weight waves start, so they are ahead of the weight stream ----
+    constexpr int CH = (KPW * W + 4 * Q - 1) / (4 * Q);     // >= ceil(K / 8 / Q / 64)
+    const int q = wave - W, nch = K >> 3;
+    const int c0 = q * nch / Q, c1 = (q + 1) * nch / Q;
+    const auto x_src = __builtin_amdgcn_make_buffer_rsrc((void*)X, 0, M * ldx * 2, kBufferWord3);
+    uint4 v[8][CH];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      if (t >= M) break;                         // rows past M: no loads issued at all
+#pragma unroll
+      for (int i = 0; i < CH; ++i) {
+        const int c = c0 + lane + 64 * i;
+        v[t][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                      x_src, c < c1 ? t * ldx * 2 + 16 * c : 0x7FFFFFF0, 0, 0));
+      }
+    }
+    if (q == 0 && lane < 2)
+      __hip_atomic_store(&cnt[lane], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    lds_barrier();                               // (the weight waves' barrier below: one barrier)
+    // partial maxima of this column range, then each row's amax over the Q ranges
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      if (t >= M) break;
+      uint32_t am = 0;
+#pragma unroll
+      for (int i = 0; i < CH; ++i) am = max(am, fp8::abs_bits_max8(v[t][i]));
+      am = fp8::wave_max(am);
+      if (lane == 0) pam[q * 8 + t] = am;
+    }
+    fq_signal(&cnt[0]);
+    fq_wait(&cnt[0], Q);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      if (t >= M) break;
+      uint32_t am = 0;
+      for (int qq = 0; qq < Q; ++qq) am = max(am, pam[qq * 8 + t]);
+      const float sc = fp8::row_scale(am), rcp = 1.0f / sc;
+#pragma unroll
+      for (int i = 0; i < CH; ++i) {
+        const int c = c0 + lane + 64 * i, k0 = 8 * c, kb = k0 & 127;
+        if (c < c1)
+          *reinterpret_cast<uint2*>(codes + ((((k0 >> 7) * 2 + (kb >> 6)) * 4 + ((kb & 63) >> 4)) *
+                                                 8 + t) * 16 + (kb & 15)) =
+              fp8::quant8_any_scale(v[t][i], sc, rcp);
+      }
+      if (q == 0 && lane == 0) tsc[t] = sc;
+    }
+    fq_signal(&cnt[1]);
+  } else {
+    lds_barrier();                               // the quantizing waves' counters are cleared
+    const int kr0 = 4 * (KG * wave / W), kr1 = 4 * (KG * (wave + 1) / W);
+    // ---- scale dwords and granules, as in gemm_stream ----
+    uint32_t sv[NT][KPW / 4];
+    v4i wv[KPW][NT];
+    {
+      __amdgpu_buffer_rsrc_t w_src[NT], s_src[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const bool have = t < nth;
+        w_src[t] = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(Wq + (size_t)(ntb0 + t) * KT * kGranuleBytes), 0,
+            have ? kr1 * kGranuleBytes : 0, kBufferWord3);
+        s_src[t] = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(Sq + (size_t)(ntb0 + t) * KG * 64), 0, have ? (kr1 >> 2) * 256 : 0,
+            kBufferWord3);
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int qq = 0; qq < KPW / 4; ++qq)
+          sv[t][qq] = __builtin_amdgcn_raw_buffer_load_b32(
+              s_src[t], (((kr0 >> 2) + qq) * 64 + lane) * 4, 0, 0);
+#pragma unroll
+      for (int u = 0; u < KPW; ++u)
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+          wv[u][t] = __builtin_amdgcn_raw_buffer_load_b128(
+              w_src[t], (kr0 + u) * kGranuleBytes + lane * 16, 0, kBufferNT);
+    }
+    __builtin_amdgcn_sched_barrier(0);           // every load above is issued before the wait
+    fq_wait(&cnt[1], Q);                         // the quantizing waves' codes
+    // fragments: lane (m, g) of k-tile kt, token m (tokens past M and k-tiles past K: zero)
+    const int m = lane & 15, g = lane >> 4, tm = m & 7;
+    v4i xlo[KPW], xhi[KPW];
+#pragma unroll
+    for (int u = 0; u < KPW; ++u) {
+      const int kt = kr0 + u, kc = min(kt, KT - 1);
+      const bool ok = m < M && kt < KT;
+      const v4i lo = *reinterpret_cast<const v4i*>(codes + (((kc * 2) * 4 + g) * 8 + tm) * 16);
+      const v4i hi = *reinterpret_cast<const v4i*>(codes + (((kc * 2 + 1) * 4 + g) * 8 + tm) * 16);
+      xlo[u] = ok ? lo : v4i{0, 0, 0, 0};
+      xhi[u] = ok ? hi : v4i{0, 0, 0, 0};
+    }
+    v4f acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < KPW; ++u) {
+      const v8i xf = {xlo[u][0], xlo[u][1], xlo[u][2], xlo[u][3],
+                      xhi[u][0], xhi[u][1], xhi[u][2], xhi[u][3]};
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        acc[t] = mfma_w4a8(wv[u][t], xf, acc[t], sv[t][u / 4] >> (8 * (u & 3)));
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) red[(wave * NT + t) * 64 + lane] = acc[t];
+  }
+
+  // ---- the W partial sums of each n-tile, added in wave order ----
+  __syncthreads();
+  const bool vec = vec_out != 0;
+  const int m = lane & 15;
+  const float tok_scale = tsc[m & 7];
+  for (int slot = tid; slot < nth * 64; slot += kFqWaves * 64) {
+    const int t = slot >> 6;                     // slot lane == this thread's lane
+    v4f v = red[t * 64 + lane];
+#pragma unroll 4
+    for (int w = 1; w < W; ++w) v += red[(w * NT + t) * 64 + lane];
+    const int n = (ntb0 + t) * kNTile + 4 * (lane >> 4);
+    if (m < M) store_out4(C, N, m, n, N, v, tok_scale, vec);
+  }
+}
+
 // (NT, KPW, W): NT * KPW granules and 2 KPW activation runs per wave in registers; W waves at
 // most 4 per SIMD. Chosen per shape by the host: the fewest granules per wave, then the fewest
 // n-tile slots, then the fewest waves.
@@ -294,13 +379,10 @@ int stream_grid(int N, int cus) {
 
 size_t stream_lds_bytes(int variant, int M, int K, bool fused) {
   (void)M;
-  (void)K;
   const StreamCfg c = kStream[variant];
   const size_t red = (size_t)c.waves * c.nt * 64 * sizeof(v4f);
-  // fused: the staging area (2 KiB per k-tile per wave), then the waves' token maxima and their
-  // scales; the final reduction reuses the staging area
-  const size_t stage = (size_t)c.waves * c.kpw * 2048 + (size_t)c.waves * (8 + 16) * 4;
-  return fused && stage > red ? stage : red;
+  // fused: the codes (1 KiB per k-tile), the scales, counters and maxima, then the partial sums
+  return fused ? (size_t)(K / kKTile) * 1024 + kFqHeader + red : red;
 }
 
 // Granules the busiest wave of a variant streams for this shape (0: the variant cannot serve it).
@@ -323,16 +405,21 @@ bool stream_fits(int variant, int M, int N, int K, int cus, size_t lds_limit) {
   return small && stream_lds_bytes(variant, M, K, false) <= lds_limit;
 }
 
-// Every workgroup quantizes the whole activation, M x K elements, so the one-launch form pays off
-// only for few rows: measured on MI355X over the four Qwen3.8-27B linear shapes, it beats the
-// quantizer + GEMM pair by 0.3-1.1 us at M = 1 and by 0.3-0.6 us at M = 2 with 4 k-tiles per wave,
-// and loses from M x KPW = 12 on (M = 2 on down's 8 k-tiles: 10.9 against 10.2 us).
+// The one-launch linear where it pays. Every workgroup quantizes all M x K elements, which stays
+// hidden behind its weight waves' loads only while the rows are few against the granules a weight
+// wave streams. Measured on MI355X over the four Qwen3.8-27B linear shapes (us, one launch against
+// quantizer + GEMM): M = 1 qkv 7.23 / 9.05, o_proj 5.64 / 7.68, gate_up 10.22 / 11.85, down 6.56 /
+// 9.18; M = 2 7.28 / 9.27, 6.21 / 7.81, 10.25 / 12.03, 6.97 / 9.41; M = 4 wins with 3 or more
+// n-tiles per workgroup (qkv 8.61 / 9.18, gate_up 10.25 / 12.12) and loses with 2 (o_proj 8.87 /
+// 8.14, down 10.2 / 9.74); M = 8 loses everywhere (13.3-16.7 against 8.5-12.5). Variants also need
+// room for the quantizing waves (W <= 12) and registers for their granules (NT KPW <= 24), 16-byte
+// rows, every row offset in 32 bits, and the codes and partial sums within the LDS.
 bool stream_linear_fits(int variant, int M, int N, int K, long ldx, int cus, size_t lds_limit) {
   const StreamCfg c = kStream[variant];
-  if (M * c.kpw > 8) return false;
-  return stream_fits(variant, M, N, K, cus, lds_limit) && ldx >= K &&
-         ldx % 8 == 0 && 16L * ldx < (1L << 31) &&   // row offsets of all 8 staged rows
-         stream_lds_bytes(variant, M, K, true) <= lds_limit;
+  if (M < 1 || !(M <= 2 || (M <= 4 && c.nt >= 3))) return false;
+  return c.waves <= kFqWaves - 4 && c.nt * c.kpw <= 24 &&
+         stream_fits(variant, M, N, K, cus, lds_limit) && ldx >= K && ldx % 8 == 0 &&
+         16L * ldx < (1L << 31) && stream_lds_bytes(variant, M, K, true) <= lds_limit;
 }
 
 // fused: g.a is the bf16 activation with row stride lda elements (the quantizer runs in the
@@ -344,28 +431,39 @@ hipError_t launch_stream(const GemmArgs& g, int variant, int cus, bool fused, lo
   const dim3 grid(stream_grid(g.N, cus)), block(kStream[variant].waves * 64);
   const size_t lds = stream_lds_bytes(variant, g.M, g.K, fused);
   int idx = 0;
-#define W4A8_STREAM_GO(nt, kpw, w, fq, h8)                                                       \
+#define W4A8_STREAM_ATTR(kern)                                                                   \
+  if (lds > 64 * 1024) {                                                                         \
+    const hipError_t e = hipFuncSetAttribute((const void*)kern,                                  \
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,         \
+                                             (int)lds);                                          \
+    if (e != hipSuccess) return e;                                                               \
+  }
+#define W4A8_STREAM_GO(nt, kpw, w, h8)                                                           \
   {                                                                                              \
-    if (lds > 64 * 1024) {                                                                       \
-      const hipError_t e = hipFuncSetAttribute((const void*)gemm_stream<nt, kpw, w, fq, h8>,     \
-                                               hipFuncAttributeMaxDynamicSharedMemorySize,       \
-                                               (int)lds);                                        \
-      if (e != hipSuccess) return e;                                                             \
-    }                                                                                            \
-    hipLaunchKernelGGL((gemm_stream<nt, kpw, w, fq, h8>), grid, block, lds, stream, g.a,         \
-                       g.a_scale, g.wq, g.sq, g.M, g.K, NTILES, (int)grid.x, (int)lda, g.c, g.N, \
-                       vec_out);                                                                 \
+    W4A8_STREAM_ATTR((gemm_stream<nt, kpw, w, h8>))                                              \
+    hipLaunchKernelGGL((gemm_stream<nt, kpw, w, h8>), grid, block, lds, stream, g.a, g.a_scale,  \
+                       g.wq, g.sq, g.M, g.K, NTILES, (int)grid.x, g.c, g.N, vec_out);           \
     return hipGetLastError();                                                                    \
   }
 #define W4A8_STREAM_LAUNCH(nt, kpw, w)                                                           \
   if (idx++ == variant) {                                                                        \
-    if (fused) W4A8_STREAM_GO(nt, kpw, w, true, false)                                           \
-    if (g.M <= 8) W4A8_STREAM_GO(nt, kpw, w, false, true)                                        \
-    W4A8_STREAM_GO(nt, kpw, w, false, false)                                                     \
+    if constexpr (w <= kFqWaves - 4) {                                                           \
+      if (fused) {                                                                               \
+        W4A8_STREAM_ATTR((gemm_stream_fq<nt, kpw, w>))                                           \
+        hipLaunchKernelGGL((gemm_stream_fq<nt, kpw, w>), grid, dim3(kFqWaves * 64), lds, stream,  \
+                           g.a, g.wq, g.sq, g.M, g.K, NTILES, (int)grid.x,                       \
+                           (int)lda, g.c, g.N, vec_out);                                         \
+        return hipGetLastError();                                                                \
+      }                                                                                          \
+    }                                                                                            \
+    if (fused) return hipErrorInvalidValue;                                                      \
+    if (g.M <= 8) W4A8_STREAM_GO(nt, kpw, w, true)                                               \
+    W4A8_STREAM_GO(nt, kpw, w, false)                                                            \
   }
   W4A8_STREAM_TABLE(W4A8_STREAM_LAUNCH)
 #undef W4A8_STREAM_LAUNCH
 #undef W4A8_STREAM_GO
+#undef W4A8_STREAM_ATTR
   return hipErrorInvalidValue;
 }
 

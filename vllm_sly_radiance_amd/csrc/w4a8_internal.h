@@ -139,7 +139,8 @@ size_t stream_lds_bytes(int variant, int M, int K, bool fused);
 int stream_granules(int variant, int N, int K, int cus);
 bool stream_fits(int variant, int M, int N, int K, int cus, size_t lds_limit);
 // The variant can also run the whole linear (bf16 activations with row stride ldx elements,
-// quantized in the kernel) and it pays: M x KPW <= 8, 16-byte rows, the staging area fits the LDS.
+// quantized in the kernel) and it pays: few rows against the weight waves' granules (M <= 2, or
+// M <= 4 with 3 or more n-tiles per workgroup), room for the quantizing waves, 16-byte rows, LDS.
 bool stream_linear_fits(int variant, int M, int N, int K, long ldx, int cus, size_t lds_limit);
 // fused: g.a is bf16 [M, K] with row stride lda elements and g.a_scale is unused
 hipError_t launch_stream(const GemmArgs& g, int variant, int cus, bool fused, long lda,
