@@ -6,7 +6,7 @@ import torch
 
 from oracle import mxfp4_oracle as O
 from tests._check import assert_gemm_close, bf16_dev, host_u16, host_u8, to_dev
-from vllm_sly_radiance_amd import radiance_mxfp4 as R
+from vllm_sly_radiance_amd import _native, radiance_mxfp4 as R
 from vllm_sly_radiance_amd import synthetic
 
 pytestmark = pytest.mark.gpu
@@ -87,14 +87,18 @@ def test_op_is_one_opaque_node_under_compile(kernel):
     assert torch.equal(f(x), kernel.apply_weights(layer, x))
 
 
-def test_hip_graph_capture_and_replay(kernel):
+@pytest.mark.parametrize("M", [1, 3, 8])
+def test_hip_graph_capture_and_replay(kernel, M):
     """The op allocates nothing natively and launches on the current stream, so it captures into a
-    HIP graph; every replay (with eager work and syncs in between) must match the eager result."""
+    HIP graph; every replay (with eager work and syncs in between) must match the eager result.
+    M = 1 and 3 run as one launch (the quantizing waves' LDS counters start from zero in every
+    replay), M = 8 as the quantizer and the GEMM."""
     N, K = 17408, 5120
+    assert _native.linear_fused(M, N, K, K) == (M <= 4)
     w, ws = synthetic.weights(N, K, seed=10)
     layer = Layer(w, ws)
     kernel.process_weights_after_loading(layer)
-    x = bf16_dev(synthetic.activations(8, K, seed=11))
+    x = bf16_dev(synthetic.activations(M, K, seed=11))
     eager = kernel.apply_weights(layer, x)
     torch.cuda.synchronize()
     s = torch.cuda.Stream()
