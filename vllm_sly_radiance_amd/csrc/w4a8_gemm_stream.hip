@@ -181,21 +181,27 @@ __global__ __launch_bounds__(W * 64) void gemm_stream(
 // The quantizing waves meet once, to take each row's amax over their partial maxima (a counter in
 // LDS). The codes come from the plain quantizer's steps (row amax, row_scale, the Markstein-
 // corrected quotient), so the output equals quantizer + GEMM bit for bit.
-// LDS: the codes [k-tile][half][lane group][8 tokens][16 B] (KT KiB), then 8 token scales, two
+// LDS: the codes [k-tile][half][lane group][8 tokens][16 B] (KT KiB), then 8 token scales, three
 // counters, Q x 8 partial maxima (512 B in all), then the partial sums. X is bf16 [M, ldx], 16-byte
 // aligned rows; the host requires M <= 8, W <= 12, K % 512 == 0 and 16 ldx < 2^31.
 constexpr int kFqWaves = 16;           // weight waves + quantizing waves
 constexpr int kFqSpin = 1 << 20;       // s_sleep(2) rounds a wave waits at most (~0.1 s)
 constexpr int kFqHeader = 512;         // scales, counters, partial maxima
 
-// the counter reaches `target` (a wave-uniform wait; bounded, so it always ends)
-__device__ __forceinline__ void fq_wait(int* counter, int target) {
+// the counter reaches `target` (a wave-uniform wait; bounded, so it always ends). A wait that
+// runs out marks the workgroup failed in `err`: its outputs are then NaN, never plausible numbers.
+__device__ __forceinline__ void fq_wait(int* counter, int target, int* err) {
   for (int it = 0; it < kFqSpin; ++it) {
     const int n = __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    if (__builtin_amdgcn_readfirstlane(n) >= target) break;
+    if (__builtin_amdgcn_readfirstlane(n) >= target) {
+      asm volatile("" ::: "memory");             // the reads after the wait stay after it
+      return;
+    }
     __builtin_amdgcn_s_sleep(2);
   }
-  asm volatile("" ::: "memory");                 // the reads after the wait stay after it
+  if ((threadIdx.x & 63) == 0)
+    __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  asm volatile("" ::: "memory");
 }
 
 // count this wave done after its LDS writes have landed: LDS serves one wave's operations in
@@ -218,8 +224,9 @@ __global__ __launch_bounds__(kFqWaves * 64) void gemm_stream_fq(
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
   uint8_t* const codes = lds;
   float* const tsc = reinterpret_cast<float*>(lds + KT * 1024);
-  int* const cnt = reinterpret_cast<int*>(tsc + 8);         // [0]: maxima posted, [1]: codes done
-  uint32_t* const pam = reinterpret_cast<uint32_t*>(cnt + 2);  // [Q][8] partial maxima
+  // cnt[0]: maxima posted, [1]: codes done, [2]: a wait ran out
+  int* const cnt = reinterpret_cast<int*>(tsc + 8);
+  uint32_t* const pam = reinterpret_cast<uint32_t*>(cnt + 3);  // [Q][8] partial maxima
   v4f* const red = reinterpret_cast<v4f*>(lds + KT * 1024 + kFqHeader);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -244,7 +251,7 @@ __global__ __launch_bounds__(kFqWaves * 64) void gemm_stream_fq(
                       x_src, c < c1 ? t * ldx * 2 + 16 * c : 0x7FFFFFF0, 0, 0));
       }
     }
-    if (q == 0 && lane < 2)
+    if (q == 0 && lane < 3)
       __hip_atomic_store(&cnt[lane], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     lds_barrier();                               // (the weight waves' barrier below: one barrier)
     // partial maxima of this column range, then each row's amax over the Q ranges
@@ -258,7 +265,7 @@ __global__ __launch_bounds__(kFqWaves * 64) void gemm_stream_fq(
       if (lane == 0) pam[q * 8 + t] = am;
     }
     fq_signal(&cnt[0]);
-    fq_wait(&cnt[0], Q);
+    fq_wait(&cnt[0], Q, &cnt[2]);
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
       if (t >= M) break;
@@ -308,7 +315,7 @@ __global__ __launch_bounds__(kFqWaves * 64) void gemm_stream_fq(
               w_src[t], (kr0 + u) * kGranuleBytes + lane * 16, 0, kBufferNT);
     }
     __builtin_amdgcn_sched_barrier(0);           // every load above is issued before the wait
-    fq_wait(&cnt[1], Q);                         // the quantizing waves' codes
+    fq_wait(&cnt[1], Q, &cnt[2]);                // the quantizing waves' codes
     // fragments: lane (m, g) of k-tile kt, token m (tokens past M and k-tiles past K: zero)
     const int m = lane & 15, g = lane >> 4, tm = m & 7;
     v4i xlo[KPW], xhi[KPW];
@@ -340,7 +347,7 @@ __global__ __launch_bounds__(kFqWaves * 64) void gemm_stream_fq(
   __syncthreads();
   const bool vec = vec_out != 0;
   const int m = lane & 15;
-  const float tok_scale = tsc[m & 7];
+  const float tok_scale = cnt[2] ? __builtin_nanf("") : tsc[m & 7];
   for (int slot = tid; slot < nth * 64; slot += kFqWaves * 64) {
     const int t = slot >> 6;                     // slot lane == this thread's lane
     v4f v = red[t * 64 + lane];
