@@ -170,11 +170,11 @@ int w4a8_workspace_bytes(int max_m, int max_n, size_t* partial_bytes, size_t* co
 
 /* Quantize + GEMM in one call: the body of radiance::mxfp4_linear (sly/mxfp4/radiance_mxfp4.py:
  * 644-816) minus the output allocation, which stays with the caller (torch.empty at
- * sly/mxfp4/radiance_mxfp4.py:737). Where w4a8_linear_fused says so (M <= 2, and M <= 4 on the
- * wider shapes; x 16-byte aligned, ldx % 8 == 0) it is one launch: waves of the streaming GEMM's
- * workgroups quantize the rows into LDS while the others stream the weights;
- * otherwise the quantizer and the GEMM, two launches on the stream. The output is the same bits
- * either way. q [M, K] and scale [M] are caller workspace (not written by the one-launch form). */
+ * sly/mxfp4/radiance_mxfp4.py:737). Where w4a8_linear_fused says so (M <= 2, and M <= 4 where the
+ * plan leaves the quantizing waves little work; x 16-byte aligned, ldx % 8 == 0) it is one launch:
+ * waves of the streaming GEMM's workgroups quantize the rows into LDS while the others stream the
+ * weights; otherwise the quantizer and the GEMM, two launches on the stream. The output is the
+ * same bits either way. q [M, K] and scale [M] are caller workspace (not written by the one-launch form). */
 int w4a8_linear(const void* x, long ldx, void* q, float* scale, const void* wq, const void* sq,
                 void* c, int M, int N, int K, void* stream);
 

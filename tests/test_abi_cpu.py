@@ -123,11 +123,13 @@ def test_plan_bands(lib):
 
 def test_one_launch_linear_where_it_pays(lib):
     """w4a8_linear runs as one launch (quantizing waves beside the streaming GEMM's weight waves)
-    at M <= 2, and up to M = 4 where a workgroup holds 3 or more n-tiles; never on 16-wave
-    variants (no room for the quantizing waves), never for rows that are not 16-byte chunks."""
+    at M <= 2, and up to M = 4 where a workgroup holds 3 or more n-tiles or a quantizing wave
+    handles at most 4 row chunks per lane (o_proj's 4-wave plan leaves 12 quantizing waves; down's
+    6-wave plan leaves 10, 7 chunks per lane at M = 3..4); never on 16-wave variants (no room for
+    the quantizing waves), never for rows that are not 16-byte chunks."""
     f = lib.w4a8_linear_fused
-    for N, K, up_to in [(17408, 5120, 4), (10240, 5120, 4), (5120, 6144, 2), (5120, 8704, 2),
-                        (5120, 5120, 2), (2048, 1024, 0), (1040, 512, 0)]:
+    for N, K, up_to in [(17408, 5120, 4), (10240, 5120, 4), (5120, 6144, 4), (5120, 8704, 2),
+                        (5120, 5120, 4), (2048, 1024, 0), (1040, 512, 0)]:
         assert [f(M, N, K, K) for M in range(1, 10)] == [int(M <= up_to) for M in range(1, 10)], \
             (N, K)
     assert f(1, 17408, 5120, 5120 + 72) == 1

@@ -58,9 +58,10 @@ def strided(x_bits, ldx):
 def test_one_launch_equals_quantizer_then_gemm(gpu_lib, N, K):
     w, ws = synthetic.weights(N, K, seed=N + K)
     wq, sq = repacked(w, ws)
-    # one launch at M <= 2, and up to M = 4 with 3 or more n-tiles per workgroup (qkv, gate_up);
-    # the small shapes plan variants of 16 waves, with no room for the quantizing waves
-    fused_up_to = {(17408, 5120): 4, (10240, 5120): 4, (5120, 6144): 2, (5120, 8704): 2}
+    # one launch at M <= 2, and up to M = 4 with 3 or more n-tiles per workgroup (qkv, gate_up)
+    # or at most 4 row chunks per lane of a quantizing wave (o_proj); the small shapes plan
+    # variants of 16 waves, with no room for the quantizing waves
+    fused_up_to = {(17408, 5120): 4, (10240, 5120): 4, (5120, 6144): 4, (5120, 8704): 2}
     assert [_native.linear_fused(M, N, K, K) for M in range(1, 9)] == \
         [M <= fused_up_to.get((N, K), 0) for M in range(1, 9)]
     for M in range(1, 9):

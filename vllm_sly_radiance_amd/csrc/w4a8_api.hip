@@ -141,15 +141,30 @@ bool scratch_fits(const Scratch& s, int variant, int N, int split_k) {
 
 Scratch registered_scratch(int dev) { return dev >= 0 ? g_scratch[dev] : Scratch{}; }
 
-// The stream variant that serves (M, N, K) with the fewest granules on its busiest wave, then the
-// fewest n-tile slots, then the fewest waves.
+// The stream variant for (M, N, K). When the workgroups cover at least half the CUs (the weight
+// stream is the whole cost), the fewest waves whose loads fit 160 registers (4 per granule, 4 per
+// activation k-tile at M <= 8, else 8) and that leave no wave without a k-group of its own, then
+// the fewest registers: every wave issues all its loads at once whatever the wave count, so fewer
+// waves move the same bytes with fewer partial sums to add and fewer waves to launch. Measured on
+// MI355X against the fewest-granules rule below (us,
+// GEMM alone, M = 1 / 8 / 16): qkv 6.58 / 6.96 / 8.01 -> 6.30 / 6.86 / 7.58 (3 x 8 x 5 waves),
+// o_proj 5.11 / 5.82 -> 4.82 / 5.50 (2 x 12 x 4), 7.01 -> 6.67 at M = 16 (2 x 8 x 6), down
+// 6.19 / 7.27 -> 6.13 / 7.14 (2 x 12 x 6; at M = 16 the 2 x 12 x 6 loses, 9.06 against 8.90, and
+// the budget keeps 2 x 8 x 9); gate_up keeps 5 x 4 x 10 (5 x 8 x 5 was within 1 %). Otherwise the
+// fewest granules on the busiest wave, then the fewest n-tile slots, then the fewest waves.
 int find_stream(int M, int N, int K, int dev) {
   const DeviceInfo d = device_info(dev);
-  int best = -1, best_key = 0;
+  const bool wide = 2 * stream_grid(N, d.cus) >= d.cus;
+  int best = -1;
+  long best_key = 0;
   for (int v = 0; v < stream_variant_count(); ++v) {
     if (!stream_fits(v, M, N, K, d.cus, d.lds)) continue;
     const StreamCfg c = stream_variant(v);
-    const int key = (stream_granules(v, N, K, d.cus) * 64 + c.nt) * 64 + c.waves;
+    const int regs = 4 * c.nt * c.kpw + (M <= 8 ? 4 : 8) * c.kpw;
+    const long key =
+        wide && regs <= 160 && c.waves <= K / kKAlign
+            ? ((long)c.waves * 4096 + regs) * 64 + c.nt
+            : (1L << 40) + ((long)stream_granules(v, N, K, d.cus) * 64 + c.nt) * 64 + c.waves;
     if (best < 0 || key < best_key) best = v, best_key = key;
   }
   return best;

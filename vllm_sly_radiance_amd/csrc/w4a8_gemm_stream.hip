@@ -183,7 +183,7 @@ __global__ __launch_bounds__(W * 64) void gemm_stream(
 // corrected quotient), so the output equals quantizer + GEMM bit for bit.
 // LDS: the codes [k-tile][half][lane group][8 tokens][16 B] (KT KiB), then 8 token scales, three
 // counters, Q x 8 partial maxima (512 B in all), then the partial sums. X is bf16 [M, ldx], 16-byte
-// aligned rows; the host requires M <= 8, W <= 12, K % 512 == 0 and 16 ldx < 2^31.
+// aligned rows; the host requires M <= 8, 4 <= W <= 12, K % 512 == 0 and 16 ldx < 2^31.
 constexpr int kFqWaves = 16;           // weight waves + quantizing waves
 constexpr int kFqSpin = 1 << 20;       // s_sleep(2) rounds a wave waits at most (~0.1 s)
 constexpr int kFqHeader = 512;         // scales, counters, partial maxima
@@ -219,7 +219,7 @@ __global__ __launch_bounds__(kFqWaves * 64) void gemm_stream_fq(
     const uint8_t* __restrict__ X, const uint8_t* __restrict__ Wq, const uint32_t* __restrict__ Sq,
     int M, int K, int NTILES, int G, int ldx, uint16_t* __restrict__ C, int N, int vec_out) {
   constexpr int Q = kFqWaves - W;                // quantizing waves
-  static_assert(KPW % 4 == 0 && NT >= 1 && W >= 1 && Q >= 4 && Q <= 8, "fq variant");
+  static_assert(KPW % 4 == 0 && NT >= 1 && W >= 1 && Q >= 4 && Q <= 12, "fq variant");
   const int KT = K / kKTile, KG = KT / kKGroup;  // K % 512 == 0
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
   uint8_t* const codes = lds;
@@ -359,11 +359,12 @@ __global__ __launch_bounds__(kFqWaves * 64) void gemm_stream_fq(
 }
 
 // (NT, KPW, W): NT * KPW granules and 2 KPW activation runs per wave in registers; W waves at
-// most 4 per SIMD. Chosen per shape by the host: the fewest granules per wave, then the fewest
-// n-tile slots, then the fewest waves.
+// most 4 per SIMD. Chosen per shape by the host (find_stream): on shapes that fill the chip the
+// fewest waves whose loads fit the register budget, otherwise the fewest granules per wave.
 #define W4A8_STREAM_TABLE(X)                                                                      \
   X(1, 4, 16) X(1, 8, 16) X(2, 4, 10) X(2, 4, 12) X(2, 4, 16) X(2, 8, 9) X(3, 4, 10)              \
-  X(3, 4, 12) X(4, 4, 10) X(5, 4, 10) X(6, 4, 8) X(8, 4, 8)
+  X(3, 4, 12) X(4, 4, 10) X(5, 4, 10) X(6, 4, 8) X(8, 4, 8) X(3, 8, 5) X(2, 8, 6) X(2, 12, 6)      \
+  X(2, 12, 4)
 
 #define W4A8_STREAM_CFG(nt, kpw, w) StreamCfg{nt, kpw, w, nt * kpw},
 constexpr StreamCfg kStream[] = {W4A8_STREAM_TABLE(W4A8_STREAM_CFG)};
@@ -414,17 +415,21 @@ bool stream_fits(int variant, int M, int N, int K, int cus, size_t lds_limit) {
 
 // The one-launch linear where it pays. Every workgroup quantizes all M x K elements, which stays
 // hidden behind its weight waves' loads only while the rows are few against the granules a weight
-// wave streams. Measured on MI355X over the four Qwen3.8-27B linear shapes (us, one launch against
-// quantizer + GEMM): M = 1 qkv 7.23 / 9.05, o_proj 5.64 / 7.68, gate_up 10.22 / 11.85, down 6.56 /
-// 9.18; M = 2 7.28 / 9.27, 6.21 / 7.81, 10.25 / 12.03, 6.97 / 9.41; M = 4 wins with 3 or more
-// n-tiles per workgroup (qkv 8.61 / 9.18, gate_up 10.25 / 12.12) and loses with 2 (o_proj 8.87 /
-// 8.14, down 10.2 / 9.74); M = 8 loses everywhere (13.3-16.7 against 8.5-12.5). Variants also need
-// room for the quantizing waves (W <= 12) and registers for their granules (NT KPW <= 24), 16-byte
+// wave streams. Measured on MI355X over the four Qwen3.8-27B linear shapes with the plan's variants
+// (us, one launch against quantizer + GEMM): M = 1 qkv 7.05 / 9.05, o_proj 5.37 / 7.68, gate_up
+// 10.33 / 11.85, down 6.44 / 9.18; M = 2 qkv 7.05, o_proj 5.71, gate_up 10.36, down 7.12 (two
+// launches 7.8-12.0); M = 4 wins with 3 or more n-tiles per workgroup (qkv 7.71 / 9.18, gate_up
+// 10.37 / 12.12) or at most 4 quantizer chunks (16 bytes of a row) per lane of a quantizing wave
+// (o_proj with 12 quantizing waves: 7.46 / 8.10), and loses otherwise (down, 7 chunks per lane:
+// 10.1 / 9.75); M = 8 loses everywhere (13.3-16.7 against 8.5-12.5). Variants also need room for
+// the quantizing waves (4 <= W <= 12) and registers for their granules (NT KPW <= 24), 16-byte
 // rows, every row offset in 32 bits, and the codes and partial sums within the LDS.
 bool stream_linear_fits(int variant, int M, int N, int K, long ldx, int cus, size_t lds_limit) {
   const StreamCfg c = kStream[variant];
-  if (M < 1 || !(M <= 2 || (M <= 4 && c.nt >= 3))) return false;
-  return c.waves <= kFqWaves - 4 && c.nt * c.kpw <= 24 &&
+  if (M < 1 || M > 4 || c.waves < 4 || c.waves > kFqWaves - 4) return false;
+  const int chunks_per_lane = ceil_div(M * (K / 8), 64 * (kFqWaves - c.waves));
+  if (M > 2 && c.nt < 3 && chunks_per_lane > 4) return false;
+  return c.nt * c.kpw <= 24 &&
          stream_fits(variant, M, N, K, cus, lds_limit) && ldx >= K && ldx % 8 == 0 &&
          16L * ldx < (1L << 31) && stream_lds_bytes(variant, M, K, true) <= lds_limit;
 }

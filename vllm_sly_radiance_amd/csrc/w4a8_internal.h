@@ -140,7 +140,8 @@ int stream_granules(int variant, int N, int K, int cus);
 bool stream_fits(int variant, int M, int N, int K, int cus, size_t lds_limit);
 // The variant can also run the whole linear (bf16 activations with row stride ldx elements,
 // quantized in the kernel) and it pays: few rows against the weight waves' granules (M <= 2, or
-// M <= 4 with 3 or more n-tiles per workgroup), room for the quantizing waves, 16-byte rows, LDS.
+// M <= 4 with 3 or more n-tiles per workgroup or at most 4 row chunks per lane of a quantizing
+// wave), room for the quantizing waves, 16-byte rows, LDS.
 bool stream_linear_fits(int variant, int M, int N, int K, long ldx, int cus, size_t lds_limit);
 // fused: g.a is bf16 [M, K] with row stride lda elements and g.a_scale is unused
 hipError_t launch_stream(const GemmArgs& g, int variant, int cus, bool fused, long lda,

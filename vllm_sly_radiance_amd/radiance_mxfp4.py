@@ -200,9 +200,9 @@ def gemm(x_fp8: torch.Tensor, x_scale: torch.Tensor, weight: torch.Tensor,
 def mxfp4_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
                  weight_ref: torch.Tensor) -> torch.Tensor:
     """bf16 x [M, K] -> bf16 [M, N]: per-token e4m3 quant + W4A8 GEMM on the current stream. At
-    M <= 2 (M <= 4 on the wider shapes) one launch quantizes beside the streaming GEMM, else two
-    launches; the bits are the same either way. N and K come from weight_ref's shape (see module
-    docstring)."""
+    M <= 2 (M <= 4 where the plan leaves its quantizing waves little work) one launch quantizes
+    beside the streaming GEMM, else two launches; the bits are the same either way. N and K come
+    from weight_ref's shape (see module docstring)."""
     STATS["calls"] += 1
     N, K = weight_ref.shape[0], weight_ref.shape[1]
     if x.dim() != 2 or x.shape[1] != K:
