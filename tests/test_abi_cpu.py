@@ -181,6 +181,24 @@ def test_plan_pipeline_depth_and_waves(lib, M, N, K, stages, waves):
     assert (c["stages"], c["waves"]) == (stages, waves)
 
 
+@pytest.mark.parametrize("M,N,K,cfg", [
+    # shapes whose workgroups cover the chip: the fewest waves whose loads fit 160 registers
+    # (4 per granule, 4 per activation k-tile at M <= 8, else 8), each wave owning a k-group
+    (1, 10240, 5120, (3, 8, 5)), (8, 10240, 5120, (3, 8, 5)), (16, 10240, 5120, (3, 8, 5)),
+    (1, 5120, 6144, (2, 12, 4)), (8, 5120, 6144, (2, 12, 4)), (16, 5120, 6144, (2, 8, 6)),
+    (1, 5120, 8704, (2, 12, 6)), (8, 5120, 8704, (2, 12, 6)), (16, 5120, 8704, (2, 8, 9)),
+    (1, 17408, 5120, (5, 4, 10)), (8, 17408, 5120, (5, 4, 10)), (16, 17408, 5120, (5, 4, 10)),
+    # narrow shapes (fewer workgroups than half the CUs) or waves without a k-group: the fewest
+    # granules on the busiest wave
+    (8, 2048, 1024, (1, 4, 16)), (8, 1040, 512, (1, 4, 16)), (8, 48, 5120, (1, 4, 16))])
+def test_plan_stream_variants(lib, M, N, K, cfg):
+    """(n-tiles per workgroup, k-tiles per wave, waves) of the stream variant the plan takes."""
+    k, v, s = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    assert lib.w4a8_plan(M, N, K, ctypes.byref(k), ctypes.byref(v), ctypes.byref(s)) == 0
+    assert k.value == 3 and s.value == 1
+    assert _native.variants(3)[v.value][:3] == cfg
+
+
 def test_variant_tables(lib):
     sk = [(lib.w4a8_variant_count(1))]
     assert sk[0] > 0 and lib.w4a8_variant_count(2) > 0 and lib.w4a8_variant_count(9) == -1
