@@ -66,8 +66,9 @@ def parse():
     ap.add_argument("--sweep-layers", type=int, default=64)
     ap.add_argument("--profile", action="store_true",
                     help="counter-run workload: the verify-GEMM graph replay, 4 launches of each "
-                         "prefill GEMM, fused producer and quantizer shape at M=4096, and one "
-                         "256 MiB device copy (the counter calibration); prints no JSON")
+                         "prefill GEMM, fused producer and quantizer shape at M=4096, 8 of each "
+                         "decode-band GEMM and M=1 linear, and one 256 MiB device copy (the "
+                         "counter calibration); prints no JSON")
     return ap.parse_args()
 
 
@@ -638,7 +639,8 @@ def profile_workload():
     graph replay: one second of warmup replays, then 64 timed launches over 16 weight copies,
     plus 64 event-bracketed single launches), each prefill GEMM (4 launches, then 4 more on
     fragment-tiled q behind its fused producer), gate_up and down
-    at M = 32 and 64 (8 launches over 4 weight copies each), each fused
+    at M = 32 and 64 (8 launches over 4 weight copies each), the four linears of the M = 1 layer
+    set on bf16 activations as the op runs them (8 launches over 4 weight copies each), each fused
     producer and the quantizer at M = 4096 (4 launches over 2 input copies each) and a plain
     256 MiB device copy
     (torch's copy kernel), whose FETCH_SIZE / WRITE_SIZE readings calibrate the counters: a copy
@@ -670,6 +672,13 @@ def profile_workload():
             g.launch(i % 4, st.cuda_stream)
         torch.cuda.synchronize()
         del g
+    for _, N, K in LAYER_M1:                       # the M = 1 layer set as the op runs it
+        g = Gemm(1, N, K, 4, seed=3)
+        lin = Linear(g)
+        for i in range(8):
+            lin.launch(i % 4, st.cuda_stream)
+        torch.cuda.synchronize()
+        del g, lin
     for kind, N in PRODUCERS:                      # the fused producers at M = 4096
         g = Producer(kind, 4096, N, 2, seed=21)
         for i in range(4):
