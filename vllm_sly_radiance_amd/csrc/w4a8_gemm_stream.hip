@@ -459,7 +459,7 @@ hipError_t launch_stream(const GemmArgs& g, int variant, int cus, bool fused, lo
   }
 #define W4A8_STREAM_LAUNCH(nt, kpw, w)                                                           \
   if (idx++ == variant) {                                                                        \
-    if constexpr (w <= kFqWaves - 4) {                                                           \
+    if constexpr (w >= 4 && w <= kFqWaves - 4 && nt * kpw <= 24) {                               \
       if (fused) {                                                                               \
         W4A8_STREAM_ATTR((gemm_stream_fq<nt, kpw, w>))                                           \
         hipLaunchKernelGGL((gemm_stream_fq<nt, kpw, w>), grid, dim3(kFqWaves * 64), lds, stream,  \
