@@ -140,17 +140,19 @@ def per_launch_us(g, n, stream_obj):
 WARM_SECONDS = 1.0
 
 
-def graph_timed(g, steps, warmup, warm_seconds=WARM_SECONDS):
+def graph_timed(g, steps, warmup, warm_seconds=WARM_SECONDS, direct=False):
     """Time exactly `steps` launches after `warmup` untimed ones, on one side stream.
 
     The timed launches are one HIP graph of `steps` launches (weight copies rotating), replayed
-    once between two events on the stream the kernels run on. Before the warmup launches the same
-    graph replays for at least `warm_seconds` (MI355X raises its clocks over the first few hundred
-    milliseconds of load; a cold GEMM reads up to 20 % slow), reported separately as the clock
-    warm-up. Its last four replays, the warmup launches, the first event and the timed replay are
-    queued without a synchronization in between, so the GPU never idles (and never drops its
-    clocks) before the timed launches start. Returns (seconds, clock warm-up dict, per-launch
-    event median, mean)."""
+    once between two events on the stream the kernels run on, or with `direct` the same launches
+    put on the stream one by one (no graph). Before the warmup launches the graph replays for at
+    least `warm_seconds` (MI355X raises its clocks over the first few hundred milliseconds of
+    load; a cold GEMM reads up to 20 % slow), reported separately as the clock warm-up. Its last
+    four replays, the warmup launches, the first event and the timed launches are queued without
+    a synchronization in between, so the GPU never idles (and never drops its clocks) before the
+    timed launches start; the four replays keep the GPU busy for four times the timed work while
+    the host queues the rest. Returns (seconds, clock warm-up dict, per-launch event median,
+    mean)."""
     import torch
     stream = torch.cuda.Stream()
     n = len(g.w)
@@ -176,7 +178,11 @@ def graph_timed(g, steps, warmup, warm_seconds=WARM_SECONDS):
         for i in range(warmup):
             g.launch(i % n, stream.cuda_stream)
         e0.record(stream)
-        graph.replay()
+        if direct:
+            for i in range(steps):
+                g.launch(i % n, stream.cuda_stream)
+        else:
+            graph.replay()
         e1.record(stream)
     torch.cuda.synchronize()
     sec = e0.elapsed_time(e1) * 1e-3
@@ -187,9 +193,14 @@ def graph_timed(g, steps, warmup, warm_seconds=WARM_SECONDS):
 
 
 def bench_verify(args):
+    """The headline: exactly --steps launches of the verify GEMM, timed as direct stream launches
+    behind the warm-up. A HIP graph replay adds ~5 us of its own on the GPU (measured on MI355X:
+    graphs of 20 launches 10.20-10.27 us per launch, of 1024 launches 9.82; 20 direct launches
+    9.87-10.01, 64-256 9.81-9.84), which at the driver's 20 steps would be 0.25 us per launch
+    that no kernel spends; the gap between consecutive kernels is the same either way."""
     M, N, K = VERIFY["M"], VERIFY["N"], VERIFY["K"]
     g = Gemm(M, N, K, COPIES, seed=1)
-    sec, clock, med_us, mean_us = graph_timed(g, args.steps, args.warmup)
+    sec, clock, med_us, mean_us = graph_timed(g, args.steps, args.warmup, direct=True)
     nbytes = gemm_bytes(M, N, K)
     us = sec / args.steps * 1e6
     return dict(M=M, N=N, K=K, steps=args.steps, warmup=args.warmup, clock_warmup=clock,
@@ -651,7 +662,7 @@ def profile_workload():
     st = torch.cuda.current_stream()
     M, N, K = VERIFY["M"], VERIFY["N"], VERIFY["K"]
     g = Gemm(M, N, K, COPIES, seed=1)
-    graph_timed(g, 64, 16)            # the same graph replay the bench times
+    graph_timed(g, 64, 16, direct=True)   # the bench's warm-up replays and timed launches
     del g
     for _, M, N, K in PREFILL:
         g = Gemm(M, N, K, 2, seed=7)
