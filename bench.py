@@ -428,10 +428,11 @@ class ReadProbe:
 
 def bench_read_probe(steps, warmup):
     """The HBM read ceiling for the verify GEMM: as many bytes per launch as its algorithmic
-    traffic, the same rotation over 16 copies and the same graph replay, nothing but reads."""
+    traffic, the same rotation over 16 copies and the same timing (direct launches behind the
+    graph warm-up), nothing but reads."""
     import torch
     g = ReadProbe(gemm_bytes(VERIFY["M"], VERIFY["N"], VERIFY["K"]), COPIES)
-    sec, _, _, _ = graph_timed(g, steps, warmup, warm_seconds=0.5)
+    sec, _, _, _ = graph_timed(g, steps, warmup, warm_seconds=0.5, direct=True)
     us = sec / steps * 1e6
     gbs = g.n / (us * 1e-6) / 1e9
     del g
