@@ -217,6 +217,23 @@ int w4a8_silu_mul_quant(const void* gate_up, void* q, float* scale, int M, int N
  * point serves callers that need the bf16 activation and lets the stage be tested bit for bit. */
 int w4a8_silu_mul(const void* gate_up, void* out, int M, int N, void* stream);
 
+/* The MLP's SiLU-and-mul and down projection in one call: c bf16 [M, N] = the W4A8 linear of
+ * w4a8_silu_mul_quant's (q, scale) for gate_up bf16 [M, 2K] (contiguous rows, 16-byte aligned),
+ * K % 512 == 0 for the one-launch form, K <= 18432. No counterpart in the reference, whose MLP runs
+ * radiance::silu_mul_quant (sly/mxfp4/radiance_fused_norm.py:163-180) and then the down
+ * projection's radiance::mxfp4_linear_pq (sly/mxfp4/radiance_mxfp4.py:825-860); this replaces the
+ * pair. Where w4a8_silu_mul_linear_fused says so (M <= 2) it is one launch: the streaming GEMM's
+ * quantizing waves form the SiLU-and-mul stage with the producer's own steps and quantize it while
+ * the weight waves stream; otherwise the producer and the GEMM, two launches. The output is the
+ * same bits either way. q [M, K] and scale [M] are caller workspace (not written by the one-launch
+ * form). */
+int w4a8_silu_mul_linear(const void* gate_up, void* q, float* scale, const void* wq,
+                         const void* sq, void* c, int M, int N, int K, void* stream);
+
+/* 1 when w4a8_silu_mul_linear runs this shape as one launch, 0 when as two, -1 for a bad shape.
+ * No counterpart in the reference. */
+int w4a8_silu_mul_linear_fused(int M, int N, int K);
+
 /* Per-head gated RMSNorm (heads of 128, norm before the gate, silu gate, weight without +1), then
  * quant: x = bf16(x * rsqrt(mean_head(x^2) + eps) * weight * silu(z)). x bf16 [M, N] contiguous,
  * z bf16 [M, N] with row stride z_stride elements (a column slice of a wider projection; a

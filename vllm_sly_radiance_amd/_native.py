@@ -49,6 +49,8 @@ SIGNATURES = {
                                   _int]),
     "w4a8_silu_mul_quant": (_int, [_vp, _vp, _vp, _int, _int, _vp, _int]),
     "w4a8_silu_mul": (_int, [_vp, _vp, _int, _int, _vp]),
+    "w4a8_silu_mul_linear": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _int, _int, _int, _vp]),
+    "w4a8_silu_mul_linear_fused": (_int, [_int, _int, _int]),
     "w4a8_gdn_norm_quant": (_int, [_vp, _vp, _long, _vp, _vp, _vp, _int, _int, _c.c_float, _vp,
                                    _int]),
     "w4a8_mfma_probe": (_int, [_int, _vp, _int, _int, _c.POINTER(_c.c_double), _vp]),
@@ -146,6 +148,19 @@ def silu_mul_quant(gu_ptr, q_ptr, s_ptr, M, N, stream, q_layout=Q_ROWS):
 
 def silu_mul(gu_ptr, out_ptr, M, N, stream):
     check(lib().w4a8_silu_mul(gu_ptr, out_ptr, M, N, stream))
+
+
+def silu_mul_linear(gu_ptr, q_ptr, s_ptr, wq_ptr, sq_ptr, c_ptr, M, N, K, stream):
+    check(lib().w4a8_silu_mul_linear(gu_ptr, q_ptr, s_ptr, wq_ptr, sq_ptr, c_ptr, M, N, K, stream))
+
+
+def silu_mul_linear_fused(M: int, N: int, K: int) -> bool:
+    """Does silu_mul_linear() run this shape as one launch (SiLU-mul and quantizer inside the
+    streaming GEMM)."""
+    r = lib().w4a8_silu_mul_linear_fused(M, N, K)
+    if r < 0:
+        check(1)
+    return bool(r)
 
 
 def gdn_norm_quant(x_ptr, z_ptr, z_stride, w_ptr, q_ptr, s_ptr, M, N, eps, stream,

@@ -146,8 +146,8 @@ Scratch registered_scratch(int dev) { return dev >= 0 ? g_scratch[dev] : Scratch
 // activation k-tile at M <= 8, else 8) and that leave no wave without a k-group of its own, then
 // the fewest registers: every wave issues all its loads at once whatever the wave count, so fewer
 // waves move the same bytes with fewer partial sums to add and fewer waves to launch. Measured on
-// MI355X against the fewest-granules rule below (us,
-// GEMM alone, M = 1 / 8 / 16): qkv 6.58 / 6.96 / 8.01 -> 6.30 / 6.86 / 7.58 (3 x 8 x 5 waves),
+// MI355X against the fewest-granules rule below (us, GEMM alone, M = 1 / 8 / 16): qkv
+// 6.58 / 6.96 / 8.01 -> 6.30 / 6.86 / 7.58 (3 x 8 x 5 waves),
 // o_proj 5.11 / 5.82 -> 4.82 / 5.50 (2 x 12 x 4), 7.01 -> 6.67 at M = 16 (2 x 8 x 6), down
 // 6.19 / 7.27 -> 6.13 / 7.14 (2 x 12 x 6; at M = 16 the 2 x 12 x 6 loses, 9.06 against 8.90, and
 // the budget keeps 2 x 8 x 9); gate_up keeps 5 x 4 x 10 (5 x 8 x 5 was within 1 %). Otherwise the
@@ -751,6 +751,41 @@ W4A8_API int w4a8_silu_mul_quant(const void* gate_up, void* q, float* scale, int
                                           part_bytes, q_layout == W4A8_Q_TILED,
                                           (hipStream_t)stream),
                     "w4a8_silu_mul_quant");
+}
+
+// The SiLU-mul linear (no counterpart in the reference, whose MLP runs radiance::silu_mul_quant
+// and then the down projection): one launch where the streaming GEMM's quantizing waves can take
+// the SiLU-and-mul stage too (M <= 2, where w4a8_linear_fused's rule holds for rows of the gate/up
+// width), else the producer and the GEMM. The same bits either way.
+static int silu_linear_fused_variant(int M, int N, int K, bool gu_aligned, int dev) {
+  if (M < 1 || M > 2) return -1;
+  return linear_fused_variant(M, N, K, 2L * K, gu_aligned, dev);
+}
+
+W4A8_API int w4a8_silu_mul_linear_fused(int M, int N, int K) {
+  if (check_gemm_shape("w4a8_silu_mul_linear_fused", M, N, K)) return -1;
+  return silu_linear_fused_variant(M, N, K, true, current_device()) >= 0 ? 1 : 0;
+}
+
+W4A8_API int w4a8_silu_mul_linear(const void* gate_up, void* q, float* scale, const void* wq,
+                                  const void* sq, void* c, int M, int N, int K, void* stream) {
+  if (int e = check_gemm_shape("w4a8_silu_mul_linear", M, N, K)) return e;
+  if (K % 8 || K > 18432)
+    return fail(W4A8_EINVAL, "w4a8_silu_mul_linear: K must be 8-aligned and <= 18432 (K=%d)", K);
+  if (M == 0) return W4A8_OK;
+  if (int e = check_gemm_ptrs("w4a8_silu_mul_linear", q, scale, wq, sq, c)) return e;
+  if (!gate_up) return fail(W4A8_EINVAL, "w4a8_silu_mul_linear: null gate_up");
+  const int dev = current_device();
+  const int v = silu_linear_fused_variant(M, N, K, aligned(gate_up, 16), dev);
+  if (v >= 0) {
+    const GemmArgs g{(const uint8_t*)gate_up, nullptr, (const uint8_t*)wq, (const uint32_t*)sq,
+                     (uint16_t*)c, M, N, K, N};
+    return hip_status(launch_stream(g, v, device_info(dev).cus, true, 2L * K, (hipStream_t)stream,
+                                    true),
+                      "w4a8_silu_mul_linear");
+  }
+  if (int e = w4a8_silu_mul_quant(gate_up, q, scale, M, K, stream, W4A8_Q_ROWS)) return e;
+  return w4a8_gemm(q, scale, wq, sq, c, M, N, K, stream);
 }
 
 W4A8_API int w4a8_silu_mul(const void* gate_up, void* out, int M, int N, void* stream) {

@@ -29,6 +29,7 @@
 //  * gemm_stream_fq (below) is the whole linear in one launch: bf16 activations, the per-token
 //    quantizer run by extra waves of each workgroup while the weight waves stream.
 #include "w4a8_fp8.h"
+#include "w4a8_silu.h"
 
 namespace w4a8 {
 namespace {
@@ -184,6 +185,9 @@ __global__ __launch_bounds__(W * 64) void gemm_stream(
 // LDS: the codes [k-tile][half][lane group][8 tokens][16 B] (KT KiB), then 8 token scales, three
 // counters, Q x 8 partial maxima (512 B in all), then the partial sums. X is bf16 [M, ldx], 16-byte
 // aligned rows; the host requires M <= 8, 4 <= W <= 12, K % 512 == 0 and 16 ldx < 2^31.
+// SILU: X is the gate/up output of the layer before, [M, ldx] with gate in columns 0..K-1 and up in
+// K..2K-1, and the row quantized is the SiLU-and-mul producer's bf16 stage,
+// bf16(bf16(silu(gate)) * up), computed with the producer's own steps (w4a8_silu.h); M <= 2.
 constexpr int kFqWaves = 16;           // weight waves + quantizing waves
 constexpr int kFqSpin = 1 << 20;       // s_sleep(2) rounds a wave waits at most (~0.1 s)
 constexpr int kFqHeader = 512;         // scales, counters, partial maxima
@@ -214,7 +218,7 @@ __device__ __forceinline__ void fq_signal(int* counter) {
     __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-template <int NT, int KPW, int W>
+template <int NT, int KPW, int W, bool SILU>
 __global__ __launch_bounds__(kFqWaves * 64) void gemm_stream_fq(
     const uint8_t* __restrict__ X, const uint8_t* __restrict__ Wq, const uint32_t* __restrict__ Sq,
     int M, int K, int NTILES, int G, int ldx, uint16_t* __restrict__ C, int N, int vec_out) {
@@ -239,24 +243,37 @@ __global__ __launch_bounds__(kFqWaves * 64) void gemm_stream_fq(
     constexpr int CH = (KPW * W + 4 * Q - 1) / (4 * Q);     // >= ceil(K / 8 / Q / 64)
     const int q = wave - W, nch = K >> 3;
     const int c0 = q * nch / Q, c1 = (q + 1) * nch / Q;
+    constexpr int MR = SILU ? 2 : 8;             // rows a launch may have
     const auto x_src = __builtin_amdgcn_make_buffer_rsrc((void*)X, 0, M * ldx * 2, kBufferWord3);
-    uint4 v[8][CH];
+    uint4 v[MR][CH], up[SILU ? MR : 1][SILU ? CH : 1];
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
+    for (int t = 0; t < MR; ++t) {
       if (t >= M) break;                         // rows past M: no loads issued at all
 #pragma unroll
       for (int i = 0; i < CH; ++i) {
         const int c = c0 + lane + 64 * i;
-        v[t][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                      x_src, c < c1 ? t * ldx * 2 + 16 * c : 0x7FFFFFF0, 0, 0));
+        const int off = c < c1 ? t * ldx * 2 + 16 * c : 0x7FFFFFF0;
+        v[t][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(x_src, off, 0, 0));
+        if constexpr (SILU)                      // the up half: K columns (2K bytes) further
+          up[t][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                         x_src, c < c1 ? off + 2 * K : 0x7FFFFFF0, 0, 0));
       }
     }
     if (q == 0 && lane < 3)
       __hip_atomic_store(&cnt[lane], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     lds_barrier();                               // (the weight waves' barrier below: one barrier)
+    if constexpr (SILU) {
+      // the producer's bf16 stage; chunks past the range loaded zeros and stay zero
+#pragma unroll
+      for (int t = 0; t < MR; ++t) {
+        if (t >= M) break;
+#pragma unroll
+        for (int i = 0; i < CH; ++i) v[t][i] = prod::silu_mul_group(v[t][i], up[t][i]);
+      }
+    }
     // partial maxima of this column range, then each row's amax over the Q ranges
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
+    for (int t = 0; t < MR; ++t) {
       if (t >= M) break;
       uint32_t am = 0;
 #pragma unroll
@@ -267,7 +284,7 @@ __global__ __launch_bounds__(kFqWaves * 64) void gemm_stream_fq(
     fq_signal(&cnt[0]);
     fq_wait(&cnt[0], Q, &cnt[2]);
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
+    for (int t = 0; t < MR; ++t) {
       if (t >= M) break;
       uint32_t am = 0;
       for (int qq = 0; qq < Q; ++qq) am = max(am, pam[qq * 8 + t]);
@@ -437,7 +454,7 @@ bool stream_linear_fits(int variant, int M, int N, int K, long ldx, int cus, siz
 // fused: g.a is the bf16 activation with row stride lda elements (the quantizer runs in the
 // kernel); otherwise g.a is e4m3 [M, K] and g.a_scale its per-token scales
 hipError_t launch_stream(const GemmArgs& g, int variant, int cus, bool fused, long lda,
-                         hipStream_t stream) {
+                         hipStream_t stream, bool silu) {
   const int NTILES = padded_n(g.N) / kNTile;
   const int vec_out = (g.N % 4 == 0 && ((uintptr_t)g.c % 8) == 0) ? 1 : 0;
   const dim3 grid(stream_grid(g.N, cus)), block(kStream[variant].waves * 64);
@@ -460,11 +477,18 @@ hipError_t launch_stream(const GemmArgs& g, int variant, int cus, bool fused, lo
 #define W4A8_STREAM_LAUNCH(nt, kpw, w)                                                           \
   if (idx++ == variant) {                                                                        \
     if constexpr (w >= 4 && w <= kFqWaves - 4 && nt * kpw <= 24) {                               \
+      if (fused && silu) {                                                                       \
+        W4A8_STREAM_ATTR((gemm_stream_fq<nt, kpw, w, true>))                                     \
+        hipLaunchKernelGGL((gemm_stream_fq<nt, kpw, w, true>), grid, dim3(kFqWaves * 64), lds,    \
+                           stream, g.a, g.wq, g.sq, g.M, g.K, NTILES, (int)grid.x, (int)lda,     \
+                           g.c, g.N, vec_out);                                                   \
+        return hipGetLastError();                                                                \
+      }                                                                                          \
       if (fused) {                                                                               \
-        W4A8_STREAM_ATTR((gemm_stream_fq<nt, kpw, w>))                                           \
-        hipLaunchKernelGGL((gemm_stream_fq<nt, kpw, w>), grid, dim3(kFqWaves * 64), lds, stream,  \
-                           g.a, g.wq, g.sq, g.M, g.K, NTILES, (int)grid.x,                       \
-                           (int)lda, g.c, g.N, vec_out);                                         \
+        W4A8_STREAM_ATTR((gemm_stream_fq<nt, kpw, w, false>))                                    \
+        hipLaunchKernelGGL((gemm_stream_fq<nt, kpw, w, false>), grid, dim3(kFqWaves * 64), lds,   \
+                           stream, g.a, g.wq, g.sq, g.M, g.K, NTILES, (int)grid.x, (int)lda,     \
+                           g.c, g.N, vec_out);                                                   \
         return hipGetLastError();                                                                \
       }                                                                                          \
     }                                                                                            \

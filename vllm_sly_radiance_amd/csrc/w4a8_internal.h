@@ -143,9 +143,11 @@ bool stream_fits(int variant, int M, int N, int K, int cus, size_t lds_limit);
 // M <= 4 with 3 or more n-tiles per workgroup or at most 4 row chunks per lane of a quantizing
 // wave), room for the quantizing waves, 16-byte rows, LDS.
 bool stream_linear_fits(int variant, int M, int N, int K, long ldx, int cus, size_t lds_limit);
-// fused: g.a is bf16 [M, K] with row stride lda elements and g.a_scale is unused
+// fused: g.a is bf16 [M, K] with row stride lda elements and g.a_scale is unused; with silu too,
+// g.a is the gate/up output [M, 2K] (row stride lda) and the kernel quantizes its SiLU-and-mul
+// stage (M <= 2)
 hipError_t launch_stream(const GemmArgs& g, int variant, int cus, bool fused, long lda,
-                         hipStream_t stream);
+                         hipStream_t stream, bool silu = false);
 
 // Pipelined streaming family (M <= 16 * MF): grid = at most one workgroup per CU, each with the
 // same number of n-tiles (at most nt) and all of K; each of the `waves` waves streams a contiguous

@@ -44,7 +44,7 @@ if A_TILED_MIN_M and A_TILED_MIN_M <= DECODE_BAND_MAX_M:
     raise RuntimeError(f"RADIANCE_MXFP4_A_TILED_MIN_M must exceed {DECODE_BAND_MAX_M} (the decode "
                        f"band reads row-major activations), got {A_TILED_MIN_M}")
 
-STATS = {"fast": 0, "refused": 0, "calls": 0, "calls_pq": 0, "calls_tiled": 0}
+STATS = {"fast": 0, "refused": 0, "calls": 0, "calls_pq": 0, "calls_tiled": 0, "calls_silu": 0}
 _scratch = [None, None]          # [partials, counters]: torch-owned, alive for the process
 
 
@@ -255,6 +255,38 @@ def mxfp4_linear_pq(x_fp8: torch.Tensor, x_scale: torch.Tensor, weight: torch.Te
 @mxfp4_linear_pq.register_fake
 def _(x_fp8, x_scale, weight, weight_scale, weight_ref, allow_tiled=True):
     return torch.empty((x_fp8.shape[0], weight_ref.shape[0]), device=x_fp8.device,
+                       dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("radiance::silu_mul_mxfp4_linear", mutates_args=())
+def silu_mul_mxfp4_linear(gate_up: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
+                          weight_ref: torch.Tensor) -> torch.Tensor:
+    """The MLP's tail in one op: gate_up bf16 [M, 2K] -> the down projection [M, N] of
+    silu(gate) * up, the same bits as radiance::silu_mul_quant followed by mxfp4_linear_pq (the
+    reference's pair, sly/mxfp4/radiance_fused_norm.py:163-180 and sly/mxfp4/radiance_mxfp4.py:
+    825-860). At M <= 2 one launch: the streaming GEMM's quantizing waves form and quantize the
+    SiLU-and-mul stage while its weight waves stream; otherwise the producer and the GEMM."""
+    STATS["calls_silu"] += 1
+    N, K = weight_ref.shape[0], weight_ref.shape[1]
+    if gate_up.dim() != 2 or gate_up.shape[1] != 2 * K:
+        raise RuntimeError(f"[radiance.mxfp4] gate_up {tuple(gate_up.shape)} does not match "
+                           f"2K={2 * K}")
+    if gate_up.dtype != torch.bfloat16:
+        raise RuntimeError(f"[radiance.mxfp4] gate_up must be bf16, got {gate_up.dtype}")
+    gate_up = gate_up.contiguous()
+    M = gate_up.shape[0]
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=gate_up.device)
+    q = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=gate_up.device)
+    s = torch.empty((M,), dtype=torch.float32, device=gate_up.device)
+    if M:
+        _native.silu_mul_linear(gate_up.data_ptr(), q.data_ptr(), s.data_ptr(), weight.data_ptr(),
+                                weight_scale.data_ptr(), out.data_ptr(), M, N, K, _stream())
+    return out
+
+
+@silu_mul_mxfp4_linear.register_fake
+def _(gate_up, weight, weight_scale, weight_ref):
+    return torch.empty((gate_up.shape[0], weight_ref.shape[0]), device=gate_up.device,
                        dtype=torch.bfloat16)
 
 
