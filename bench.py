@@ -524,6 +524,18 @@ def _timed_graph(fn, reps, warm_seconds=0.2):
     return ms
 
 
+def tiled_q(q):
+    """Row-major e4m3 codes [M, K] (K % 128 == 0) -> the fragment-tiled bytes the producers write
+    with Q_TILED: 16-token blocks, then k-tiles, then the two 64-byte halves, each 16 tokens x 4
+    runs of 16 bytes in lane order (the last block's padding tokens zero)."""
+    import torch
+    M, K = q.shape
+    Mp = -(-M // 16) * 16
+    p = torch.zeros((Mp, K), dtype=torch.uint8, device=q.device)
+    p[:M] = q.view(torch.uint8)
+    return p.view(Mp // 16, 16, K // 128, 2, 4, 16).permute(0, 2, 3, 4, 1, 5).contiguous().view(-1)
+
+
 def bench_sweep(n_layers):
     """64 stacked Qwen3.8-27B-shaped layers (qkv, o_proj, gate_up, down), random-init MXFP4
     checkpoint tensors generated on the device. Loads every linear through the plugin's
@@ -598,8 +610,10 @@ def bench_sweep(n_layers):
     # crossover: GEMM only (pre-quantized activations), up to 16 layers' weights rotating. The
     # decode family is the streaming kernel where it serves (M <= 16), else the pipelined ring
     # kernel with the fragments covering M (its first variant that serves the shape; a forced
-    # plan, kept to show why the plan takes the tiles there); the tile family is the macro tile
-    # the plan takes at M, or at M = 17 below that.
+    # plan, kept to show why the plan takes the tiles there), timed on row-major q and, as
+    # ring_at_us, on the same codes fragment-tiled (contiguous 1 KiB activation loads instead of
+    # 16 token rows x 64 bytes); the tile family is the macro tile the plan takes at M, or at
+    # M = 17 below that, with the plan's K split (tile_split; tile_unsplit_us beside it).
     ring = _native.variants(_native.KERNEL_RING)
     cross = {}
     for name, N, K in LAYER_M1:
@@ -610,16 +624,26 @@ def bench_sweep(n_layers):
             lins = layers[name][:16]
             per = len(lins)
 
-            def run(kernel, variant, split, q=q, sc=sc, out=out, lins=lins, M=M):
+            qt = tiled_q(q) if M <= 64 else q
+
+            def run(kernel, variant, split, q=q, qt=qt, sc=sc, out=out, lins=lins, M=M):
+                if kernel == _native.KERNEL_RING_AT:
+                    q = qt
                 for lin in lins:
                     _native.gemm(q.data_ptr(), sc.data_ptr(), lin.weight.data_ptr(),
                                  lin.weight_scale.data_ptr(), out.data_ptr(), M, N, K,
                                  torch.cuda.current_stream().cuda_stream, kernel, variant, split)
 
             k, v, sp = _native.plan(M, N, K)
-            tile_v = v if k == _native.KERNEL_TILE else _native.plan(max(M, 17), N, K)[1]
+            tile_v, tile_sp = (v, sp) if k == _native.KERNEL_TILE else \
+                _native.plan(max(M, 17), N, K)[1:]
             row = dict(M=M, tile_us=round(_timed_graph(
-                lambda: run(_native.KERNEL_TILE, tile_v, 1), 5) * 1e3 / per, 2))
+                lambda: run(_native.KERNEL_TILE, tile_v, tile_sp), 5) * 1e3 / per, 2))
+            if tile_sp > 1:
+                # the plan splits K here: the same tile unsplit beside it
+                row["tile_split"] = tile_sp
+                row["tile_unsplit_us"] = round(_timed_graph(
+                    lambda: run(_native.KERNEL_TILE, tile_v, 1), 5) * 1e3 / per, 2)
             if k != _native.KERNEL_STREAM and M <= 64:
                 mf = -(-M // 16)
                 k, sp = _native.KERNEL_RING, 1
@@ -629,6 +653,9 @@ def bench_sweep(n_layers):
                     row["decode_us"] = round(_timed_graph(lambda: run(k, v, sp), 5) * 1e3 / per,
                                              2)
                     row["decode_kernel"] = "stream" if k == _native.KERNEL_STREAM else "ring"
+                    if k == _native.KERNEL_RING:
+                        row["ring_at_us"] = round(_timed_graph(
+                            lambda: run(_native.KERNEL_RING_AT, v, sp), 5) * 1e3 / per, 2)
                 except RuntimeError:
                     pass
             rows.append(row)

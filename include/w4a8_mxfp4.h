@@ -41,7 +41,8 @@ enum {
   W4A8_KERNEL_TILE = 2,    /* LDS-pipelined macro tiles (M > 16) */
   W4A8_KERNEL_STREAM = 3,  /* whole k-range of every wave in flight at once, M <= 16 */
   W4A8_KERNEL_RING = 4,    /* per-wave pipeline of k-tile stages, M <= 64 (forced plans only) */
-  W4A8_KERNEL_TILE_AT = 5  /* the macro tiles on fragment-tiled activations (same variants) */
+  W4A8_KERNEL_TILE_AT = 5, /* the macro tiles on fragment-tiled activations (same variants) */
+  W4A8_KERNEL_RING_AT = 6  /* the ring kernel on fragment-tiled activations (same variants) */
 };
 
 /* Layouts of the producers' e4m3 output q (the q_layout argument).
@@ -124,7 +125,7 @@ int w4a8_tiled_bytes(int M, int K, size_t* bytes);
 /* w4a8_gemm with an explicit plan, for sweeps and tests (the reference forces cells through the
  * RADIANCE_MXFP4_DECODE_KS / _BK environment knobs, sly/mxfp4/radiance_mxfp4_fp8.hip:1464-1475).
  * split_k > 1 needs registered scratch of w4a8_scratch_bytes(); kernels 2 and 5 ignore split_k;
- * kernel 5 reads fragment-tiled activations. */
+ * kernels 5 and 6 read fragment-tiled activations. */
 int w4a8_gemm_planned(const void* a, const float* a_scale, const void* wq, const void* sq, void* c,
                       int M, int N, int K, int kernel, int variant, int split_k, void* stream);
 

@@ -47,16 +47,21 @@ def stream() -> int:
     return torch.cuda.current_stream().cuda_stream
 
 
-def gemm_errors(out_bits: np.ndarray, q, s, w, ws):
+def gemm_reference(q, s, w, ws):
+    """(ref, terms): the oracle's fp32-accumulated GEMM and the sum of |terms| per output, which
+    gemm_errors needs; compute once when several outputs of one GEMM are checked."""
+    return O.gemm_ref_f32(q, s, w, ws).astype(np.float64), O.gemm_abs_terms(q, s, w, ws)
+
+
+def gemm_errors(out_bits: np.ndarray, q, s, w, ws, reference=None):
     """(rel_l2, worst ratio of |out - ref| to the per-element allowance, max ulp error, fraction
-    of elements within ULP_MAX bf16 ulp of ref)."""
-    ref = O.gemm_ref_f32(q, s, w, ws).astype(np.float64)
+    of elements within ULP_MAX bf16 ulp of ref). reference: gemm_reference's pair, if at hand."""
+    ref, terms = reference if reference is not None else gemm_reference(q, s, w, ws)
     refb = O.bf16_to_f32(O.f32_to_bf16(ref.astype(np.float32))).astype(np.float64)
     out = O.bf16_to_f32(out_bits).astype(np.float64)
     if not np.all(np.isfinite(out)):
         return np.inf, np.inf, np.inf, 0.0
     rel = np.linalg.norm(out - refb) / max(np.linalg.norm(refb), 1e-300)
-    terms = O.gemm_abs_terms(q, s, w, ws)
     ulp = O.bf16_ulp(ref)
     allow = ULP_MAX * ulp + HW_ACC_EPS * terms
     err = np.abs(out - ref)
@@ -93,8 +98,8 @@ def parity_stats(out_bits: np.ndarray, q, s, w, ws):
                 outputs=int(out.size))
 
 
-def assert_gemm_close(out_bits: np.ndarray, q, s, w, ws, what: str = ""):
-    rel, ratio, ulps, within = gemm_errors(out_bits, q, s, w, ws)
+def assert_gemm_close(out_bits: np.ndarray, q, s, w, ws, what: str = "", reference=None):
+    rel, ratio, ulps, within = gemm_errors(out_bits, q, s, w, ws, reference)
     print(f"[parity] {what}: rel_l2={rel:.3e} worst/allowance={ratio:.3f} max_ulp={ulps:.2f} "
           f"within_{ULP_MAX:g}ulp={within:.6f}")
     assert rel <= REL_L2_MAX and ratio <= 1.0, \

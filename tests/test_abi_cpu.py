@@ -266,12 +266,40 @@ def test_tiled_gemm_validates_before_launch(lib):
     assert b"K % 128" in lib.w4a8_last_error()
     assert lib.w4a8_gemm_at(None, p, p, p, p, 64, 256, 5120, None) == 1          # null a
     assert lib.w4a8_gemm_at(None, None, None, None, None, 0, 256, 5120, None) == 0
-    # fragment-tiled activations go to the tile kernel only
+    # fragment-tiled activations go to the tile and ring kernels only
     assert lib.w4a8_gemm_planned(p, p, p, p, p, 8, 256, 512, _native.KERNEL_TILE_AT, 99, 1,
                                  None) == 1
     assert b"tile variant 99 out of range" in lib.w4a8_last_error()
     assert lib.w4a8_variant_count(_native.KERNEL_TILE_AT) == \
         lib.w4a8_variant_count(_native.KERNEL_TILE)
+    assert lib.w4a8_gemm_planned(p, p, p, p, p, 32, 256, 5120 + 32, _native.KERNEL_RING_AT, 0, 1,
+                                 None) == 1
+    assert b"K % 128" in lib.w4a8_last_error()
+    assert lib.w4a8_gemm_planned(p, p, p, p, p, 32, 256, 512, _native.KERNEL_RING_AT, 99, 1,
+                                 None) == 1
+    assert b"ring variant 99 out of range" in lib.w4a8_last_error()
+    assert lib.w4a8_variant_count(_native.KERNEL_RING_AT) == \
+        lib.w4a8_variant_count(_native.KERNEL_RING)
+
+
+def test_tile_k_split_validates_before_launch(lib):
+    """A forced tile plan with split_k > 1 splits K over workgroup rows: it needs a variant with a
+    K-split form (the 4-wave tiles up to 64 tokens tall), N % 16 == 0, at most one split per
+    k-group, and registered scratch for the fp32 partials."""
+    p = 1 << 20
+    big = next(v for v, c in enumerate(_native.variants(_native.KERNEL_TILE)) if c[2] == 256)
+    assert lib.w4a8_gemm_planned(p, p, p, p, p, 32, 1024, 8704, _native.KERNEL_TILE, big, 3,
+                                 None) == 1
+    assert b"no K-split form" in lib.w4a8_last_error()
+    assert lib.w4a8_gemm_planned(p, p, p, p, p, 32, 1000, 8704, _native.KERNEL_TILE, 0, 3,
+                                 None) == 1
+    assert b"N % 16 == 0" in lib.w4a8_last_error()
+    assert lib.w4a8_gemm_planned(p, p, p, p, p, 32, 1024, 1024, _native.KERNEL_TILE, 0, 3,
+                                 None) == 1
+    assert b"one split per k-group (2)" in lib.w4a8_last_error()
+    assert lib.w4a8_gemm_planned(p, p, p, p, p, 32, 1024, 8704, _native.KERNEL_TILE, 0, 3,
+                                 None) == 2
+    assert b"needs 393216 B of partials" in lib.w4a8_last_error()
 
 
 @pytest.mark.parametrize("M,K,want", [(0, 128, 0), (1, 128, 2048), (16, 5120, 16 * 5120),
@@ -297,12 +325,19 @@ def test_read_probe_validates_before_launch(lib):
     assert b"w4a8_read_probe" in lib.w4a8_last_error()
 
 
-def test_workspace_bytes_is_a_few_hundred_kib(lib):
-    """The scratch the plugin registers, sized by the library's own plan: split-K partials for the
-    decode band's small-N shapes plus SiLU-mul's split-row maxima, well under 1 MiB at the model's
-    widths (the reference registered 37.7 MB, sly/mxfp4/radiance_mxfp4.py:1064-1070)."""
+def test_workspace_bytes_covers_the_band_split_in_4_mib(lib):
+    """The scratch the plugin registers, sized by the library's own plan: the skinny kernel's
+    split-K partials for small-N shapes at M <= 16, SiLU-mul's split-row maxima, and the band's
+    three-way K split of the tile kernel (fp32 partials of 3 x M x N, M <= 48), which fires only
+    where the unsplit grid leaves half the CUs idle (N <= 85 x 64 = 5440 on 256 CUs): 3.1 MB in
+    all, within the allocation-free entry point's 4 MiB (the reference registered 37.7 MB,
+    sly/mxfp4/radiance_mxfp4.py:1064-1070)."""
     part, cnt = _native.workspace_bytes(64, 36864)
-    assert 9216 <= part < 1 << 20 and 0 < cnt <= 4096
+    assert part == 3 * 48 * 5440 * 4 and 0 < cnt <= 4096
+    assert part <= 4 << 20
+    # down (N = 5120) at M = 48 fits; without the band (M <= 16) it stays under 1 MiB
+    assert _native.workspace_bytes(64, 5120)[0] == 3 * 48 * 5120 * 4
+    assert 9216 <= _native.workspace_bytes(16, 36864)[0] < 1 << 20
     # monotone in the limits, and never below SiLU-mul's own need (64 rows x 36 chunks x 4 B)
     p2, c2 = _native.workspace_bytes(64, 65536)
     assert p2 >= part and c2 >= cnt

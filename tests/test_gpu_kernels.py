@@ -12,14 +12,15 @@ import torch
 
 from oracle import mfma_model as MM
 from oracle import mxfp4_oracle as O
-from tests._check import (HW_ACC_EPS, assert_gemm_close, bf16_dev, host_u16, host_u8, stream,
-                          to_dev)
+from tests._check import (HW_ACC_EPS, assert_gemm_close, bf16_dev, gemm_reference, host_u16,
+                          host_u8, stream, to_dev)
 from vllm_sly_radiance_amd import _native, synthetic
 
 pytestmark = pytest.mark.gpu
 
 SKINNY, TILE, STREAM = _native.KERNEL_SKINNY, _native.KERNEL_TILE, _native.KERNEL_STREAM
 RING = _native.KERNEL_RING
+RING_AT = _native.KERNEL_RING_AT
 
 
 @pytest.fixture(scope="module")
@@ -78,6 +79,27 @@ def gpu_gemm(q, s, wq, sq, N, K, kernel=0, variant=-1, split_k=0):
     out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
     _native.gemm(qd.data_ptr(), sd.data_ptr(), wq.data_ptr(), sq.data_ptr(), out.data_ptr(), M, N,
                  K, stream(), kernel, variant, split_k)
+    torch.cuda.synchronize()
+    return host_u16(out)
+
+
+def gpu_gemm_tiled(q, s, wq, sq, N, K, kernel, variant):
+    """gpu_gemm on the fragment-tiled bytes of q (oracle tile_q)."""
+    M = q.shape[0]
+    qd, sd = to_dev(O.tile_q(q)), to_dev(s.astype(np.float32))
+    out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+    _native.gemm(qd.data_ptr(), sd.data_ptr(), wq.data_ptr(), sq.data_ptr(), out.data_ptr(), M, N,
+                 K, stream(), kernel, variant, 1)
+    torch.cuda.synchronize()
+    return host_u16(out)
+
+
+def gpu_gemm_tiled_split(q, s, wq, sq, N, K, variant, split):
+    M = q.shape[0]
+    qd, sd = to_dev(O.tile_q(q)), to_dev(s.astype(np.float32))
+    out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+    _native.gemm(qd.data_ptr(), sd.data_ptr(), wq.data_ptr(), sq.data_ptr(), out.data_ptr(), M, N,
+                 K, stream(), _native.KERNEL_TILE_AT, variant, split)
     torch.cuda.synchronize()
     return host_u16(out)
 
@@ -298,10 +320,11 @@ def test_mfma_model_matches_device_on_random_granules(gpu_lib):
     assert np.all(np.abs(O.bf16_to_f32(out) - model) <= 2 * O.bf16_ulp(model) + HW_ACC_EPS * terms)
 
 
-DECODE_SHAPES = [(5120, 5120), (17408, 5120), (5120, 8704), (48, 5120), (33, 640), (10240, 96)]
+DECODE_SHAPES = [(5120, 5120), (17408, 5120), (5120, 8704), (10240, 5120), (5120, 6144),
+                 (48, 5120), (33, 640), (10240, 96)]
 
 
-@pytest.mark.parametrize("M", [1, 2, 8, 16, 17, 24, 33, 48, 64])
+@pytest.mark.parametrize("M", [1, 2, 8, 16, 17, 24, 32, 33, 48, 64])
 @pytest.mark.parametrize("N,K", DECODE_SHAPES)
 def test_gemm_decode_band_auto_plan(gpu_lib, scratch, M, N, K):
     x = synthetic.activations(M, K, seed=11 * M + K)
@@ -381,7 +404,9 @@ def test_gemm_every_ring_variant(gpu_lib, N, K):
     """The pipelined streaming family at every variant that serves (M, N, K): M up to each
     variant's fragments (ragged), N ragged against the n-tile shares, K ending inside a k-tile
     (1056) or a k-group (640, 4128), ranges whose last round is padded. A variant that does not
-    serve a shape (n-tiles per workgroup beyond NT, fewer k-tiles than waves) must refuse it."""
+    serve a shape (n-tiles per workgroup beyond NT, fewer k-tiles than waves) must refuse it.
+    Where K % 128 == 0 the same variant on the fragment-tiled codes (kernel RING_AT) must give the
+    same bits."""
     w, ws = cached_weights(N, K, N + 5 * K)
     wq, sq = gpu_repack(w, ws)
     ran = 0
@@ -399,6 +424,9 @@ def test_gemm_every_ring_variant(gpu_lib, N, K):
                 continue
             ran += 1
             assert_gemm_close(out, q, s, w, ws, f"M={M} N={N} K={K} ring variant {v} {cfg}")
+            if K % 128 == 0:
+                out_at = gpu_gemm_tiled(q, s, wq, sq, N, K, RING_AT, v)
+                assert np.array_equal(out_at, out), f"M={M} N={N} K={K} ring variant {v} tiled"
     assert ran > 0
 
 
@@ -502,6 +530,57 @@ def test_split_k_reduction_has_no_race(gpu_lib, scratch):
         for j in range(2):
             miss = int((outs[j] != gold[j]).flatten(1).any(1).sum())
             assert miss == 0, f"split {ks}: {miss}/64 launches differ from golden {j}"
+
+
+@pytest.mark.parametrize("M,N,K", [(17, 5120, 8704), (40, 1040, 2080), (64, 256, 8704),
+                                   (33, 48, 1056), (20, 5120, 6144)])
+def test_gemm_tile_k_split(gpu_lib, scratch, M, N, K):
+    """The tile kernel with K split over workgroup rows (fp32 partials, then the reducing launch)
+    at the band's tile shapes and 2..6 splits: K ending inside a k-tile (1056) or a k-group (2080),
+    so the last split runs zero slabs; N ragged against the tile (1040, 48). Against the oracle, and
+    the row-major and fragment-tiled activations give the same bits."""
+    x = synthetic.activations(M, K, seed=M + K)
+    w, ws = cached_weights(N, K, N + 7 * K)
+    q, s = O.quant_per_token(x)
+    wq, sq = gpu_repack(w, ws)
+    ref = gemm_reference(q, s, w, ws)
+    kg = -(-K // 512)
+    ran = 0
+    for v, (wm, wn, bm, bn) in enumerate(_native.variants(TILE)):
+        cfg = _native.tile_config(v)
+        if cfg["waves"] != 4 or wm > 2:
+            # only the 4-wave band tiles have a K-split form; the others refuse one
+            with pytest.raises(RuntimeError, match="no K-split form"):
+                gpu_gemm(q, s, wq, sq, N, K, TILE, v, 2)
+            continue
+        # every split count on the band plan's two tiles, three splits on the others
+        full = cfg["stages"] in (5, 8) and bn == 64
+        for split in (range(2, min(6, kg) + 1) if full else (min(3, kg),)):
+            print(f"[tile split] M={M} N={N} K={K} variant {v} ({bm}x{bn}) split {split}",
+                  flush=True)
+            out = gpu_gemm(q, s, wq, sq, N, K, TILE, v, split)
+            ran += 1
+            assert_gemm_close(out, q, s, w, ws, f"M={M} N={N} K={K} tile {v} split {split}", ref)
+            if K % 128 == 0 and split == min(3, kg):
+                out_at = gpu_gemm_tiled_split(q, s, wq, sq, N, K, v, split)
+                assert np.array_equal(out_at, out), f"tiled split {v}"
+    assert ran > 0
+
+
+def test_band_split_plan_for_down(gpu_lib):
+    """With the plugin's scratch registered, the automatic plan splits down (5120 x 8704) three
+    ways at M = 17..48 on the 32 x 64 (8-stage) / 64 x 64 (5-stage) tiles, not at M = 64, and no
+    other BASELINE shape."""
+    from vllm_sly_radiance_amd import radiance_mxfp4 as R
+    R.ensure_scratch("cuda")
+    assert _native.plan(64, 5120, 8704)[2] == 1
+    for M in (17, 24, 32, 33, 48):
+        k, v, sp = _native.plan(M, 5120, 8704)
+        want = (32, 64, 8) if M <= 32 else (64, 64, 5)
+        c = _native.tile_config(v)
+        assert (k, sp, c["bm"], c["bn"], c["stages"]) == (TILE, 3, *want), (M, k, v, sp, c)
+        for N, K in ((10240, 5120), (5120, 6144), (17408, 5120)):
+            assert _native.plan(M, N, K)[2] == 1, (M, N, K)
 
 
 # ---- diagnostics --------------------------------------------------------------------------------

@@ -14,7 +14,8 @@ import threading
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libw4a8_mxfp4.so")
 ABI_VERSION = 2
-KERNEL_AUTO, KERNEL_SKINNY, KERNEL_TILE, KERNEL_STREAM, KERNEL_RING, KERNEL_TILE_AT = range(6)
+(KERNEL_AUTO, KERNEL_SKINNY, KERNEL_TILE, KERNEL_STREAM, KERNEL_RING, KERNEL_TILE_AT,
+ KERNEL_RING_AT) = range(7)
 Q_ROWS, Q_TILED = 0, 1          # layouts of a producer's q
 
 _c = ctypes

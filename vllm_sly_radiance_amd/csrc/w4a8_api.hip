@@ -264,6 +264,34 @@ int big_tile(int M, int N, int dev) {
 // Qwen3.8-27B shapes (it stays available to a forced plan).
 int plan_tile(int M, int N, int dev);
 
+// Decode band, K split across workgroup rows (the tile kernel writes fp32 partials, a second launch
+// adds them in split order). At these M every workgroup streams the whole M x K activation panel
+// whatever its share of N, so a grid that leaves most CUs idle is bound by the panel each of its
+// CUs fetches; splitting K three ways cuts that panel to a third at the cost of the reducing
+// launch (~1.5-2 us). Measured on MI355X (graph replays over rotating weights, us, plan before ->
+// split): down N=5120 K=8704 at M = 17 / 32 / 48 / 64: 11.2 -> 9.0, 11.2 -> 9.9, 12.8 -> 11.5,
+// 13.0 -> 12.4 (within the spread between boxes at 64); o_proj K=6144 (12 k-groups) gains at
+// M = 17 only and loses above, and the shapes whose unsplit grid covers most CUs (qkv, gate_up)
+// lose at every split. So: up to 48 tokens, three splits of at least 5 k-groups each, when the
+// unsplit grid would leave at least half of the CUs idle and three times it fits one round, with
+// 32 x 64 tiles (8 stages) up to 32 tokens and 64 x 64 (5 stages) above, and only when the scratch
+// holds the partials. Returns the split (1: none).
+constexpr int kBandSplit = 3, kBandSplitMaxM = 48;
+
+int band_split(int M, int N, int K, int cus, const Scratch& sc, int* variant) {
+  if (M <= 16 || M > kBandSplitMaxM || N % kNTile) return 1;
+  const int v = M <= 32 ? find_tile(1, 2, 4, 8) : find_tile(2, 2, 4, 5);
+  if (v < 0) return 1;
+  const TileCfg c = tile_variant(v);
+  const long grid = (long)ceil_div(M, c.bm) * ceil_div(N, c.bn);
+  const int kg = padded_k(K) / (kKTile * kKGroup);
+  if (2 * grid > cus || grid * kBandSplit > cus || kg < 5 * kBandSplit ||
+      tile_split_bytes(M, N, kBandSplit) > sc.partial_bytes || !tile_fits(M, N, K))
+    return 1;
+  *variant = v;
+  return kBandSplit;
+}
+
 void plan_impl(int M, int N, int K, int dev, const Scratch& sc, int* kernel, int* variant,
                int* split_k) {
   if (M <= 16) {
@@ -289,8 +317,8 @@ void plan_impl(int M, int N, int K, int dev, const Scratch& sc, int* kernel, int
     return;
   }
   *kernel = W4A8_KERNEL_TILE;
-  *variant = plan_tile(M, N, dev);
-  *split_k = 1;
+  *split_k = band_split(M, N, K, device_info(dev).cus, sc, variant);
+  if (*split_k == 1) *variant = plan_tile(M, N, dev);
 }
 
 // The macro-tile variant for an M x N GEMM: the decode-band rule for M <= 64, the prefill rule
@@ -394,16 +422,31 @@ int gemm_dispatch(const void* a, const float* as, const void* wq, const void* sq
     if (!tile_fits(M, N, K))
       return fail(W4A8_EINVAL, "%s: M=%d K=%d exceeds the tile kernel's 32-bit offsets", who,
                   M, K);
+    if (split_k > 1) {
+      const int kg = padded_k(K) / (kKTile * kKGroup);
+      if (!tile_splits(variant))
+        return fail(W4A8_EINVAL, "%s: tile variant %d has no K-split form (4-wave tiles up to 64 "
+                    "tokens tall have one)", who, variant);
+      if (split_k > kg || N % kNTile)
+        return fail(W4A8_EINVAL, "%s: a tile K split needs N %% %d == 0 and at most one split per "
+                    "k-group (%d), got N=%d split_k=%d", who, kNTile, kg, N, split_k);
+      if (tile_split_bytes(M, N, split_k) > sc.partial_bytes)
+        return fail(W4A8_ESCRATCH, "%s: tile split_k=%d needs %zu B of partials; %s holds %zu B",
+                    who, split_k, tile_split_bytes(M, N, split_k), sc.what, sc.partial_bytes);
+      return hip_status(launch_tile(g, variant, kernel == W4A8_KERNEL_TILE_AT, st, sc.partial,
+                                    split_k),
+                        who);
+    }
     return hip_status(launch_tile(g, variant, kernel == W4A8_KERNEL_TILE_AT, st), who);
   }
-  if (kernel == W4A8_KERNEL_RING) {
+  if (kernel == W4A8_KERNEL_RING || kernel == W4A8_KERNEL_RING_AT) {
     if (variant < 0 || variant >= ring_variant_count())
       return fail(W4A8_EINVAL, "%s: ring variant %d out of range", who, variant);
     const DeviceInfo d = device_info(current_device());
     if (!ring_fits(variant, M, N, K, d.cus, d.lds))
       return fail(W4A8_EINVAL, "%s: ring variant %d does not serve M=%d N=%d K=%d", who, variant,
                   M, N, K);
-    return hip_status(launch_ring(g, variant, d.cus, st), who);
+    return hip_status(launch_ring(g, variant, d.cus, kernel == W4A8_KERNEL_RING_AT, st), who);
   }
   if (kernel == W4A8_KERNEL_STREAM) {
     if (variant < 0 || variant >= stream_variant_count())
@@ -424,10 +467,11 @@ int gemm_run(const void* a, const float* as, const void* wq, const void* sq, voi
              int K, int kernel, int variant, int split_k, bool a_tiled, const Scratch& sc,
              const char* who, void* stream) {
   if (int e = check_gemm_shape(who, M, N, K)) return e;
-  a_tiled = a_tiled || kernel == W4A8_KERNEL_TILE_AT;
-  if (a_tiled && kernel != W4A8_KERNEL_AUTO && kernel != W4A8_KERNEL_TILE_AT)
-    return fail(W4A8_EINVAL, "%s: fragment-tiled activations are read by the tile kernel only "
-                "(kernel %d)", who, kernel);
+  a_tiled = a_tiled || kernel == W4A8_KERNEL_TILE_AT || kernel == W4A8_KERNEL_RING_AT;
+  if (a_tiled && kernel != W4A8_KERNEL_AUTO && kernel != W4A8_KERNEL_TILE_AT &&
+      kernel != W4A8_KERNEL_RING_AT)
+    return fail(W4A8_EINVAL, "%s: fragment-tiled activations are read by the tile and ring "
+                "kernels only (kernel %d)", who, kernel);
   if (a_tiled && K % kKTile)
     return fail(W4A8_EINVAL, "%s: fragment-tiled activations need K %% %d == 0, got K=%d", who,
                 kKTile, K);
@@ -437,8 +481,8 @@ int gemm_run(const void* a, const float* as, const void* wq, const void* sq, voi
     const int dev = current_device();
     if (a_tiled) {
       kernel = W4A8_KERNEL_TILE_AT;
-      variant = plan_tile(M, N, dev);
-      split_k = 1;
+      split_k = band_split(M, N, K, device_info(dev).cus, sc, &variant);
+      if (split_k == 1) variant = plan_tile(M, N, dev);
     } else {
       plan_impl(M, N, K, dev, sc, &kernel, &variant, &split_k);
     }
@@ -551,7 +595,7 @@ W4A8_API int w4a8_variant_count(int kernel) {
   if (kernel == W4A8_KERNEL_SKINNY) return skinny_variant_count();
   if (kernel == W4A8_KERNEL_TILE || kernel == W4A8_KERNEL_TILE_AT) return tile_variant_count();
   if (kernel == W4A8_KERNEL_STREAM) return stream_variant_count();
-  if (kernel == W4A8_KERNEL_RING) return ring_variant_count();
+  if (kernel == W4A8_KERNEL_RING || kernel == W4A8_KERNEL_RING_AT) return ring_variant_count();
   fail(W4A8_EINVAL, "w4a8_variant_count: unknown kernel %d", kernel);
   return -1;
 }
@@ -581,7 +625,8 @@ W4A8_API int w4a8_variant_info(int kernel, int variant, int* p0, int* p1, int* p
   } else if (kernel == W4A8_KERNEL_STREAM && variant >= 0 && variant < stream_variant_count()) {
     const StreamCfg c = stream_variant(variant);
     v[0] = c.nt; v[1] = c.kpw; v[2] = c.waves; v[3] = c.u;
-  } else if (kernel == W4A8_KERNEL_RING && variant >= 0 && variant < ring_variant_count()) {
+  } else if ((kernel == W4A8_KERNEL_RING || kernel == W4A8_KERNEL_RING_AT) && variant >= 0 &&
+             variant < ring_variant_count()) {
     const RingCfg c = ring_variant(variant);
     v[0] = c.mf; v[1] = c.nt; v[2] = c.d; v[3] = c.waves;
   } else {
@@ -657,7 +702,11 @@ W4A8_API int w4a8_workspace_bytes(int max_m, int max_n, size_t* partial_bytes,
       const int n = N < max_n ? N : max_n;
       int kernel = 0, variant = 0, split = 1;
       plan_impl(M, n, 1 << 16, dev, kPlanAnySplit, &kernel, &variant, &split);
-      if (kernel != W4A8_KERNEL_SKINNY || split <= 1) continue;
+      if (split <= 1) continue;
+      if (kernel == W4A8_KERNEL_TILE) {       // the band's K split: partials only
+        if (tile_split_bytes(M, n, split) > part) part = tile_split_bytes(M, n, split);
+        continue;
+      }
       const size_t p = skinny_scratch_bytes(variant, n, split);
       const size_t c = (size_t)skinny_counter_count(variant, n) * sizeof(int);
       if (p > part) part = p;

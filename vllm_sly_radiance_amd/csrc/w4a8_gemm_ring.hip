@@ -28,6 +28,9 @@
 //  * The W partial sums of each output meet in LDS, one 16-token fragment at a time, and are
 //    added in wave order (deterministic), scaled by the per-token fp32 scale and stored as bf16.
 //    Nothing crosses workgroups.
+//  * AT: the activations arrive fragment-tiled (16-token blocks, k-tile after k-tile, each
+//    fragment half one contiguous KiB in lane order), so every activation load is a contiguous
+//    1 KiB instead of 16 token rows x 64 bytes; same operands, same bits as the row-major form.
 #include "w4a8_internal.h"
 
 namespace w4a8 {
@@ -37,7 +40,7 @@ constexpr int kOutOfRange = 0x7FFFFFF0;   // an offset past every buffer resourc
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-template <int MF, int NT, int D, int W>
+template <int MF, int NT, int D, int W, bool AT>
 __global__ __launch_bounds__(W * 64) void gemm_ring(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
     const uint32_t* __restrict__ Sq, uint16_t* __restrict__ C, int M, int N, int K, int KT,
@@ -75,7 +78,9 @@ __global__ __launch_bounds__(W * 64) void gemm_ring(
             g0 + r <= glast ? (t * KG + g0 + r) * 256 + lane * 4 : kOutOfRange, 0, 0, 0);
   }
 
-  const auto a_src = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, M * K, kBufferWord3);
+  // tiled: whole 16-token blocks, the last one's padding tokens zero (K % 128 == 0)
+  const int a_bytes = AT ? (M + 15) / 16 * 16 * K : M * K;
+  const auto a_src = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, a_bytes, kBufferWord3);
   const int m = lane & 15, g = lane >> 4;
   // activation offset of fragment f's lane run at k-tile 0, and the k (per lane) from which the
   // lane's low / high run would leave its row: such runs are pointed past the buffer (K % 32 == 0,
@@ -101,10 +106,21 @@ __global__ __launch_bounds__(W * 64) void gemm_ring(
                                                        0, kBufferNT);
 #pragma unroll
     for (int f = 0; f < MF; ++f) {
-      const int lo = kx < lo_end ? a_row[f] + kx : kOutOfRange;
-      const int hi = kx < hi_end ? a_row[f] + kx + 64 : kOutOfRange;
-      xlo[j][f] = __builtin_amdgcn_raw_buffer_load_b128(a_src, lo, 0, 0);
-      xhi[j][f] = __builtin_amdgcn_raw_buffer_load_b128(a_src, hi, 0, 0);
+      if constexpr (AT) {
+        // block f, k-tile kt of the layout's K / 128 (not the weights' padded KT): halves at +0 /
+        // +1 KiB; a k-tile past K would be the next block's tokens, so it reads as zero; blocks
+        // past the last end the buffer and read as zero
+        const int kta = K >> 7;
+        const int base = kt < kta ? (f * kta + kt) * 2048 + lane * 16 : kOutOfRange;
+        xlo[j][f] = __builtin_amdgcn_raw_buffer_load_b128(a_src, base, 0, 0);
+        xhi[j][f] = __builtin_amdgcn_raw_buffer_load_b128(
+            a_src, kt < kta ? base + 1024 : kOutOfRange, 0, 0);
+      } else {
+        const int lo = kx < lo_end ? a_row[f] + kx : kOutOfRange;
+        const int hi = kx < hi_end ? a_row[f] + kx + 64 : kOutOfRange;
+        xlo[j][f] = __builtin_amdgcn_raw_buffer_load_b128(a_src, lo, 0, 0);
+        xhi[j][f] = __builtin_amdgcn_raw_buffer_load_b128(a_src, hi, 0, 0);
+      }
     }
   };
 
@@ -221,7 +237,7 @@ bool ring_fits(int variant, int M, int N, int K, int cus, size_t lds_limit) {
   return small && KT >= c.waves && ring_lds_bytes(variant, K) <= lds_limit;
 }
 
-hipError_t launch_ring(const GemmArgs& g, int variant, int cus, hipStream_t stream) {
+hipError_t launch_ring(const GemmArgs& g, int variant, int cus, bool a_tiled, hipStream_t stream) {
   const int KT = padded_k(g.K) / kKTile, KG = KT / kKGroup;
   const int NTILES = padded_n(g.N) / kNTile;
   const int vec_out = (g.N % 4 == 0 && ((uintptr_t)g.c % 8) == 0) ? 1 : 0;
@@ -229,20 +245,26 @@ hipError_t launch_ring(const GemmArgs& g, int variant, int cus, hipStream_t stre
   const size_t lds = ring_lds_bytes(variant, g.K);
   const int SG = ring_scale_groups(variant, g.K);
   int idx = 0;
-#define W4A8_RING_LAUNCH(mf, nt, d, w)                                                           \
-  if (idx++ == variant) {                                                                        \
+#define W4A8_RING_GO(mf, nt, d, w, at)                                                           \
+  {                                                                                              \
     if (lds > 64 * 1024) {                                                                       \
-      const hipError_t e = hipFuncSetAttribute((const void*)gemm_ring<mf, nt, d, w>,             \
+      const hipError_t e = hipFuncSetAttribute((const void*)gemm_ring<mf, nt, d, w, at>,         \
                                                hipFuncAttributeMaxDynamicSharedMemorySize,       \
                                                (int)lds);                                        \
       if (e != hipSuccess) return e;                                                             \
     }                                                                                            \
-    hipLaunchKernelGGL((gemm_ring<mf, nt, d, w>), grid, block, lds, stream, g.a, g.a_scale, g.wq, \
-                       g.sq, g.c, g.M, g.N, g.K, KT, KG, NTILES, SG, vec_out);                   \
+    hipLaunchKernelGGL((gemm_ring<mf, nt, d, w, at>), grid, block, lds, stream, g.a, g.a_scale,  \
+                       g.wq, g.sq, g.c, g.M, g.N, g.K, KT, KG, NTILES, SG, vec_out);             \
     return hipGetLastError();                                                                    \
+  }
+#define W4A8_RING_LAUNCH(mf, nt, d, w)                                                           \
+  if (idx++ == variant) {                                                                        \
+    if (a_tiled) W4A8_RING_GO(mf, nt, d, w, true)                                               \
+    W4A8_RING_GO(mf, nt, d, w, false)                                                            \
   }
   W4A8_RING_TABLE(W4A8_RING_LAUNCH)
 #undef W4A8_RING_LAUNCH
+#undef W4A8_RING_GO
   return hipErrorInvalidValue;
 }
 

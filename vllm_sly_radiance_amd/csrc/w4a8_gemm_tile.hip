@@ -115,11 +115,17 @@ constexpr bool ring_slots_hold() {
 static_assert(ring_slots_hold(), "scale ring: NS < 4 R - 6");
 
 // The kernel body; the two entry points below differ only in the order of their arguments.
-template <int WM, int WN, int NS, int NW, bool AT>
+// SPLIT: K split over workgroup rows. Row blockIdx.y = s of `splits` covers the k-groups
+// [KG s / splits, KG (s + 1) / splits) and writes its unscaled fp32 sums to P[s][M][N] (N % 16 == 0);
+// split_reduce adds them in split order, scales and rounds. A compile-time switch: the unsplit
+// kernels keep exactly their own code (a run-time k-range cost the 256 x 256 tile 20 spilled
+// registers and 28 % of its speed).
+template <int WM, int WN, int NS, int NW, bool AT, bool SPLIT>
 __device__ __forceinline__ void tile_body(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
     const uint32_t* __restrict__ Sq, uint16_t* __restrict__ C, int M, int N, int K, int KTp,
-    int KTe, int KG, int NTILES, int grid_m, int grid_n, int ldc, int vec_out) {
+    int KTe, int KG, int NTILES, int grid_m, int grid_n, int ldc, int vec_out,
+    float* __restrict__ P, int splits) {
   using S = TileShape<WM, WN, NW>;
   static_assert(NS >= 2 && NS <= 16 && (NS - 1) * (S::OPS + 1) < 64, "pipeline depth");
   constexpr int RING = ring_slots(NS);
@@ -144,6 +150,12 @@ __device__ __forceinline__ void tile_body(
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;      // (NW / 2) x 2 waves
+
+  // this workgroup's slabs: whole k-groups [kt0, kt1); fills at or past kend read zero
+  const int split = SPLIT ? (int)blockIdx.y : 0;
+  const int kt0 = SPLIT ? 4 * (KG * split / splits) : 0;
+  const int kt1 = SPLIT ? 4 * (KG * (split + 1) / splits) : (KTe + 3) & ~3;
+  const int kend = SPLIT ? min(kt1, KTe) : KTe;
 
   // buffer resources: activations (all M x K; tiled: whole 16-token blocks), this tile's weight
   // granules and scale dwords
@@ -172,7 +184,7 @@ __device__ __forceinline__ void tile_body(
 
   // Fill op o of slab kt into stage base: an activation unit (o < A_PER_WAVE) or a weight granule.
   auto fill_op = [&](int kt, uint8_t* base, int o) {
-    const bool kin = kt < KTe;
+    const bool kin = kt < kend;
     if (o < S::A_PER_WAVE) {
       const int unit = wave * S::A_PER_WAVE + o;
       int off;
@@ -256,14 +268,13 @@ __device__ __forceinline__ void tile_body(
                                                0, 0, 0);
   }
 
-  // k-group 0's scale unit goes out first, so the wait for slab 0 covers it too
-  fill_scales(0);
+  // the first k-group's scale unit goes out first, so the wait for the first slab covers it too
+  fill_scales(kt0 >> 2);
 
   // The k-loops run whole k-groups (4 slabs, the last group padded with zero slabs: the weight
   // stripes are padded to whole k-groups and activations past K fill zeros), unrolled so that
   // every slab knows at compile time whether its refill carries a scale unit, and so how many
   // fills its wait may leave in flight.
-  const int KT4 = (KTe + 3) & ~3;
 
   if constexpr (WM >= 3) {
     // ---- NS-stage pipeline, barrier two MFMA groups before the end of each slab. At the
@@ -277,12 +288,12 @@ __device__ __forceinline__ void tile_body(
     constexpr int R = WM >= 4 ? ((NW == 8 && WN >= 8) ? 2 : 3) : 2;
     constexpr int P = WM - R;
 #pragma unroll
-    for (int p = 0; p < NS; ++p) fill(p, p);
-    wait_vmcnt<S::fills_after(0, NS - 1)>();     // slab 0 (and k-group 0's scales) have landed
+    for (int p = 0; p < NS; ++p) fill(kt0 + p, p);
+    wait_vmcnt<S::fills_after(0, NS - 1)>();     // the first slab and its scales have landed
     bare_barrier();
     v4i wf[WN], lo, hi;
     uint32_t sc[WN];
-    read_w(0, 0, wf, sc);
+    read_w(0, kt0, wf, sc);
     read_a(0, 0, lo, hi);
     __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0): the loop starts with nothing pending
     int st = 0;
@@ -355,7 +366,7 @@ __device__ __forceinline__ void tile_body(
       hi = hin;
       st = nst;
     };
-    for (int kt = 0; kt < KT4; kt += 4) {
+    for (int kt = kt0; kt < kt1; kt += 4) {
       slab(kt, IntC<0>{});
       slab(kt + 1, IntC<1>{});
       slab(kt + 2, IntC<2>{});
@@ -366,7 +377,7 @@ __device__ __forceinline__ void tile_body(
     //      shares between the MFMA groups of slab kt; fragment i+1 is read before fragment i's
     //      MFMAs, and scheduling barriers keep the compiler from sinking either below them ----
 #pragma unroll
-    for (int p = 0; p < NS - 1; ++p) fill(p, p);
+    for (int p = 0; p < NS - 1; ++p) fill(kt0 + p, p);
     int st = 0;
     auto slab = [&](int kt, auto qc) {
       constexpr int q = decltype(qc)::value;    // kt % 4
@@ -394,7 +405,7 @@ __device__ __forceinline__ void tile_body(
       }
       st = st + 1 == NS ? 0 : st + 1;
     };
-    for (int kt = 0; kt < KT4; kt += 4) {
+    for (int kt = kt0; kt < kt1; kt += 4) {
       slab(kt, IntC<0>{});
       slab(kt + 1, IntC<1>{});
       slab(kt + 2, IntC<2>{});
@@ -402,6 +413,22 @@ __device__ __forceinline__ void tile_body(
     }
   }
   wait_vmcnt<0>();                               // no fill may outlive the workgroup's LDS
+
+  if constexpr (SPLIT) {
+    // split K: this k-range's unscaled sums, 4 consecutive columns of one token per lane
+    float* const ps = P + (size_t)split * M * N;
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+      const int m = m0 + (wm * WM + i) * 16 + (lane & 15);
+      if (m >= M) continue;
+#pragma unroll
+      for (int j = 0; j < WN; ++j) {
+        const int n = (nt_base + wn * WN + j) * kNTile + 4 * (lane >> 4);
+        if (n < N) *reinterpret_cast<v4f*>(ps + (size_t)m * N + n) = acc[i][j];
+      }
+    }
+    return;
+  }
 
   float tsc[WM];
 #pragma unroll
@@ -462,8 +489,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
     const uint32_t* __restrict__ Sq, uint16_t* __restrict__ C, int M, int N, int K, int KTp,
     int KTe, int KG, int NTILES, int grid_m, int grid_n, int ldc, int vec_out) {
-  tile_body<WM, WN, NS, NW, AT>(A, As, Wq, Sq, C, M, N, K, KTp, KTe, KG, NTILES, grid_m, grid_n,
-                                ldc, vec_out);
+  tile_body<WM, WN, NS, NW, AT, false>(A, As, Wq, Sq, C, M, N, K, KTp, KTe, KG, NTILES, grid_m,
+                                       grid_n, ldc, vec_out, nullptr, 1);
 }
 
 template <int WM, int WN, int NS, int NW, bool AT>
@@ -471,8 +498,20 @@ __global__ __launch_bounds__(NW * 64) void gemm_tile_pre(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
     const uint32_t* __restrict__ Sq, int M, int K, int KTp, int NTILES, int grid_m, int grid_n,
     int N, int ldc, int vec_out, uint16_t* __restrict__ C) {
-  tile_body<WM, WN, NS, NW, AT>(A, As, Wq, Sq, C, M, N, K, KTp, ceil_div(K, kKTile),
-                                KTp / kKGroup, NTILES, grid_m, grid_n, ldc, vec_out);
+  tile_body<WM, WN, NS, NW, AT, false>(A, As, Wq, Sq, C, M, N, K, KTp, ceil_div(K, kKTile),
+                                       KTp / kKGroup, NTILES, grid_m, grid_n, ldc, vec_out,
+                                       nullptr, 1);
+}
+
+// The K-split form of the 4-wave band tiles (WM <= 2): the preloaded argument order of
+// gemm_tile_pre, then the partials and the split count.
+template <int WM, int WN, int NS, int NW, bool AT>
+__global__ __launch_bounds__(NW * 64) void gemm_tile_split(
+    const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
+    const uint32_t* __restrict__ Sq, int M, int K, int KTp, int NTILES, int grid_m, int grid_n,
+    int N, int splits, float* __restrict__ P) {
+  tile_body<WM, WN, NS, NW, AT, true>(A, As, Wq, Sq, nullptr, M, N, K, KTp, ceil_div(K, kKTile),
+                                      KTp / kKGroup, NTILES, grid_m, grid_n, N, 0, P, splits);
 }
 
 
@@ -498,6 +537,8 @@ constexpr int kTileCount = sizeof(kTile) / sizeof(kTile[0]);
 }  // namespace
 
 int tile_variant_count() { return kTileCount; }
+bool tile_splits(int v) { return kTile[v].nw == 4 && kTile[v].wm <= 2; }
+size_t tile_split_bytes(int M, int N, int splits) { return (size_t)splits * M * N * sizeof(float); }
 TileCfg tile_variant(int v) { return kTile[v]; }
 
 bool tile_fits(int M, int N, int K) {
@@ -507,7 +548,28 @@ bool tile_fits(int M, int N, int K) {
          (long)16 * padded_k(K) / 2 * 16 < (1L << 31) && (long)N < (1L << 24);
 }
 
-hipError_t launch_tile(const GemmArgs& g, int variant, bool a_tiled, hipStream_t stream) {
+hipError_t launch_tile_body(const GemmArgs& g, int variant, bool a_tiled, hipStream_t stream,
+                            float* P, int splits, int KTp, int KTe, int KG, int NTILES,
+                            int grid_m, int grid_n, int vec_out, dim3 grid, dim3 block);
+
+// Adds the `splits` fp32 partial sums P[s][M][N] of a split-K tile launch in split order, scales
+// by the per-token scale and stores bf16: one thread per 4 consecutive columns of one token.
+__global__ __launch_bounds__(256) void split_reduce(const float* __restrict__ P,
+                                                    const float* __restrict__ As,
+                                                    uint16_t* __restrict__ C, int M, int N,
+                                                    int ldc, int splits, int vec_out) {
+  const int n4 = N >> 2;
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (long)M * n4) return;
+  const int m = (int)(idx / n4), n = 4 * (int)(idx - (long)m * n4);
+  const size_t plane = (size_t)M * N, at = (size_t)m * N + n;
+  v4f v = *reinterpret_cast<const v4f*>(P + at);
+  for (int s = 1; s < splits; ++s) v += *reinterpret_cast<const v4f*>(P + s * plane + at);
+  store_out4(C, ldc, m, n, N, v, As[m], vec_out != 0);
+}
+
+hipError_t launch_tile(const GemmArgs& g, int variant, bool a_tiled, hipStream_t stream,
+                       float* partial, int splits) {
   const TileCfg c = kTile[variant];
   const int KTp = padded_k(g.K) / kKTile, KTe = ceil_div(g.K, kKTile), KG = KTp / kKGroup;
   const int NTILES = padded_n(g.N) / kNTile;
@@ -516,18 +578,45 @@ hipError_t launch_tile(const GemmArgs& g, int variant, bool a_tiled, hipStream_t
   const int vec_out = (g.N % 8 == 0 && g.ldc % 8 == 0 && ((uintptr_t)g.c % 16) == 0)  ? 2
                       : (g.N % 4 == 0 && g.ldc % 4 == 0 && ((uintptr_t)g.c % 8) == 0) ? 1
                                                                                          : 0;
-  const dim3 grid(grid_m * grid_n), block(c.nw * 64);
+  float* const P = splits > 1 ? partial : nullptr;
+  const dim3 grid(grid_m * grid_n, P ? splits : 1), block(c.nw * 64);
+  if (P) {
+    // the partial launch, then the reduction on the same stream
+    const hipError_t e = launch_tile_body(g, variant, a_tiled, stream, P, splits, KTp, KTe, KG,
+                                          NTILES, grid_m, grid_n, vec_out, grid, block);
+    if (e != hipSuccess) return e;
+    const long threads = (long)g.M * (g.N / 4);
+    hipLaunchKernelGGL(split_reduce, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
+                       P, g.a_scale, g.c, g.M, g.N, g.ldc, splits,
+                       (g.ldc % 4 == 0 && ((uintptr_t)g.c % 8) == 0) ? 1 : 0);
+    return hipGetLastError();
+  }
+  return launch_tile_body(g, variant, a_tiled, stream, nullptr, 1, KTp, KTe, KG, NTILES, grid_m,
+                          grid_n, vec_out, grid, block);
+}
+
+hipError_t launch_tile_body(const GemmArgs& g, int variant, bool a_tiled, hipStream_t stream,
+                            float* P, int splits, int KTp, int KTe, int KG, int NTILES,
+                            int grid_m, int grid_n, int vec_out, dim3 grid, dim3 block) {
   int idx = 0;
 #define W4A8_TILE_GO(wm, wn, ns, nw, at)                                                         \
   {                                                                                              \
-    if constexpr (nw == 8 || wm > 2)                                                             \
+    if (P) {                                                                                     \
+      if constexpr (nw == 4 && wm <= 2)                                                          \
+        hipLaunchKernelGGL((gemm_tile_split<wm, wn, ns, nw, at>), grid, block, 0, stream, g.a,   \
+                           g.a_scale, g.wq, g.sq, g.M, g.K, KTp, NTILES, grid_m, grid_n, g.N,   \
+                           splits, P);                                                           \
+      else                                                                                       \
+        return hipErrorInvalidValue;                                                             \
+    } else if constexpr (nw == 8 || wm > 2) {                                                    \
       hipLaunchKernelGGL((gemm_tile<wm, wn, ns, nw, at>), grid, block, 0, stream, g.a,           \
                          g.a_scale, g.wq, g.sq, g.c, g.M, g.N, g.K, KTp, KTe, KG, NTILES, grid_m, \
                          grid_n, g.ldc, vec_out);                                                \
-    else                                                                                         \
+    } else {                                                                                     \
       hipLaunchKernelGGL((gemm_tile_pre<wm, wn, ns, nw, at>), grid, block, 0, stream, g.a,       \
                          g.a_scale, g.wq, g.sq, g.M, g.K, KTp, NTILES, grid_m, grid_n, g.N,     \
                          g.ldc, vec_out, g.c);                                                   \
+    }                                                                                            \
     return hipGetLastError();                                                                    \
   }
 #define W4A8_TILE_LAUNCH(wm, wn, ns, nw)                                                       \

@@ -158,7 +158,8 @@ RingCfg ring_variant(int v);
 int ring_grid(int variant, int N, int cus);
 size_t ring_lds_bytes(int variant, int K);
 bool ring_fits(int variant, int M, int N, int K, int cus, size_t lds_limit);
-hipError_t launch_ring(const GemmArgs& g, int variant, int cus, hipStream_t stream);
+hipError_t launch_ring(const GemmArgs& g, int variant, int cus, bool a_tiled,
+                       hipStream_t stream);
 
 // Macro-tile family (M > 16). variant indexes the instantiated (WM, WN, NS, NW) table: nw waves of
 // wm x wn 16 x 16 MFMA tiles, a bm x bn workgroup tile.
@@ -167,7 +168,12 @@ int tile_variant_count();
 TileCfg tile_variant(int v);
 bool tile_fits(int M, int N, int K);
 // a_tiled: the activations are fragment-tiled (16-token blocks; K a multiple of 128)
-hipError_t launch_tile(const GemmArgs& g, int variant, bool a_tiled, hipStream_t stream);
+// splits > 1: K split over `splits` workgroup rows into fp32 partials [splits][M][N] (N % 16 == 0),
+// then a reducing launch on the same stream
+hipError_t launch_tile(const GemmArgs& g, int variant, bool a_tiled, hipStream_t stream,
+                       float* partial = nullptr, int splits = 1);
+size_t tile_split_bytes(int M, int N, int splits);
+bool tile_splits(int variant);   // the variant has a K-split form (4-wave tiles, WM <= 2)
 
 // Register-resident MFMA throughput probe (shape 0: 16x16x128, 1: 32x32x64).
 hipError_t launch_read_probe(const void* buf, int bytes, int* out, hipStream_t stream);
