@@ -669,16 +669,18 @@ def bench_sweep(n_layers):
 
 
 CALIBRATION_BYTES = 256 * 2 ** 20
-# decode-band GEMMs in the counter runs: gate_up and down at M = 32 and 64
-BAND_PROFILE = [(32, 17408, 5120), (64, 17408, 5120), (32, 5120, 8704), (64, 5120, 8704)]
+# decode-band GEMMs in the counter runs: gate_up at M = 32 and 64, down at M = 17, 32, 48 and 64
+# (the plan splits down's K three ways up to M = 48)
+BAND_PROFILE = [(32, 17408, 5120), (64, 17408, 5120), (17, 5120, 8704), (32, 5120, 8704),
+                (48, 5120, 8704), (64, 5120, 8704)]
 
 
 def profile_workload():
     """The launches the committed rocprofv3 summaries are taken on: the verify GEMM (the bench's
     graph replay: one second of warmup replays, then 64 timed launches over 16 weight copies,
     plus 64 event-bracketed single launches), each prefill GEMM (4 launches, then 4 more on
-    fragment-tiled q behind its fused producer), gate_up and down
-    at M = 32 and 64 (8 launches over 4 weight copies each), the four linears of the M = 1 layer
+    fragment-tiled q behind its fused producer), gate_up at M = 32 and 64 and down at M = 17, 32,
+    48 and 64 (8 launches over 4 weight copies each), the four linears of the M = 1 layer
     set on bf16 activations as the op runs them (8 launches over 4 weight copies each), each fused
     producer and the quantizer at M = 4096 (4 launches over 2 input copies each) and a plain
     256 MiB device copy
