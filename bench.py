@@ -248,10 +248,27 @@ def bench_prefill():
     return res
 
 
+class SiluLinear:
+    """The MLP's tail as radiance::silu_mul_mxfp4_linear runs it: gate_up bf16 [M, 2K] in, the
+    down projection of silu(gate) * up out (w4a8_silu_mul_linear: one launch where
+    w4a8_silu_mul_linear_fused says so, else the SiLU-mul producer and the GEMM)."""
+
+    def __init__(self, g, prod):
+        self.g, self.p, self.w = g, prod, g.w
+
+    def launch(self, i, stream):
+        g, p = self.g, self.p
+        g._native.silu_mul_linear(p.w[i].data_ptr(), p.q.data_ptr(), p.s.data_ptr(),
+                                  g.w[i].data_ptr(), g.ws[i].data_ptr(), g.out.data_ptr(), g.M,
+                                  g.N, g.K, stream)
+
+
 def bench_layer_m1():
     """The four linears of one layer at M = 1: the GEMM on pre-quantized activations (`us`), and
     the linear on bf16 activations as the op runs it (`linear_us`: one launch with the quantizer
-    inside where `one_launch`, else quantizer + GEMM)."""
+    inside where `one_launch`, else quantizer + GEMM). For down also the MLP's tail from the
+    gate_up output: SiLU-and-mul + down in one op (`silu_down_us`) against the SiLU-mul producer
+    followed by the GEMM (`silu_then_down_us`)."""
     import torch
     out, tot_us, tot_lin, tot_bytes = [], 0.0, 0.0, 0
     for name, N, K in LAYER_M1:
@@ -269,6 +286,16 @@ def bench_layer_m1():
                         gbs=round(nb / (us * 1e-6) / 1e9, 1), plan=g.plan,
                         linear_us=round(lin, 2),
                         one_launch=bool(g._native.linear_fused(1, N, K, K))))
+        if name == "down":
+            prod = Producer("silu", 1, K, copies, seed=41)
+            sec, _, _, _ = graph_timed(SiluLinear(g, prod), 32 * copies, 4 * copies,
+                                       warm_seconds=0.2)
+            out[-1]["silu_down_us"] = round(sec / (32 * copies) * 1e6, 2)
+            out[-1]["silu_down_one_launch"] = bool(g._native.silu_mul_linear_fused(1, N, K))
+            pg = ProducerGemm("silu", 1, N, K, copies, 41, 0)
+            sec, _, _, _ = graph_timed(pg, 32 * copies, 4 * copies, warm_seconds=0.2)
+            out[-1]["silu_then_down_us"] = round(sec / (32 * copies) * 1e6, 2)
+            del prod, pg
         del g
         torch.cuda.empty_cache()
     return dict(layers=out, us_per_layer=round(tot_us, 2),
