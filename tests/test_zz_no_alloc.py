@@ -59,8 +59,10 @@ def run(fn, op, kernel=_native.KERNEL_AUTO, variant=-1, split=0):
 
 
 # (M, N, K) pairs: first call, then a smaller one. 65 and 33 n-tiles plan split-K on the skinny
-# kernel; N = 2048, K = 5120 plans the streaming kernel (no scratch).
-CASES = [((8, 1040, 2560), (3, 528, 1024)), ((16, 2048, 5120), (5, 1040, 2560))]
+# kernel; N = 2048, K = 5120 plans the streaming kernel (no scratch); down-shaped K = 8704 at
+# M = 32 and 17 plans the tile kernel with K split three ways (fp32 partials in the scratch).
+CASES = [((8, 1040, 2560), (3, 528, 1024)), ((16, 2048, 5120), (5, 1040, 2560)),
+         ((32, 5120, 8704), (17, 1024, 8704))]
 
 
 @pytest.mark.parametrize("first,second", CASES)
@@ -100,5 +102,17 @@ def test_noalloc_refuses_a_split_beyond_its_static_scratch(registered):
     v = [i for i, c in enumerate(_native.variants(SKINNY)) if c[:3] == (1, 1, 16)][0]
     p = 1 << 20
     rc = _native.lib().w4a8_gemm_noalloc(p, p, p, p, p, 8, 36864, 5120, SKINNY, v, 16, None)
+    assert rc == 2
+    assert b"static scratch" in _native.lib().w4a8_last_error()
+
+
+def test_noalloc_refuses_a_tile_split_beyond_its_static_scratch(registered):
+    """A forced three-way K split of the 64 x 64 band tile at M = 48, N = 16384 needs 9.4 MB of
+    partials: refused before any launch."""
+    v = [i for i, c in enumerate(_native.variants(_native.KERNEL_TILE))
+         if c[2:] == (64, 64) and _native.tile_config(i)["stages"] == 5][0]
+    p = 1 << 20
+    rc = _native.lib().w4a8_gemm_noalloc(p, p, p, p, p, 48, 16384, 8704, _native.KERNEL_TILE, v,
+                                         3, None)
     assert rc == 2
     assert b"static scratch" in _native.lib().w4a8_last_error()
