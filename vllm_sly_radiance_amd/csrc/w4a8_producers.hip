@@ -108,6 +108,13 @@ __global__ __launch_bounds__(kThreads) void add_rms_quant(
   res_out += (size_t)row * nv;
   float v[G][8];
   float part = 0.0f;
+  // the weight groups are requested with the row, so no load waits behind the row's reduction
+  uint4 wv[G];
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int g = tid + i * kThreads;
+    wv[i] = g < nv ? w[g] : make_uint4(0, 0, 0, 0);
+  }
 #pragma unroll
   for (int i = 0; i < G; ++i) {
     const int g = tid + i * kThreads;
@@ -130,7 +137,7 @@ __global__ __launch_bounds__(kThreads) void add_rms_quant(
     const int g = tid + i * kThreads;
     if (g < nv) {
       float wf[8], n[8];
-      unpack8(w[g], wf);
+      unpack8(wv[i], wf);
 #pragma unroll
       for (int j = 0; j < 8; ++j) n[j] = (v[i][j] * inv) * (wf[j] + 1.0f);
       nb[i] = pack8_hw(n);
