@@ -87,7 +87,8 @@ int w4a8_quant_per_token(const void* x, long ldx, void* q, float* scale, int M, 
  * make_row_ref, permute_w, psw_pack_w_, psw_fold_ws (sly/mxfp4/radiance_mxfp4.py:1083-1171). */
 int w4a8_repack(const void* w, const void* ws, void* wq, void* sq, int N, int K, void* stream);
 
-/* Register caller-owned split-K scratch for the current device: fp32 partials and int counters.
+/* Register caller-owned split-K scratch for the current device: fp32 partials (the skinny kernel's
+ * split-K and the macro tiles' K split in the decode band) and int counters (the skinny kernel's).
  * The counters must be zeroed once by the caller; the kernel's last-arriving workgroup resets each
  * counter it used, so they stay zeroed. Launches that overlap on one device race on it. Replaces
  * set_decode_scratch (sly/mxfp4/radiance_mxfp4_fp8.hip:1356-1360, registered from
