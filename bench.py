@@ -244,6 +244,9 @@ def bench_prefill():
             del g
             torch.cuda.empty_cache()
         row["producer"] = PREFILL_PRODUCER[name]
+        util = measured_mfma_util(f"prefill_{name}")
+        if util is not None:
+            row["mfma_util"] = util
         res.append(row)
     return res
 
@@ -776,6 +779,22 @@ def measured_traffic(kernel_prefix):
             t = json.load(f)
         k = t["kernels"][kernel_prefix]
         return int(round(k["fetch_bytes"] + k["write_bytes"]))
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def measured_mfma_util(kernel_key):
+    """MFMA-busy fraction (SQ_VALU_MFMA_BUSY_CYCLES over active cycles, rocprofv3) of a prefill
+    GEMM's two launches and the clock they ran at, from the committed counter summary, or None:
+    counters need their own profiler run, so the bench reports the committed measurement."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            k = json.load(f)["kernels"][kernel_key]
+        return dict(main=k["mfma_util_main"], tail=k["mfma_util_tail"],
+                    clock_ghz_main=k["clock_ghz_main"],
+                    source="profiles/traffic.json (rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES "
+                           "GRBM_GUI_ACTIVE)")
     except (OSError, KeyError, ValueError):
         return None
 
