@@ -569,8 +569,8 @@ def test_gemm_tile_k_split(gpu_lib, scratch, M, N, K):
 
 def test_band_split_plan_for_down(gpu_lib):
     """With the plugin's scratch registered, the automatic plan splits down (5120 x 8704) three
-    ways at M = 17..48 on the 32 x 64 (8-stage) / 64 x 64 (5-stage) tiles, not at M = 64, and no
-    other BASELINE shape."""
+    ways at M = 17..48 on the 32 x 64 (8-stage) / 64 x 64 (5-stage) tiles, not at M = 64; o_proj
+    (5120 x 6144, 12 k-groups) at M = 17..20 only; never qkv or gate_up."""
     from vllm_sly_radiance_amd import radiance_mxfp4 as R
     R.ensure_scratch("cuda")
     assert _native.plan(64, 5120, 8704)[2] == 1
@@ -579,8 +579,10 @@ def test_band_split_plan_for_down(gpu_lib):
         want = (32, 64, 8) if M <= 32 else (64, 64, 5)
         c = _native.tile_config(v)
         assert (k, sp, c["bm"], c["bn"], c["stages"]) == (TILE, 3, *want), (M, k, v, sp, c)
-        for N, K in ((10240, 5120), (5120, 6144), (17408, 5120)):
+        for N, K in ((10240, 5120), (17408, 5120)):
             assert _native.plan(M, N, K)[2] == 1, (M, N, K)
+        assert _native.plan(M, 5120, 6144)[2] == (3 if M <= 20 else 1), M
+    assert _native.plan(20, 5120, 6144)[2] == 3 and _native.plan(21, 5120, 6144)[2] == 1
 
 
 # ---- diagnostics --------------------------------------------------------------------------------

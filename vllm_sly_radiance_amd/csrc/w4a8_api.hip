@@ -270,13 +270,14 @@ int plan_tile(int M, int N, int dev);
 // CUs fetches; splitting K three ways cuts that panel to a third at the cost of the reducing
 // launch (~1.5-2 us). Measured on MI355X (graph replays over rotating weights, us, plan before ->
 // split): down N=5120 K=8704 at M = 17 / 32 / 48 / 64: 11.2 -> 9.0, 11.2 -> 9.9, 12.8 -> 11.5,
-// 13.0 -> 12.4 (within the spread between boxes at 64); o_proj K=6144 (12 k-groups) gains at
-// M = 17 only and loses above, and the shapes whose unsplit grid covers most CUs (qkv, gate_up)
-// lose at every split. So: up to 48 tokens, three splits of at least 5 k-groups each, when the
-// unsplit grid would leave at least half of the CUs idle and three times it fits one round, with
-// 32 x 64 tiles (8 stages) up to 32 tokens and 64 x 64 (5 stages) above, and only when the scratch
-// holds the partials. Returns the split (1: none).
-constexpr int kBandSplit = 3, kBandSplitMaxM = 48;
+// 13.0 -> 12.4 (within the spread between boxes at 64); o_proj K=6144 (12 k-groups) 8.25 -> 7.67
+// at M = 17 and 8.25 -> 7.92 at 20, 2 % at 24 and nothing above; the shapes whose unsplit grid
+// covers most CUs (qkv, gate_up) lose at every split. So: three splits of at least 5 k-groups
+// each up to 48 tokens, or of 4 k-groups up to 20, when the unsplit grid would leave at least half
+// of the CUs idle and three times it fits one round, with 32 x 64 tiles (8 stages) up to 32
+// tokens and 64 x 64 (5 stages) above, and only when the scratch holds the partials. Returns the
+// split (1: none).
+constexpr int kBandSplit = 3, kBandSplitMaxM = 48, kBandSplitShortK = 20;
 
 int band_split(int M, int N, int K, int cus, const Scratch& sc, int* variant) {
   if (M <= 16 || M > kBandSplitMaxM || N % kNTile) return 1;
@@ -285,7 +286,8 @@ int band_split(int M, int N, int K, int cus, const Scratch& sc, int* variant) {
   const TileCfg c = tile_variant(v);
   const long grid = (long)ceil_div(M, c.bm) * ceil_div(N, c.bn);
   const int kg = padded_k(K) / (kKTile * kKGroup);
-  if (2 * grid > cus || grid * kBandSplit > cus || kg < 5 * kBandSplit ||
+  const int kg_min = (M <= kBandSplitShortK ? 4 : 5) * kBandSplit;
+  if (2 * grid > cus || grid * kBandSplit > cus || kg < kg_min ||
       tile_split_bytes(M, N, kBandSplit) > sc.partial_bytes || !tile_fits(M, N, K))
     return 1;
   *variant = v;
