@@ -117,6 +117,38 @@ def test_hip_graph_capture_and_replay(kernel, M):
         _ = (x.float() * 2).sum().item()          # unrelated eager work between replays
 
 
+def test_hip_graph_capture_of_the_band_k_split(kernel):
+    """down (5120 x 8704) at M = 24 runs the quantizer, the tile kernel's K-split launch into the
+    registered scratch and the reducing launch: captured into a HIP graph, every replay (with eager
+    work and syncs in between, and an eager call of another shape reusing the scratch) matches the
+    eager result."""
+    M, N, K = 24, 5120, 8704
+    w, ws = synthetic.weights(N, K, seed=12)
+    layer = Layer(w, ws)
+    kernel.process_weights_after_loading(layer)
+    assert _native.plan(M, N, K)[2] == 3, "the band's K split is what this test captures"
+    x = bf16_dev(synthetic.activations(M, K, seed=13))
+    x2 = bf16_dev(synthetic.activations(40, K, seed=14))
+    eager = kernel.apply_weights(layer, x)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            kernel.apply_weights(layer, x)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y = kernel.apply_weights(layer, x)
+    for i in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager), f"replay {i}"
+        kernel.apply_weights(layer, x2)           # another split call between the replays
+        torch.cuda.synchronize()
+    assert R._scratch[0] is not None
+
+
 def test_checkpoint_ingestion_end_to_end(kernel, tmp_path):
     """A merged gate/up linear read from a sharded safetensors checkpoint, repacked in place by
     process_weights_after_loading and applied: equal to the oracle on the concatenated tensors."""
