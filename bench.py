@@ -456,19 +456,58 @@ class ReadProbe:
         self._native.read_probe(self.w[i].data_ptr(), self.n, self.out.data_ptr(), stream)
 
 
+class ReadShape:
+    """A ReadProbe's buffers read by w4a8_read_probe_shape: `blocks` workgroups of one variant."""
+
+    def __init__(self, probe, blocks, variant):
+        self.p, self.w, self.blocks, self.variant = probe, probe.w, blocks, variant
+
+    def launch(self, i, stream):
+        p = self.p
+        p._native.read_probe_shape(p.w[i].data_ptr(), p.n, p.out.data_ptr(), self.blocks,
+                                   self.variant, stream)
+
+
+# (workgroups, read-probe variant) pairs of the launch-shape sweep over the verify GEMM's bytes:
+# the GEMM's own grid (218 workgroups of 10 waves) and the 233-234 of the plain probe, fewer
+# workgroups with more bytes each (136-182), grids that give every CU equal bytes (256) with 4-16
+# waves, 12-46 KiB per wave, all loads issued at once or a window of 4-12 in flight, non-temporal
+# or not, and two or four workgroups per CU
+READ_SWEEP = [(234, 0), (218, 1), (136, 18), (160, 17), (182, 16), (240, 0), (248, 0), (256, 0),
+              (256, 2), (256, 3), (256, 4), (256, 5), (256, 6), (256, 7), (256, 8), (256, 9),
+              (256, 10), (256, 14), (256, 15), (512, 11), (512, 13), (1013, 12)]
+
+
 def bench_read_probe(steps, warmup):
     """The HBM read ceiling for the verify GEMM: as many bytes per launch as its algorithmic
     traffic, the same rotation over 16 copies and the same timing (direct launches behind the
-    graph warm-up), nothing but reads."""
+    graph warm-up), nothing but reads. First the fixed probe (the GEMM's launch shape), then the
+    launch-shape sweep (READ_SWEEP, 256 launches each), whose fastest shape is the ceiling the
+    GEMM is held against."""
     import torch
-    g = ReadProbe(gemm_bytes(VERIFY["M"], VERIFY["N"], VERIFY["K"]), COPIES)
+    nbytes = gemm_bytes(VERIFY["M"], VERIFY["N"], VERIFY["K"])
+    g = ReadProbe(nbytes, COPIES)
     sec, _, _, _ = graph_timed(g, steps, warmup, warm_seconds=0.5, direct=True)
     us = sec / steps * 1e6
     gbs = g.n / (us * 1e-6) / 1e9
+    res = dict(bytes=nbytes, us=round(us, 3), gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4))
+    variants = g._native.read_probe_variants()
+    shapes = []
+    for blocks, v in READ_SWEEP:
+        waves, units, window, nt = variants[v]
+        sec, _, _, _ = graph_timed(ReadShape(g, blocks, v), 256, 16, warm_seconds=0.2,
+                                   direct=True)
+        us_s = sec / 256 * 1e6
+        shapes.append(dict(blocks=blocks, waves=waves, kib_per_wave=units, in_flight=window,
+                           nontemporal=bool(nt), us=round(us_s, 3),
+                           gbs=round(nbytes / (us_s * 1e-6) / 1e9, 1)))
+        print(f"[bench] read sweep {shapes[-1]}", file=sys.stderr, flush=True)
+    best = min(shapes, key=lambda r: r["us"])
+    res["sweep"] = shapes
+    res["best"] = dict(best, frac=round(best["gbs"] / HBM_PEAK_GBS, 4))
     del g
     torch.cuda.empty_cache()
-    return dict(bytes=gemm_bytes(VERIFY["M"], VERIFY["N"], VERIFY["K"]), us=round(us, 3),
-                gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4))
+    return res
 
 
 def mfma_probe():
@@ -490,30 +529,71 @@ def mfma_probe():
     return res
 
 
+# the CPU baseline's configurations: (name, M, N, K, reps); reps 1 for the M = 4096 calls
+CPU_CONFIGS = [("plumbing", 8, 5120, 5120, 5), ("verify", 8, 17408, 5120, 5),
+               ("layer_qkv", 1, 10240, 5120, 5), ("layer_o_proj", 1, 5120, 6144, 5),
+               ("layer_gate_up", 1, 17408, 5120, 5), ("layer_down", 1, 5120, 8704, 5),
+               ("prefill_gate_up", 4096, 17408, 5120, 1), ("prefill_down", 4096, 5120, 8704, 1)]
+# one layer of the 64-layer sweep at the M the other rows do not cover
+CPU_SWEEP_M = [16, 64, 512]
+
+
 def cpu_baseline():
-    """The oracle's dequant + fp32 matmul (the reference's _exact_ref path restated) on this host's
-    cores, on the verify-decode workload itself, bytes counted as for the GPU."""
-    from threadpoolctl import threadpool_limits
-    from oracle import mxfp4_oracle as O
+    """The reference's CPU path, _exact_ref's dequant + fp32 matmul (sly/mxfp4/radiance_mxfp4.py:
+    507-527) with _traced_quant in front (:392-396), restated in torch (oracle/torch_ref.py) and
+    timed on this host's cores: quant, dequant and matmul separately, median of `reps` after one
+    warm-up call, on every configuration at M <= 64, one M = 4096 call of gate_up and of down, and
+    one layer of the sweep at M = 16, 64, 512. `value` is the verify GEMM's algorithmic bytes over
+    its dequant + matmul time (activations already quantized, as for the GPU line)."""
+    import torch
+    from oracle import torch_ref as T
     from vllm_sly_radiance_amd import synthetic
-    M, N, K = VERIFY["M"], VERIFY["N"], VERIFY["K"]
     cores = os.cpu_count() or 1
-    w, ws = synthetic.weights(N, K, 1)
-    q, s = O.quant_per_token(synthetic.activations(M, K, 2))
-    with threadpool_limits(limits=cores):
-        O.gemm_ref_f32(q, s, w[:256], ws[:256])          # warm
-        times = []
-        t_end = time.perf_counter() + 20.0
-        while len(times) < 5 and (len(times) < 2 or time.perf_counter() < t_end):
+    cores = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
+    torch.set_num_threads(cores)
+
+    def med(fn, reps):
+        fn()                                            # warm-up (allocations, thread pool)
+        t = []
+        for _ in range(reps):
             t0 = time.perf_counter()
-            O.gemm_ref_f32(q, s, w, ws)
-            times.append(time.perf_counter() - t0)
-    sec = float(np.median(times))
-    return {"value": round(gemm_bytes(M, N, K) / sec / 1e9, 3), "unit": "GB/s", "cores": cores,
-            "kind": "port",
-            "sample": f"oracle dequant + fp32 matmul (numpy/OpenBLAS, {cores} threads) of the full "
-                      f"M=8 N=17408 K=5120 GEMM, median of {len(times)} runs, "
-                      f"{sec:.3f} s per GEMM"}
+            out = fn()
+            t.append(time.perf_counter() - t0)
+        return float(np.median(t)), out
+
+    def one(M, N, K, reps, seed):
+        x = torch.from_numpy(synthetic.activations(M, K, seed).view(np.int16)).view(torch.bfloat16)
+        w, ws = synthetic.weights(N, K, seed + 1)
+        w, ws = torch.from_numpy(w), torch.from_numpy(ws)
+        tq, (q, s) = med(lambda: T.quant_per_token(x), reps)
+        td, wd = med(lambda: T.dequant_weight(w, ws), reps)
+        tm, _ = med(lambda: T.gemm(q, s, wd), reps)
+        nb = gemm_bytes(M, N, K)
+        return dict(M=M, N=N, K=K, reps=reps, quant_ms=round(tq * 1e3, 3),
+                    dequant_ms=round(td * 1e3, 3), matmul_ms=round(tm * 1e3, 3),
+                    gbs=round(nb / (td + tm) / 1e9, 3),
+                    tflops=round(2.0 * M * N * K / (td + tm) / 1e12, 4))
+
+    t_start = time.perf_counter()
+    rows = {}
+    for name, M, N, K, reps in CPU_CONFIGS:
+        rows[name] = one(M, N, K, reps, seed=len(rows) + 1)
+    sweep = {}
+    for M in CPU_SWEEP_M:
+        per = [one(M, N, K, 3, seed=100 + M) for _, N, K in LAYER_M1]
+        sweep[M] = dict(ms_per_layer=round(sum(r["dequant_ms"] + r["matmul_ms"] for r in per), 2),
+                        quant_ms_per_layer=round(sum(r["quant_ms"] for r in per), 3))
+    layer = [rows[f"layer_{n}"] for n, _, _ in LAYER_M1]
+    v = rows["verify"]
+    return {"value": v["gbs"], "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"torch CPU dequant + fp32 matmul ({cores} threads) of the full M=8 N=17408 "
+                      f"K=5120 GEMM, median of {v['reps']} after a warm-up: dequant "
+                      f"{v['dequant_ms']} ms + matmul {v['matmul_ms']} ms (quant {v['quant_ms']} "
+                      f"ms, not in value); the other configurations under 'configs'",
+            "configs": rows,
+            "layer_m1_ms": round(sum(r["dequant_ms"] + r["matmul_ms"] for r in layer), 2),
+            "sweep_one_layer": sweep,
+            "seconds": round(time.perf_counter() - t_start, 1)}
 
 
 SWEEP_M = [1, 8, 16, 64, 512, 4096]
@@ -874,6 +954,7 @@ def main():
         "mfma_probe_tflops": probe,
         "hbm_read_probe": rprobe,
         "value_vs_read_probe": round(v["gbs"] / rprobe["gbs"], 4),
+        "value_vs_best_read_shape": round(v["gbs"] / rprobe["best"]["gbs"], 4),
         "decode_m1_layer": layer,
         "producers": producers,
         "quantizer": quant,

@@ -107,8 +107,9 @@ int w4a8_gemm(const void* a, const float* a_scale, const void* wq, const void* s
  * the reference's band/split policy (sly/mxfp4/radiance_mxfp4_fp8.hip:1252-1343, :1390-1500) and
  * its Python replica band_map (sly/mxfp4/band_map.py:31-95). For a macro-tile plan whose
  * workgroups fill a CU each, w4a8_gemm may run the variant on the leading columns that fill whole
- * rounds of workgroups and a 128 x 128 tile variant on the rest (two launches on the stream);
- * w4a8_gemm_planned with the returned triple always makes one launch. */
+ * rounds of workgroups and a 128 x 128 tile variant on the rest (two launches on the stream); the
+ * returned triple names the first. A tile plan with split_k > 1 (the decode band's K split) is
+ * two launches under w4a8_gemm_planned too: the partial launch and the reducing launch. */
 int w4a8_plan(int M, int N, int K, int* kernel, int* variant, int* split_k);
 
 /* The GEMM on fragment-tiled activations (W4A8_Q_TILED, as the producers write them; K % 128 == 0):
@@ -125,8 +126,13 @@ int w4a8_tiled_bytes(int M, int K, size_t* bytes);
 
 /* w4a8_gemm with an explicit plan, for sweeps and tests (the reference forces cells through the
  * RADIANCE_MXFP4_DECODE_KS / _BK environment knobs, sly/mxfp4/radiance_mxfp4_fp8.hip:1464-1475).
- * split_k > 1 needs registered scratch of w4a8_scratch_bytes(); kernels 2 and 5 ignore split_k;
- * kernels 5 and 6 read fragment-tiled activations. */
+ * split_k: the skinny kernel (1) splits K over split_k workgroups that meet in one launch
+ * (registered scratch of w4a8_scratch_bytes()); the tile kernels (2, 5) with split_k > 1 run their
+ * K-split form, which only the 4-wave tiles up to 64 tokens tall have (any other tile variant
+ * returns W4A8_EINVAL): K over split_k workgroup rows writing fp32 partials to the registered
+ * scratch (3 * M * N * 4 bytes for three splits), then a reducing launch; split_k 0 or 1 is one
+ * launch. The stream and ring kernels (3, 4, 6) ignore split_k. Kernels 5 and 6 read
+ * fragment-tiled activations. */
 int w4a8_gemm_planned(const void* a, const float* a_scale, const void* wq, const void* sq, void* c,
                       int M, int N, int K, int kernel, int variant, int split_k, void* stream);
 
@@ -135,10 +141,13 @@ int w4a8_gemm_planned(const void* a, const float* a_scale, const void* wq, const
  * harnesses that forbid hipMalloc). No counterpart in the reference. Split-K partials and counters
  * live in a static device array of the library (4 MiB + 16 KiB per device, held until the process
  * ends); the automatic plan takes only splits that fit it, and a forced plan needing more returns
- * W4A8_ESCRATCH. The first call on a device finds the array's address and queues the clearing of
- * its counters on `stream`. Every call on a device shares the array: calls that overlap on one
- * device race and must be ordered by the caller (one stream, or events). Same kernels, plans and
- * results as w4a8_gemm_planned with enough registered scratch. */
+ * W4A8_ESCRATCH. The array is zero-initialised static storage and the split kernels reset the
+ * counters they use, so nothing is cleared at set-up. The first call on a device looks up the
+ * array's address (a runtime call) and must be made outside HIP graph capture: under capture it
+ * returns W4A8_EINVAL; later calls may be captured. Every call on a device shares the array: calls
+ * that overlap on one device race and must be ordered by the caller (one stream, or events); a
+ * captured call shares it with eager ones too. Same kernels, plans and results as
+ * w4a8_gemm_planned with enough registered scratch. */
 int w4a8_gemm_noalloc(const void* a, const float* a_scale, const void* wq, const void* sq, void* c,
                       int M, int N, int K, int kernel, int variant, int split_k, void* stream);
 
@@ -259,6 +268,20 @@ int w4a8_mfma_probe(int shape, float* out, int blocks, int iters, double* flop, 
  * counterpart in the reference, which quotes its decode kernel against the GDDR6 specification
  * (autoround-tests/RESULTS.md:404-405). */
 int w4a8_read_probe(const void* buf, long bytes, int* out, void* stream);
+
+/* Diagnostic: the read probe over launch shapes, to find the fastest way to stream `bytes` (1 ..
+ * 2^31 - 2^20, 16-byte aligned buffer): `blocks` workgroups share the bytes in equal 1 KiB-aligned
+ * ranges (the last one shorter; no workgroup may be left without bytes), and each of a variant's
+ * `waves` waves reads `units` KiB of its workgroup's range as 64-lane 16-byte loads, `window` of
+ * them in flight (window == units: all issued before any is used), non-temporal or not. A variant
+ * that cannot cover a workgroup's range at this grid returns W4A8_EINVAL. out receives nothing
+ * unless the data xor to a fixed pattern; the caller times the launch. No counterpart in the
+ * reference. */
+int w4a8_read_probe_variants(void);
+int w4a8_read_probe_variant_info(int variant, int* waves, int* units, int* window,
+                                 int* nontemporal);
+int w4a8_read_probe_shape(const void* buf, long bytes, int* out, int blocks, int variant,
+                          void* stream);
 
 /* Diagnostic: `count` independent scaled MFMAs (16x16x128, fp4 e2m1 A x fp8 e4m3 B, the instruction
  * every GEMM here issues) on raw lane operands, one wave per tile: a [count][64][4] dwords (16 fp4

@@ -325,6 +325,28 @@ def test_read_probe_validates_before_launch(lib):
     assert b"w4a8_read_probe" in lib.w4a8_last_error()
 
 
+def test_read_probe_shape_validates_before_launch(lib):
+    """The launch-shape sweep of the read probe: every variant describes itself, and a grid whose
+    workgroups the variant cannot cover, or that leaves a workgroup without bytes, is refused."""
+    n = lib.w4a8_read_probe_variants()
+    assert n >= 16
+    p = [ctypes.c_int() for _ in range(4)]
+    for v in range(n):
+        assert lib.w4a8_read_probe_variant_info(v, *[ctypes.byref(x) for x in p]) == 0
+        waves, units, window, nt = (x.value for x in p)
+        assert 1 <= waves <= 16 and 1 <= window <= units and nt in (0, 1)
+    assert lib.w4a8_read_probe_variant_info(n, *[ctypes.byref(x) for x in p]) == 1
+    b = 4096
+    nbytes = 47_669_280
+    assert lib.w4a8_read_probe_shape(None, nbytes, b, 218, 1, None) == 1
+    assert lib.w4a8_read_probe_shape(b + 4, nbytes, b, 218, 1, None) == 1          # misaligned
+    assert lib.w4a8_read_probe_shape(b, 1 << 31, b, 218, 1, None) == 1
+    assert lib.w4a8_read_probe_shape(b, nbytes, b, 100, 1, None) == 1       # 10 x 22 KiB < share
+    assert lib.w4a8_read_probe_shape(b, nbytes, b, 1012, 12, None) == 1    # last workgroup empty
+    assert lib.w4a8_read_probe_shape(b, nbytes, b, 218, n, None) == 1
+    assert b"w4a8_read_probe_shape" in lib.w4a8_last_error()
+
+
 def test_workspace_bytes_covers_the_band_split_in_4_mib(lib):
     """The scratch the plugin registers, sized by the library's own plan: the skinny kernel's
     split-K partials for small-N shapes at M <= 16, SiLU-mul's split-row maxima, and the band's

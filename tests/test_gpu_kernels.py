@@ -112,7 +112,8 @@ def canon_nan(c):
 @pytest.mark.parametrize("M,K,ldx", [(1, 5120, None), (8, 5120, None), (17, 1000, None),
                                      (64, 8704, None), (3, 17408, None), (5, 24, None),
                                      (9, 5120, 5128), (7, 640, 641), (1, 40000, None),
-                                     (4096, 5120, None), (300, 5120, None), (257, 8704, 8712),
+                                     (4096, 5120, None), (4096, 8704, None), (300, 5120, None),
+                                     (257, 8704, 8712),
                                      (256, 24, None), (261, 10240, None), (256, 10248, None),
                                      (258, 1000, 1001)])
 def test_quant_bit_exact(gpu_lib, M, K, ldx):
@@ -184,9 +185,11 @@ def test_quant_rounding_ties_and_subnormals(gpu_lib):
     assert np.array_equal(q, oq)
 
 
-def test_quant_full_size_digest(gpu_lib):
-    # M=4096 K=5120 prefill activations: codes and scales hashed and compared with the oracle's
-    x = synthetic.activations(4096, 5120, seed=4096)
+@pytest.mark.parametrize("K", [5120, 8704])
+def test_quant_full_size_digest(gpu_lib, K):
+    # M=4096 prefill activations of gate_up (K=5120) and down (K=8704): codes and scales hashed
+    # and compared with the oracle's
+    x = synthetic.activations(4096, K, seed=4096 + (K != 5120))
     q, s = gpu_quant(x)
     oq, os_ = O.quant_per_token(x)
     h = lambda a: hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
@@ -618,6 +621,20 @@ def test_plugin_scratch_covers_every_automatic_plan(gpu_lib):
         _native.set_scratch(part.data_ptr(), part.numel() * 4, cnt.data_ptr(), cnt.numel() * 4)
 
 
+def test_read_probe_shapes_read_without_writing(gpu_lib):
+    """Every read-probe variant at a grid it covers, over the verify GEMM's byte count and a short
+    ragged buffer: it runs, and with data that never xors to its pattern it writes nothing."""
+    for nbytes in (47_669_280, 5000):
+        buf = torch.full((nbytes + 16,), 3, dtype=torch.uint8, device="cuda")
+        out = torch.zeros(2, dtype=torch.int32, device="cuda")
+        for v, (waves, units, window, nt) in enumerate(_native.read_probe_variants()):
+            blocks = -(-nbytes // (waves * units * 1024))     # the fewest workgroups that cover it
+            print(f"[probe] read shape v={v} blocks={blocks} {nbytes} B", flush=True)
+            _native.read_probe_shape(buf.data_ptr(), nbytes, out.data_ptr(), blocks, v, stream())
+        torch.cuda.synchronize()
+        assert out.cpu().tolist() == [0, 0]
+
+
 @pytest.mark.parametrize("nbytes", [1000, 204800, 47_669_280])
 def test_read_probe_reads_without_writing(gpu_lib, nbytes):
     """The HBM read probe over buffers shorter than, equal to and longer than one workgroup's
@@ -646,7 +663,8 @@ def random_shapes(count, seed):
     (17, 5120, 6144), (21, 5120, 8704), (19, 2048, 1024), (20, 4000, 544)])
 def test_gemm_random_shapes_planned(gpu_lib, M, N, K):
     """The automatic plan on seeded random shapes, every output against the oracle; the last four
-    take the skinny kernel just above the streaming band (M = 17 .. 21, N = 2048 .. 5120)."""
+    sit just above the streaming band (M = 17 .. 21, N = 2048 .. 5120), where the plan takes the
+    decode-band tiles (with the K split for the down-shaped one)."""
     x = synthetic.activations(M, K, seed=M * 31 + K)
     w, ws = synthetic.weights(N, K, seed=N * 7 + K)
     q, s = O.quant_per_token(x)

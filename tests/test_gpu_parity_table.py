@@ -27,9 +27,11 @@ SHAPES = {"qkv": (10240, 5120), "o_proj": (5120, 6144), "gate_up": (17408, 5120)
 MS = [1, 8, 16, 64, 512, 4096]
 CELLS = [(name, M) for name in SHAPES for M in MS] + [("plumbing", 8)]
 SAMPLED_ROWS = 192
-# the measured fraction of outputs beyond 2 ulp is 0.03-0.1 % on these cells (the exact result's
-# own is 0-0.003 %); a layout or scale mistake puts most outputs beyond it
-FRAC_BEYOND_2ULP_MAX = 5e-3
+# the measured fraction of outputs beyond 2 ulp is 0.020-0.078 % on these cells (the exact
+# result's own is 0-0.020 %); the bound is twice the worst measured cell, so a regression that
+# moves a few hundredths of a percent of the outputs fails it, and a layout or scale mistake puts
+# most outputs beyond it
+FRAC_BEYOND_2ULP_MAX = 1.6e-3
 
 
 @functools.lru_cache(maxsize=2)

@@ -141,15 +141,28 @@ def test_silu_mul_linear_op(gpu_lib):
     layer.weight_scale = torch.nn.Parameter(to_dev(ws), requires_grad=False)
     layer.bias = None
     R.kernel_class()().process_weights_after_loading(layer)
-    for M in (1, 2, 4):
+    for M in (1, 2, 3, 4):
         gu = bf16_dev(synthetic.activations(M, 2 * K, seed=M))
-        y = F.silu_mul_down(layer, gu)
+        y, y_bias = F.silu_mul_down(layer, gu)          # unpacked as RowParallelLinear's output
+        assert y_bias is None
         q, s = torch.ops.radiance.silu_mul_quant(gu)
         ref = torch.ops.radiance.mxfp4_linear_pq(q, s, layer.weight, layer.weight_scale,
                                                  layer.radiance_wref)
         torch.cuda.synchronize()
         assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), f"M={M}"
     gu3 = bf16_dev(synthetic.activations(6, 2 * K, seed=6)).view(2, 3, 2 * K)
-    assert F.silu_mul_down(layer, gu3).shape == (2, 3, N)
+    assert F.silu_mul_down(layer, gu3)[0].shape == (2, 3, N)
     empty = torch.empty((0, 2 * K), dtype=torch.bfloat16, device="cuda")
-    assert F.silu_mul_down(layer, empty).shape == (0, N)
+    assert F.silu_mul_down(layer, empty)[0].shape == (0, N)
+    # a bias is added unless the layer defers it (skip_bias_add), as RowParallelLinear does
+    layer.bias = torch.nn.Parameter(bf16_dev(synthetic.activations(1, N, seed=12)[0]),
+                                    requires_grad=False)
+    gu = bf16_dev(synthetic.activations(2, 2 * K, seed=13))
+    y, y_bias = F.silu_mul_down(layer, gu)
+    q, s = torch.ops.radiance.silu_mul_quant(gu)
+    ref = torch.ops.radiance.mxfp4_linear_pq(q, s, layer.weight, layer.weight_scale,
+                                             layer.radiance_wref)
+    assert y_bias is None and torch.equal(y, ref + layer.bias)
+    layer.skip_bias_add = True
+    y, y_bias = F.silu_mul_down(layer, gu)
+    assert y_bias is layer.bias and torch.equal(y.view(torch.int16), ref.view(torch.int16))

@@ -24,6 +24,28 @@ def test_gemm_f32_vs_exact_f64(M, N, K):
     assert np.all(np.abs(ref - exact) <= K * 2.0 ** -24 * terms + 1e-30)
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 16, 32), (8, 48, 256), (5, 33, 640)])
+def test_gemm_abs_terms_is_the_exact_sum_of_magnitudes(M, N, K):
+    """gemm_abs_terms (which sizes the GEMM tolerance's accumulation allowance) pinned without
+    restating it: on operands whose every term is non-negative it is the GEMM itself, computed
+    exactly by gemm_exact_f64; and it does not change when signs are flipped, on either operand."""
+    _, q, s, w, ws = _case(M, N, K, 3 * M + N + K)
+    qp = np.minimum(q & 0x7F, 0x7E).astype(np.uint8)    # e4m3 sign bit clear, no NaN code
+    wp = (w & 0x77).astype(np.uint8)                      # e2m1 sign bit (bit 3) of both nibbles
+    got = O.gemm_abs_terms(qp, s, wp, ws)
+    exact = O.gemm_exact_f64(qp, s, wp, ws)
+    assert np.all(got >= 0) and got.max() > 0
+    assert np.allclose(got, exact, rtol=1e-14, atol=0)
+    rng = np.random.default_rng(M + N + K)
+    qs = (qp | (rng.integers(0, 2, qp.shape) << 7)).astype(np.uint8)
+    ws_signs = (rng.integers(0, 2, wp.shape) << 3) | (rng.integers(0, 2, wp.shape) << 7)
+    assert np.allclose(O.gemm_abs_terms(qs, s, (wp | ws_signs).astype(np.uint8), ws), exact,
+                       rtol=1e-14, atol=0)
+    # and it bounds the signed GEMM: |y| <= sum |terms|, with equality where no sign was flipped
+    assert np.all(np.abs(O.gemm_exact_f64(q, s, w, ws)) <= O.gemm_abs_terms(q, s, w, ws) *
+                  (1 + 1e-14))
+
+
 def test_gemm_one_hot_known_answer():
     M, N, K = 2, 16, 64
     q = np.zeros((M, K), np.uint8)

@@ -172,6 +172,52 @@ def test_can_implement_declines_aiter_asm_layout(fake_vllm):
     assert ok is False and "AITER" in why
 
 
+def _install_backend_filter(fake_vllm, monkeypatch, keep):
+    """A stand-in for vLLM's --linear-backend filter (_resolve_backend_kernels): with a backend
+    set, only the kernels it names survive; and init_mxfp4_linear_kernel's order of operations
+    (list, filter, first kernel whose is_supported and can_implement accept)."""
+    registry = fake_vllm.registry
+
+    def _resolve_backend_kernels(possible, quantization):
+        return [k for k in possible if k in keep]
+    monkeypatch.setattr(registry, "_resolve_backend_kernels", _resolve_backend_kernels,
+                        raising=False)
+
+    def init_mxfp4_linear_kernel(cfg):
+        possible = list(registry._POSSIBLE_MXFP4_KERNELS.get(ROCM, []))
+        possible = registry._resolve_backend_kernels(possible, "MXFP4")
+        for k in possible:
+            if k is _OtherKernel:
+                return k, possible
+            if k.is_supported()[0] and k.can_implement(cfg)[0]:
+                return k, possible
+        return None, possible
+    return init_mxfp4_linear_kernel
+
+
+def test_registration_survives_the_linear_backend_filter(fake_vllm, monkeypatch):
+    """With --linear-backend naming another kernel, the filter drops every class it does not name;
+    the reference's insertion point (after the filter, sly/patch_quark_mxfp4.py:74-103) keeps the
+    plugin at the head anyway, and so does register_with_vllm."""
+    monkeypatch.setattr(_native, "lib", lambda: object())
+    monkeypatch.setattr(R, "on_gfx950", lambda: True)
+    monkeypatch.setattr(R, "ENABLED", True)
+    init = _install_backend_filter(fake_vllm, monkeypatch, keep={_OtherKernel})
+    cfg = fake_vllm.config(K_MXFP4_DYNAMIC)
+    assert init(cfg)[0] is _OtherKernel                  # not registered: the backend's kernel
+    R.register_with_vllm()
+    R.register_with_vllm()                               # idempotent: the filter wrapped once
+    picked, possible = init(cfg)
+    assert picked is R.kernel_class()
+    assert possible == [R.kernel_class(), _OtherKernel]
+    # other quantizations and an unfiltered list pass through unchanged
+    resolve = fake_vllm.registry._resolve_backend_kernels
+    assert resolve([R.kernel_class(), _OtherKernel], "FP8") == [_OtherKernel]
+    assert resolve([_OtherKernel], quantization="mxfp4") == [_OtherKernel]
+    monkeypatch.setattr(R, "ENABLED", False)             # declining still hands the layer on
+    assert init(cfg)[0] is _OtherKernel
+
+
 def test_selection_order_picks_the_plugin_first(fake_vllm, monkeypatch):
     """What init_mxfp4_linear_kernel does with the list: the first class whose is_supported and
     can_implement both accept. With the plugin registered and accepting it is chosen; declining

@@ -118,3 +118,37 @@ def test_noalloc_refuses_a_tile_split_beyond_its_static_scratch(registered):
                                          3, None)
     assert rc == 2
     assert b"static scratch" in _native.lib().w4a8_last_error()
+
+
+def test_noalloc_under_graph_capture(registered):
+    """w4a8_gemm_noalloc captured into a HIP graph on a split plan (down 5120 x 8704 at M = 24: the
+    band tile with K in three, partials in the static array), replayed three times with eager
+    split calls of another shape between the replays (they overwrite the same static partials):
+    every replay equals the eager call bit for bit. The capture itself allocates nothing through
+    the entry point (the set-up call ran eagerly in the tests above)."""
+    op = operands(24, 5120, 8704, seed=5)
+    other = operands(17, 5120, 8704, seed=6)
+    plan = _native.plan(24, 5120, 8704)
+    assert plan[0] == _native.KERNEL_TILE and plan[2] == 3, plan
+    eager, _ = run(_native.gemm_noalloc, op)
+    other_eager, _ = run(_native.gemm_noalloc, other)
+    torch.cuda.synchronize()
+    want, want_other = host_u16(eager), host_u16(other_eager)
+    out = torch.full((24, 5120), float("nan"), dtype=torch.bfloat16, device="cuda")
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        _native.gemm_noalloc(op["qd"].data_ptr(), op["sd"].data_ptr(), op["wq"].data_ptr(),
+                             op["sq"].data_ptr(), out.data_ptr(), 24, 5120, 8704,
+                             side.cuda_stream)
+    for r in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        print(f"[noalloc] graph replay {r}", flush=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host_u16(out), want), f"replay {r}"
+        got_other, _ = run(_native.gemm_noalloc, other)
+        torch.cuda.synchronize()
+        assert np.array_equal(host_u16(got_other), want_other), f"eager call after replay {r}"
+    del graph

@@ -56,6 +56,9 @@ SIGNATURES = {
                                    _int]),
     "w4a8_mfma_probe": (_int, [_int, _vp, _int, _int, _c.POINTER(_c.c_double), _vp]),
     "w4a8_read_probe": (_int, [_vp, _long, _vp, _vp]),
+    "w4a8_read_probe_variants": (_int, []),
+    "w4a8_read_probe_variant_info": (_int, [_int, _pint, _pint, _pint, _pint]),
+    "w4a8_read_probe_shape": (_int, [_vp, _long, _vp, _int, _int, _vp]),
     "w4a8_mfma_tile": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _vp]),
 }
 
@@ -224,6 +227,20 @@ def workspace_bytes(max_m: int, max_n: int):
 
 def read_probe(buf_ptr, nbytes, out_ptr, stream) -> None:
     check(lib().w4a8_read_probe(buf_ptr, nbytes, out_ptr, stream))
+
+
+def read_probe_variants():
+    """[(waves, KiB per wave, loads in flight per wave, non-temporal)] of the shape probe."""
+    out = []
+    for v in range(lib().w4a8_read_probe_variants()):
+        p = [_c.c_int() for _ in range(4)]
+        check(lib().w4a8_read_probe_variant_info(v, *[_c.byref(x) for x in p]))
+        out.append(tuple(x.value for x in p))
+    return out
+
+
+def read_probe_shape(buf_ptr, nbytes, out_ptr, blocks, variant, stream) -> None:
+    check(lib().w4a8_read_probe_shape(buf_ptr, nbytes, out_ptr, blocks, variant, stream))
 
 
 def mfma_probe(shape, out_ptr, blocks, iters, stream) -> float:

@@ -14,7 +14,8 @@
 // ---- scratch of the allocation-free entry point (w4a8_gemm_noalloc) -----------------------------
 // One copy per device in the code object's static data, held until the process ends: split-K
 // partials first, then the counters. Every call on a device shares it; the counters start at
-// zero (cleared at set-up) and each split reduction's last workgroup resets the ones it used.
+// zero (the array is zero-initialised static storage, so nothing is cleared at set-up) and each
+// split reduction's last workgroup resets the ones it used.
 constexpr size_t kStaticPartialBytes = 4u << 20;
 constexpr size_t kStaticCounterBytes = 16u << 10;
 static __device__ __align__(256) uint8_t scratch[kStaticPartialBytes + kStaticCounterBytes];
@@ -653,13 +654,11 @@ W4A8_API int w4a8_scratch_bytes(int variant, int N, int split_k, size_t* partial
 
 namespace {
 
-__global__ void clear_words(int* p, int n) {
-  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
-}
-
 // The device address of this device's static scratch, found once per device (with the device
-// current) by hipGetSymbolAddress; the host-side name `scratch` is not a device address. The first
-// call on a device also queues the counters' clear on its stream, ahead of its own launches.
+// current) by hipGetSymbolAddress; the host-side name `scratch` is not a device address. The
+// lookup is a runtime call outside any stream, so the first call on a device must not be made
+// while `st` is being captured into a HIP graph: it is refused then (W4A8_EINVAL), and every later
+// call, captured or not, uses the address found.
 std::mutex g_static_fill;
 uint8_t* g_static_addr[kMaxDevices];
 std::atomic<bool> g_static_set[kMaxDevices];
@@ -669,16 +668,20 @@ int static_scratch(int dev, hipStream_t st, Scratch* out) {
   if (!g_static_set[dev].load(std::memory_order_acquire)) {
     std::lock_guard<std::mutex> lock(g_static_fill);
     if (!g_static_set[dev].load(std::memory_order_relaxed)) {
+      hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+      if (int e = hip_status(hipStreamIsCapturing(st, &cap),
+                             "w4a8_gemm_noalloc: hipStreamIsCapturing"))
+        return e;
+      if (cap != hipStreamCaptureStatusNone)
+        return fail(W4A8_EINVAL, "w4a8_gemm_noalloc: the first call on device %d is being "
+                    "captured into a HIP graph; make one call outside capture first (it looks "
+                    "up the static scratch's address)", dev);
       void* p = nullptr;
       if (int e = hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)),
                              "w4a8_gemm_noalloc: hipGetSymbolAddress(scratch)"))
         return e;
       if (!p || !aligned(p, 256))
         return fail(W4A8_EHIP, "w4a8_gemm_noalloc: static scratch has no usable address");
-      const int words = (int)(kStaticCounterBytes / sizeof(int));
-      hipLaunchKernelGGL(clear_words, dim3(16), dim3(256), 0, st,
-                         (int*)((uint8_t*)p + kStaticPartialBytes), words);
-      if (int e = hip_status(hipGetLastError(), "w4a8_gemm_noalloc: counter clear")) return e;
       g_static_addr[dev] = (uint8_t*)p;
       g_static_set[dev].store(true, std::memory_order_release);
     }
@@ -880,6 +883,29 @@ W4A8_API int w4a8_read_probe(const void* buf, long bytes, int* out, void* stream
                 "w4a8_read_probe: need a 16-byte aligned buffer of 1 .. 2^31 - 2^20 bytes and out");
   return hip_status(launch_read_probe(buf, (int)bytes, out, (hipStream_t)stream),
                     "w4a8_read_probe");
+}
+
+W4A8_API int w4a8_read_probe_variants(void) { return read_variant_count(); }
+
+W4A8_API int w4a8_read_probe_variant_info(int variant, int* waves, int* units, int* window,
+                                          int* nontemporal) {
+  if (!waves || !units || !window || !nontemporal ||
+      !read_variant_info(variant, waves, units, window, nontemporal))
+    return fail(W4A8_EINVAL, "w4a8_read_probe_variant_info: variant %d outside 0..%d or null "
+                "output", variant, read_variant_count() - 1);
+  return W4A8_OK;
+}
+
+W4A8_API int w4a8_read_probe_shape(const void* buf, long bytes, int* out, int blocks, int variant,
+                                   void* stream) {
+  if (!buf || !out || bytes <= 0 || bytes > (1L << 31) - (1L << 20) || !aligned(buf, 16))
+    return fail(W4A8_EINVAL, "w4a8_read_probe_shape: need a 16-byte aligned buffer of 1 .. "
+                "2^31 - 2^20 bytes and out");
+  if (read_shape_wg_bytes(variant, bytes, blocks) == 0)
+    return fail(W4A8_EINVAL, "w4a8_read_probe_shape: variant %d with %d workgroups cannot cover "
+                "%ld bytes (or leaves a workgroup empty)", variant, blocks, bytes);
+  return hip_status(launch_read_shape(buf, (int)bytes, out, blocks, variant, (hipStream_t)stream),
+                    "w4a8_read_probe_shape");
 }
 
 W4A8_API int w4a8_mfma_probe(int shape, float* out, int blocks, int iters, double* flop,

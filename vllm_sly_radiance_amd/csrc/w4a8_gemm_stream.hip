@@ -58,19 +58,26 @@ __device__ __forceinline__ void lds_barrier() {
 // live tokens (lanes 8..15 of each row of 16 load the second run of token r - 8, and a row
 // rotation by 8 lanes hands it to lane r), half the activation loads; the MFMA columns of tokens
 // 8..15 then hold other tokens' bytes, and those columns are never stored.
+// The 14 argument dwords are exactly what the kernel arguments preloaded into SGPRs hold, so no
+// wave reads the kernarg segment, not even for the epilogue (whose scalar load used to sit on the
+// critical path after the last MFMA); the n-tile count and the store width follow from N and C.
 template <int NT, int KPW, int W, bool H8>
 __global__ __launch_bounds__(W * 64) void gemm_stream(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
-    const uint32_t* __restrict__ Sq, int M, int K, int NTILES, int G,
-    uint16_t* __restrict__ C, int N, int vec_out) {
+    const uint32_t* __restrict__ Sq, uint16_t* __restrict__ C, int M, int K, int N, int G) {
   static_assert(KPW % 4 == 0 && NT >= 1 && W >= 1 && W <= 16, "stream variant");
   const int KT = K / kKTile, KG = KT / kKGroup;  // K % 512 == 0
+  const int NTILES = (N + kNTile - 1) / kNTile;
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   // Wave-uniform work selection in scalar registers; 32-bit products only (the host bounds them).
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int b = blockIdx.x;
   const int ntb0 = b * NTILES / G, nth = (b + 1) * NTILES / G - ntb0;
+  // the epilogue: thread tid adds the partials of output slot tid (below); at M <= 8 a slot is one
+  // of the 32 lanes of an n-tile that hold tokens 0..7
+  constexpr int LIVE = H8 ? 32 : 64;
+  const int om = H8 ? (tid & 7) : (tid & 15), og = (tid % LIVE) / (H8 ? 8 : 16);
   const int kr0 = 4 * (KG * wave / W), kr1 = 4 * (KG * (wave + 1) / W);
 
   // ---- 1. activation fragments of k-tiles kr0.. (L2): token lane % 16, two 16-byte runs.
@@ -129,10 +136,9 @@ __global__ __launch_bounds__(W * 64) void gemm_stream(
   }
   float tok_scale;
   {
-    // the epilogue's per-token scale, last: it is needed last
+    // the epilogue's per-token scale (of the token this thread stores), last: it is needed last
     const auto as_src = __builtin_amdgcn_make_buffer_rsrc((void*)As, 0, M * 4, kBufferWord3);
-    tok_scale = __builtin_bit_cast(
-        float, __builtin_amdgcn_raw_buffer_load_b32(as_src, (lane & 15) * 4, 0, 0));
+    tok_scale = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(as_src, om * 4, 0, 0));
     __builtin_amdgcn_sched_barrier(0);           // every load above is issued before any MFMA
     if constexpr (H8) {
       // DPP row_ror:8 (within each row of 16 lanes, lane r takes lane (r + 8) % 16's value)
@@ -157,19 +163,36 @@ __global__ __launch_bounds__(W * 64) void gemm_stream(
       acc[t] = mfma_w4a8(wv[u][t], xf, acc[t], sv[t][u / 4] >> (8 * (u & 3)));
   }
 
-  // ---- 4. the W partial sums of each n-tile meet in LDS and are added in wave order ----
+  // ---- 4. the W partial sums of each n-tile meet in LDS and are added in wave order. Every lane
+  //         writes its partials (no branch here: the compiler would sink the MFMA operands' lane
+  //         arithmetic under it, and the MFMA reads every lane); only the lanes that hold tokens
+  //         are read back (at M <= 8 half of them: lanes 8..15 of each row of 16 hold other
+  //         tokens' bytes). Slot c of n-tile t is (token, column group) (c % 8, c / 8) at M <= 8,
+  //         (c % 16, c / 16) above, lane 16 (c / 8) + c % 8 or c. One slot per thread, every
+  //         partial read before the first add ----
   v4f* red = reinterpret_cast<v4f*>(lds);
 #pragma unroll
   for (int t = 0; t < NT; ++t) red[(wave * NT + t) * 64 + lane] = acc[t];
   __syncthreads();
-  const bool vec = vec_out != 0;
-  for (int slot = tid; slot < nth * 64; slot += W * 64) {
-    const int t = slot >> 6;                     // slot lane == this thread's lane
-    v4f v = red[t * 64 + lane];
-#pragma unroll 4
-    for (int w = 1; w < W; ++w) v += red[(w * NT + t) * 64 + lane];
-    const int n = (ntb0 + t) * kNTile + 4 * (lane >> 4);
-    if (m < M) store_out4(C, N, m, n, N, v, tok_scale, vec);
+  if (tid < nth * LIVE && om < M) {
+    const int t = tid / LIVE, c = tid % LIVE;
+    const int cl = H8 ? ((c >> 3) << 4) | (c & 7) : c;
+    v4f p[W];
+#pragma unroll
+    for (int w = 0; w < W; ++w) p[w] = red[(w * NT + t) * 64 + cl];
+    v4f v = p[0];
+#pragma unroll
+    for (int w = 1; w < W; ++w) v += p[w];
+    const int n = (ntb0 + t) * kNTile + 4 * og;
+    uint16_t* row = C + (size_t)om * N;
+    if (N % 4 == 0 && ((uintptr_t)C & 7) == 0 && n + 3 < N) {
+      *reinterpret_cast<uint2*>(row + n) = make_uint2(bf16x2_rne(v[0] * tok_scale, v[1] * tok_scale),
+                                                      bf16x2_rne(v[2] * tok_scale, v[3] * tok_scale));
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (n + i < N) row[n + i] = (uint16_t)f32_to_bf16(v[i] * tok_scale);
+    }
   }
 }
 
@@ -471,7 +494,7 @@ hipError_t launch_stream(const GemmArgs& g, int variant, int cus, bool fused, lo
   {                                                                                              \
     W4A8_STREAM_ATTR((gemm_stream<nt, kpw, w, h8>))                                              \
     hipLaunchKernelGGL((gemm_stream<nt, kpw, w, h8>), grid, block, lds, stream, g.a, g.a_scale,  \
-                       g.wq, g.sq, g.M, g.K, NTILES, (int)grid.x, g.c, g.N, vec_out);           \
+                       g.wq, g.sq, g.c, g.M, g.K, g.N, (int)grid.x);                            \
     return hipGetLastError();                                                                    \
   }
 #define W4A8_STREAM_LAUNCH(nt, kpw, w)                                                           \

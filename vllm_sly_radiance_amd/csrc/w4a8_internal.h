@@ -72,6 +72,19 @@ __device__ __forceinline__ v8i load_x_frag(const uint8_t* row, int k0, int g, in
   return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
+// Two bf16 of the hardware convert (v_cvt_pk_bf16_f32: round to nearest even, the same bits as
+// f32_to_bf16 for every non-NaN input), NaNs put back to f32_to_bf16's canonical 0x7FC0 | sign.
+typedef __bf16 w4a8_bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float w4a8_f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t bf16x2_rne(float lo, float hi) {
+  const uint32_t r =
+      __builtin_bit_cast(uint32_t, __builtin_convertvector(w4a8_f32x2_t{lo, hi}, w4a8_bf16x2_t));
+  const uint32_t l = lo != lo ? (((__float_as_uint(lo) >> 16) & 0x8000u) | 0x7FC0u) : r & 0xFFFFu;
+  const uint32_t h = hi != hi ? ((__float_as_uint(hi) & 0x80000000u) | 0x7FC00000u)
+                              : r & 0xFFFF0000u;
+  return l | h;
+}
+
 // Four consecutive outputs of one token, scaled and rounded, as one 8-byte store when aligned.
 __device__ __forceinline__ void store_out4(uint16_t* C, int ldc, int m, int n, int N, v4f v,
                                            float scale, bool vec_ok) {
@@ -177,6 +190,12 @@ bool tile_splits(int variant);   // the variant has a K-split form (4-wave tiles
 
 // Register-resident MFMA throughput probe (shape 0: 16x16x128, 1: 32x32x64).
 hipError_t launch_read_probe(const void* buf, int bytes, int* out, hipStream_t stream);
+// launch-shape sweep of the read probe: variant v of read_variant_count(), `blocks` workgroups
+int read_variant_count();
+int read_variant_info(int v, int* waves, int* units, int* window, int* nt);
+int read_shape_wg_bytes(int v, long bytes, int blocks);
+hipError_t launch_read_shape(const void* buf, int bytes, int* out, int blocks, int v,
+                             hipStream_t stream);
 hipError_t launch_mfma_probe(int shape, float* out, int blocks, int iters, double* flop,
                              hipStream_t stream);
 // Raw scaled-MFMA tiles on caller-given lane operands (layout diagnostic).

@@ -101,7 +101,90 @@ __global__ __launch_bounds__(kReadWaves * 64) void read_stream(const uint8_t* __
   if ((acc[0] ^ acc[1] ^ acc[2] ^ acc[3]) == 0x5A17C0DE) out[0] = w;
 }
 
+// The read ceiling over launch shapes: G workgroups of W waves, workgroup b reading bytes
+// [b * wg_bytes, (b + 1) * wg_bytes) of buf (wg_bytes a multiple of 1 KiB; the last workgroup's
+// range ends at `bytes`) and wave w of it the U KiB from w * U KiB of that range, as 64-lane
+// 16-byte loads; loads past the range return zero without a memory access. R == U: every load
+// issued before any is used (the decode GEMM's pattern); R < U: R loads in flight, each consumed
+// (xor) before its register is refilled with the load R further on. NT: non-temporal loads.
+template <int W, int U, int R, bool NT>
+__global__ __launch_bounds__(W * 64) void read_sweep(const uint8_t* __restrict__ buf, int bytes,
+                                                     int wg_bytes, int* __restrict__ out) {
+  static_assert(W >= 1 && W <= 16 && U >= 1 && R >= 1 && R <= U && R <= 60, "read variant");
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int base = blockIdx.x * wg_bytes;            // < bytes for every launched workgroup
+  const int len = min(wg_bytes, bytes - base);
+  const auto rs = __builtin_amdgcn_make_buffer_rsrc((void*)(buf + base), 0, len, kBufferWord3);
+  const int off = wave * U * 1024 + lane * 16;
+  constexpr int aux = NT ? kBufferNT : 0;
+  v4i acc = {0, 0, 0, 0};
+  v4i v[R];
+#pragma unroll
+  for (int u = 0; u < R; ++u) v[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, off + u * 1024, 0, aux);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int u = R; u < U; ++u) {
+    acc ^= v[u % R];                                 // waits for the oldest load only
+    v[u % R] = __builtin_amdgcn_raw_buffer_load_b128(rs, off + u * 1024, 0, aux);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int u = U; u < U + R; ++u) acc ^= v[u % R];
+  if ((acc[0] ^ acc[1] ^ acc[2] ^ acc[3]) == 0x5A17C0DE) out[0] = blockIdx.x;
+}
+
+// (W, U, R, NT): W waves of U KiB each, R loads in flight per wave
+#define W4A8_READ_TABLE(X)                                                                        \
+  X(10, 20, 20, 1) X(10, 22, 22, 1) X(4, 46, 46, 1) X(8, 23, 23, 1) X(10, 19, 19, 1)              \
+  X(12, 16, 16, 1) X(16, 12, 12, 1) X(10, 19, 19, 0) X(10, 19, 8, 1) X(16, 12, 4, 1)              \
+  X(8, 23, 8, 1) X(8, 12, 12, 1) X(4, 12, 12, 1) X(16, 6, 6, 1) X(16, 12, 12, 0) X(8, 23, 12, 1)  \
+  X(10, 26, 26, 1) X(10, 30, 30, 1) X(10, 35, 35, 1)
+
+struct ReadCfg { int w, u, r, nt; };
+#define W4A8_READ_CFG(w, u, r, nt) ReadCfg{w, u, r, nt},
+constexpr ReadCfg kRead[] = {W4A8_READ_TABLE(W4A8_READ_CFG)};
+#undef W4A8_READ_CFG
+constexpr int kReadCount = sizeof(kRead) / sizeof(kRead[0]);
+
 }  // namespace
+
+int read_variant_count() { return kReadCount; }
+
+int read_variant_info(int v, int* waves, int* units, int* window, int* nt) {
+  if (v < 0 || v >= kReadCount) return 0;
+  *waves = kRead[v].w;
+  *units = kRead[v].u;
+  *window = kRead[v].r;
+  *nt = kRead[v].nt;
+  return 1;
+}
+
+// Bytes per workgroup when `blocks` workgroups share `bytes` (a multiple of 1 KiB), or 0 when the
+// variant cannot cover them or a workgroup would be left without bytes.
+int read_shape_wg_bytes(int v, long bytes, int blocks) {
+  if (v < 0 || v >= kReadCount || blocks < 1 || bytes < 1) return 0;
+  const long per = ((bytes + blocks - 1) / blocks + 1023) / 1024 * 1024;
+  if ((long)(blocks - 1) * per >= bytes) return 0;
+  if ((long)kRead[v].w * kRead[v].u * 1024 < per) return 0;
+  return (int)per;
+}
+
+hipError_t launch_read_shape(const void* buf, int bytes, int* out, int blocks, int v,
+                             hipStream_t stream) {
+  const int per = read_shape_wg_bytes(v, bytes, blocks);
+  if (per == 0) return hipErrorInvalidValue;
+  int idx = 0;
+#define W4A8_READ_GO(w, u, r, nt)                                                                 \
+  if (idx++ == v) {                                                                              \
+    hipLaunchKernelGGL((read_sweep<w, u, r, nt != 0>), dim3(blocks), dim3(w * 64), 0, stream,    \
+                       (const uint8_t*)buf, bytes, per, out);                                    \
+    return hipGetLastError();                                                                    \
+  }
+  W4A8_READ_TABLE(W4A8_READ_GO)
+#undef W4A8_READ_GO
+  return hipErrorInvalidValue;
+}
 
 hipError_t launch_read_probe(const void* buf, int bytes, int* out, hipStream_t stream) {
   const int blocks = ceil_div(ceil_div(bytes, kReadRun), kReadWaves);

@@ -368,18 +368,27 @@ def silu_mul_quant(gate_up: torch.Tensor):
     return tuple(torch.ops.radiance.silu_mul_quant(gate_up))
 
 
-def silu_mul_down(down, gate_up: torch.Tensor) -> torch.Tensor:
+def silu_mul_down(down, gate_up: torch.Tensor):
     """Stands in for down(act_fn(gate_up)) when `down` is a layer this plugin serves: the
     SiLU-and-mul and the down projection in one op (one launch at M <= 2; the same bits as
-    down(silu_mul_quant(gate_up)))."""
+    down(silu_mul_quant(gate_up))).
+
+    Returns what vLLM's RowParallelLinear.forward returns, so the model's `x, _ = down(...)`
+    unpacks it unchanged: (output, output_bias), where the bias is added to output unless the
+    layer has skip_bias_add (then output_bias is the bias, else None), or output alone when the
+    layer has return_bias = False."""
     lead = gate_up.shape[:-1]
     y = torch.ops.radiance.silu_mul_mxfp4_linear(gate_up.reshape(-1, gate_up.shape[-1]),
                                                  down.weight, down.weight_scale,
                                                  down.radiance_wref)
     bias = getattr(down, "bias", None)
-    if bias is not None:
+    skip = bool(getattr(down, "skip_bias_add", False))
+    if bias is not None and not skip:
         y = y + bias
-    return y.reshape(*lead, y.shape[-1])
+    y = y.reshape(*lead, y.shape[-1])
+    if not getattr(down, "return_bias", True):
+        return y
+    return y, (bias if skip else None)
 
 
 def gdn_norm_quant(attn, core_attn_out: torch.Tensor, z: torch.Tensor):

@@ -426,12 +426,23 @@ def kernel_class():
     return _KERNEL_CLS
 
 
+def _is_mxfp4(args, kwargs) -> bool:
+    q = kwargs.get("quantization", args[0] if args else None)
+    return isinstance(q, str) and q.lower() == "mxfp4"
+
+
 def register_with_vllm(platform=None) -> bool:
     """Put the plugin at the head of vLLM's MXFP4 kernel priority list, the one change
     sly/patch_quark_mxfp4.py:76-103 makes. The list is `_POSSIBLE_MXFP4_KERNELS[platform]` of
     vllm.model_executor.kernels.linear (the module init_mxfp4_linear_kernel reads it from), keyed
     by current_platform._enum unless `platform` is given. Idempotent: the class appears once, at
-    index 0. Returns False when vLLM is not importable."""
+    index 0. Returns False when vLLM is not importable.
+
+    The reference inserts the class after init_mxfp4_linear_kernel's --linear-backend filter
+    (`possible = _resolve_backend_kernels(possible, "MXFP4")`), so the filter never drops it. An
+    entry in the list alone would go through that filter, so the module's _resolve_backend_kernels
+    is wrapped once as well: for the MXFP4 list, a filtered result that lost the plugin gets it back
+    at its head, which is the reference's order; every other call passes through unchanged."""
     try:
         import vllm.model_executor.kernels.linear as registry
         if platform is None:
@@ -443,4 +454,14 @@ def register_with_vllm(platform=None) -> bool:
     cls = kernel_class()
     kernels = registry._POSSIBLE_MXFP4_KERNELS.setdefault(platform, [])
     kernels[:] = [cls] + [k for k in kernels if k is not cls]
+    resolve = getattr(registry, "_resolve_backend_kernels", None)
+    if resolve is not None and not getattr(resolve, "_radiance_keeps_plugin", False):
+        def _resolve_backend_kernels(possible, *args, **kwargs):
+            out = resolve(possible, *args, **kwargs)
+            if _is_mxfp4(args, kwargs) and cls in possible and cls not in out:
+                out = [cls] + list(out)
+            return out
+        _resolve_backend_kernels._radiance_keeps_plugin = True
+        _resolve_backend_kernels.__wrapped__ = resolve
+        registry._resolve_backend_kernels = _resolve_backend_kernels
     return True
