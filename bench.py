@@ -12,9 +12,10 @@ duration comes from HIP event pairs around individual launches on the launch str
 
 Alongside: the M=4096 prefill GEMMs (gate_up 17408x5120, down 5120x8704) in TFLOP/s against the
 fp8 x fp4 MFMA peak, the M=1 per-layer linear set, the fused producers and the per-token quantizer
-at M=8 and M=4096 in GB/s, the register-resident MFMA rate and a streaming read of the verify
-GEMM's bytes in its launch shape (the HBM ceiling it is held against), and the CPU baseline (the
-oracle's dequant + fp32 matmul, timed on this host). Prints ONE JSON line.
+at M=8 and M=4096 in GB/s, the register-resident MFMA rate, a streaming read of the verify
+GEMM's bytes in its launch shape and over a sweep of launch shapes (the HBM ceiling it is held
+against), and the CPU baseline (a torch restatement of the reference's dequant + fp32 matmul,
+timed on this host's cores). Prints ONE JSON line.
 
   python bench.py [--gpus 1] [--steps 1024] [--warmup 64]
 
@@ -723,8 +724,11 @@ def bench_sweep(n_layers):
     # plan, kept to show why the plan takes the tiles there), timed on row-major q and, as
     # ring_at_us, on the same codes fragment-tiled (contiguous 1 KiB activation loads instead of
     # 16 token rows x 64 bytes); the tile family is the macro tile the plan takes at M, or at
-    # M = 17 below that, with the plan's K split (tile_split; tile_unsplit_us beside it).
+    # M = 17 below that, with the plan's K split (tile_split; tile_unsplit_us beside it). From 17
+    # to 64 tokens band_us is the fastest band-kernel variant (weight waves and activation waves)
+    # that serves the shape unsplit; where the plan takes the band kernel, plan_us is the plan.
     ring = _native.variants(_native.KERNEL_RING)
+    band_cfg = _native.variants(_native.KERNEL_BAND)
     cross = {}
     for name, N, K in LAYER_M1:
         rows = []
@@ -745,10 +749,31 @@ def bench_sweep(n_layers):
                                  torch.cuda.current_stream().cuda_stream, kernel, variant, split)
 
             k, v, sp = _native.plan(M, N, K)
-            tile_v, tile_sp = (v, sp) if k == _native.KERNEL_TILE else \
-                _native.plan(max(M, 17), N, K)[1:]
-            row = dict(M=M, tile_us=round(_timed_graph(
-                lambda: run(_native.KERNEL_TILE, tile_v, tile_sp), 5) * 1e3 / per, 2))
+            row = dict(M=M)
+            if M > 16 and k == _native.KERNEL_BAND:
+                # the plan takes the band kernel here; the tile beside it is the one the plan
+                # takes otherwise (its tile rule is the same for 33 .. 64 tokens, so M = 64's plan
+                # names it)
+                row["plan_kernel"] = "band"
+                row["plan_us"] = round(_timed_graph(
+                    lambda: run(_native.KERNEL_AUTO, -1, 0), 5) * 1e3 / per, 2)
+                tile_v, tile_sp = _native.plan(64, N, K)[1:]
+            else:
+                tile_v, tile_sp = (v, sp) if k == _native.KERNEL_TILE else \
+                    _native.plan(max(M, 17), N, K)[1:]
+            row["tile_us"] = round(_timed_graph(
+                lambda: run(_native.KERNEL_TILE, tile_v, tile_sp), 5) * 1e3 / per, 2)
+            if 16 < M <= 64:
+                # every band variant that serves the shape unsplit; the fastest is reported
+                band = []
+                for bv in range(len(band_cfg)):
+                    if _native.variant_serves(_native.KERNEL_BAND, bv, M, N, K, 1):
+                        band.append((_timed_graph(lambda: run(_native.KERNEL_BAND, bv, 1), 5)
+                                     * 1e3 / per, bv))
+                if band:
+                    t, bv = min(band)
+                    row["band_us"] = round(t, 2)
+                    row["band_variant"] = list(band_cfg[bv])
             if tile_sp > 1:
                 # the plan splits K here: the same tile unsplit beside it
                 row["tile_split"] = tile_sp
@@ -779,19 +804,21 @@ def bench_sweep(n_layers):
 
 
 CALIBRATION_BYTES = 256 * 2 ** 20
-# decode-band GEMMs in the counter runs: gate_up at M = 32 and 64, down at M = 17, 32, 48 and 64
-# (the plan splits down's K three ways up to M = 48)
-BAND_PROFILE = [(32, 17408, 5120), (64, 17408, 5120), (17, 5120, 8704), (32, 5120, 8704),
-                (48, 5120, 8704), (64, 5120, 8704)]
+# decode-band GEMMs in the counter runs: gate_up at M = 32, 48 and 64, qkv at M = 48 (the band
+# kernel's two plan points), down at M = 17, 32, 48 and 64 (the plan splits down's K three ways up
+# to M = 48)
+BAND_PROFILE = [(32, 17408, 5120), (48, 17408, 5120), (64, 17408, 5120), (48, 10240, 5120),
+                (17, 5120, 8704), (32, 5120, 8704), (48, 5120, 8704), (64, 5120, 8704)]
 
 
 def profile_workload():
     """The launches the committed rocprofv3 summaries are taken on: the verify GEMM (the bench's
     graph replay: one second of warmup replays, then 64 timed launches over 16 weight copies,
     plus 64 event-bracketed single launches), each prefill GEMM (4 launches, then 4 more on
-    fragment-tiled q behind its fused producer), gate_up at M = 32 and 64 and down at M = 17, 32,
-    48 and 64 (8 launches over 4 weight copies each), the four linears of the M = 1 layer
-    set on bf16 activations as the op runs them (8 launches over 4 weight copies each), each fused
+    fragment-tiled q behind its fused producer), gate_up at M = 32, 48 and 64, qkv at M = 48 and
+    down at M = 17, 32, 48 and 64 (8 launches over 4 weight copies each), the four linears of the
+    M = 1 layer set on bf16 activations as the op runs them (8 launches over 4 weight copies
+    each), each fused
     producer and the quantizer at M = 4096 (4 launches over 2 input copies each) and a plain
     256 MiB device copy
     (torch's copy kernel), whose FETCH_SIZE / WRITE_SIZE readings calibrate the counters: a copy

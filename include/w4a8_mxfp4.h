@@ -42,7 +42,8 @@ enum {
   W4A8_KERNEL_STREAM = 3,  /* whole k-range of every wave in flight at once, M <= 16 */
   W4A8_KERNEL_RING = 4,    /* per-wave pipeline of k-tile stages, M <= 64 (forced plans only) */
   W4A8_KERNEL_TILE_AT = 5, /* the macro tiles on fragment-tiled activations (same variants) */
-  W4A8_KERNEL_RING_AT = 6  /* the ring kernel on fragment-tiled activations (same variants) */
+  W4A8_KERNEL_RING_AT = 6, /* the ring kernel on fragment-tiled activations (same variants) */
+  W4A8_KERNEL_BAND = 7     /* weight waves + activation waves, 16 < M <= 64, optional K split */
 };
 
 /* Layouts of the producers' e4m3 output q (the q_layout argument).
@@ -131,8 +132,9 @@ int w4a8_tiled_bytes(int M, int K, size_t* bytes);
  * K-split form, which only the 4-wave tiles up to 64 tokens tall have (any other tile variant
  * returns W4A8_EINVAL): K over split_k workgroup rows writing fp32 partials to the registered
  * scratch (3 * M * N * 4 bytes for three splits), then a reducing launch; split_k 0 or 1 is one
- * launch. The stream and ring kernels (3, 4, 6) ignore split_k. Kernels 5 and 6 read
- * fragment-tiled activations. */
+ * launch. The band kernel (7) with split_k > 1 splits K over grid rows the same way (partials
+ * of split_k * M * N * 4 bytes, then the reducing launch). The stream and ring kernels (3, 4, 6)
+ * ignore split_k. Kernels 5 and 6 read fragment-tiled activations. */
 int w4a8_gemm_planned(const void* a, const float* a_scale, const void* wq, const void* sq, void* c,
                       int M, int N, int K, int kernel, int variant, int split_k, void* stream);
 
@@ -160,9 +162,22 @@ int w4a8_gemm_noalloc(const void* a, const float* a_scale, const void* wq, const
  *         forcing one that does not returns W4A8_EINVAL.
  * ring:   p = {MF (16-token fragments), NT (n-tiles per workgroup at most), D (k-tile stages in
  *         flight per wave), waves}. A ring variant serves (M, N, K) when M <= 16 * MF, the
- *         shape's n-tiles per workgroup fit NT and every wave owns a k-tile. */
+ *         shape's n-tiles per workgroup fit NT and every wave owns a k-tile.
+ * band:   p = {MF (16-token fragments), NT (n-tiles per workgroup at most), SG (scale dwords per
+ *         n-tile a weight wave holds), R (granule k-tiles in flight per weight wave)}. Four weight
+ *         waves and four activation waves per workgroup. A band variant serves (M, N, K, split_k)
+ *         when M <= 16 * MF, K % 128 == 0, the shape's n-tiles per workgroup fit NT, every weight
+ *         wave owns a k-tile and its k-range spans at most SG k-groups; split_k > 1 splits K over
+ *         grid rows (fp32 partials in registered scratch, split_k * M * N * 4 bytes, N % 16 == 0)
+ *         and adds a reducing launch. */
 int w4a8_variant_count(int kernel);
 int w4a8_variant_info(int kernel, int variant, int* p0, int* p1, int* p2, int* p3);
+
+/* 1 when w4a8_gemm_planned(kernel, variant, split_k) serves an M x N x K GEMM (the shape checks it
+ * makes before launching; registered scratch for a split is checked at the call), 0 when it
+ * would refuse the shape, -1 for an unknown kernel. For sweeps and tests; no counterpart in the
+ * reference. */
+int w4a8_variant_serves(int kernel, int variant, int M, int N, int K, int split_k);
 
 /* Diagnostic: the macro-tile variant's workgroup tile (bm tokens x bn columns), LDS pipeline
  * depth, waves per workgroup and static LDS bytes. No counterpart in the reference, whose tile
@@ -253,6 +268,14 @@ int w4a8_silu_mul_linear_fused(int M, int N, int K);
  * radiance::gdn_norm_quant (sly/mxfp4/radiance_fused_norm.py:189-220). */
 int w4a8_gdn_norm_quant(const void* x, const void* z, long z_stride, const void* weight, void* q,
                         float* scale, int M, int N, float eps, void* stream, int q_layout);
+
+/* Diagnostic: the producers' fp32 silu, x / (1 + exp(-x)), of n bf16 inputs (n % 8 == 0; x
+ * 16-byte aligned) into y fp32 [n], unrounded, through the same device function the gated norm
+ * and SiLU-and-mul evaluate (each consecutive 8 inputs are one of their 8-element groups). Lets a
+ * test compare the quotient with an exactly dividing restatement over every bf16 input. No
+ * counterpart in the reference, whose silu is libm's expf and an fp32 division
+ * (sly/mxfp4/radiance_mxfp4_fp8.hip:1962, :2109). */
+int w4a8_silu_f32(const void* x, float* y, int n, void* stream);
 
 /* Diagnostic: register-resident throughput probe of the scaled MFMA (fp4 A x fp8 B) the GEMMs
  * issue; shape 0 = 16x16x128, 1 = 32x32x64. Launches `blocks` workgroups of 4 waves that write

@@ -88,8 +88,13 @@ def test_gemm_with_m_zero_is_a_no_op(lib):
 
 def test_planned_rejects_unknown_kernel_and_variant(lib):
     p = 1 << 20
-    assert lib.w4a8_gemm_planned(p, p, p, p, p, 8, 16, 128, 7, 0, 1, None) == 1
+    assert lib.w4a8_gemm_planned(p, p, p, p, p, 8, 16, 128, 8, 0, 1, None) == 1
     assert b"unknown kernel" in lib.w4a8_last_error()
+    assert lib.w4a8_variant_serves(8, 0, 8, 16, 128, 1) == -1
+    # the band kernel (7): a variant index past its table, and one that does not serve the shape
+    assert lib.w4a8_gemm_planned(p, p, p, p, p, 32, 16, 128, 7, 999, 1, None) == 1
+    assert b"out of range" in lib.w4a8_last_error()
+    assert lib.w4a8_variant_serves(7, 999, 32, 5120, 5120, 1) == 0
     assert lib.w4a8_gemm_planned(p, p, p, p, p, 8, 16, 128, 1, 999, 1, None) == 1
     assert b"out of range" in lib.w4a8_last_error()
     # a skinny variant refuses an M it does not cover

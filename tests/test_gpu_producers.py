@@ -203,6 +203,63 @@ def test_gdn_norm_quant_bit_exact(gpu_lib, M, heads, extra):
     assert_same_qs(q, s, oq, os_, f"gdn M={M} heads={heads} z offset {extra}")
 
 
+def _silu_groups(bits):
+    """bf16 patterns -> the kernels' fp32 silu through w4a8_silu_f32 (len % 8 == 0)."""
+    x = bf16_dev(np.ascontiguousarray(bits, dtype=np.uint16))
+    y = torch.empty(len(bits), dtype=torch.float32, device="cuda")
+    _native.silu_f32(x.data_ptr(), y.data_ptr(), len(bits), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+def _assert_same_f32(got, want, bits, what):
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan), what
+    bad = np.argwhere(got[~nan].view(np.uint32) != want[~nan].view(np.uint32)).ravel()
+    assert bad.size == 0, (what, [(hex(int(b)), float(g), float(w)) for b, g, w in
+                                  zip(bits[~nan][bad[:6]], got[~nan][bad[:6]], want[~nan][bad[:6]])])
+
+
+def test_silu_quotient_every_bf16_input(gpu_lib):
+    """The unrounded fp32 silu the producers compute (the gated norm multiplies it into its
+    output), against the oracle's exact division for every bf16 input, on both of the kernels'
+    paths: groups of 8 inputs that all have |x| <= 44 take the hardware reciprocal and one
+    Markstein correction, any other group divides; every such input also goes through the
+    division path, by sharing its group with one wide value."""
+    print("[producers] silu fp32 over every bf16 input", flush=True)
+    allb = np.arange(65536, dtype=np.uint16)
+    xf = O.bf16_to_f32(allb)
+    narrow = allb[np.abs(xf) <= 44.0]                     # NaN compares false: wide
+    wide = allb[~(np.abs(xf) <= 44.0)]
+    pad = lambda a: np.r_[a, a[:(-len(a)) % 8]]
+    for what, bits in (("reciprocal path", pad(narrow)), ("division path", pad(wide))):
+        _assert_same_f32(_silu_groups(bits), P.silu_f32(O.bf16_to_f32(bits)), bits, what)
+    seven = np.r_[narrow, narrow[:(-len(narrow)) % 7]].reshape(-1, 7)
+    forced = np.c_[seven, np.full(len(seven), O.f32_to_bf16(np.float32([100.0]))[0])].ravel()
+    _assert_same_f32(_silu_groups(forced), P.silu_f32(O.bf16_to_f32(forced)), forced,
+                     "narrow inputs on the division path")
+
+
+def test_gdn_norm_quant_every_z(gpu_lib):
+    """The gated norm over every bf16 gate value z (65536 patterns, shuffled over 11 rows of 48
+    heads; the NaN and infinite z in their own rows, since one makes its whole row NaN)."""
+    rng = np.random.default_rng(3)
+    N = 48 * 128
+    allb = np.arange(65536, dtype=np.uint16)
+    special = ~np.isfinite(O.bf16_to_f32(allb))
+    fin = rng.permutation(allb[~special])
+    rows = -(-len(fin) // N)
+    z = np.r_[fin, rng.choice(fin, rows * N - len(fin))].reshape(rows, N)
+    zs = np.resize(rng.permutation(allb[special]), (2, N))
+    zall = np.r_[z, zs].astype(np.uint16)
+    M = zall.shape[0]
+    x = synthetic.activations(M, N, seed=5)
+    w = weight_bits(128, 7, mean=1.0, sd=0.2)
+    q, s = gpu_gdn(x, zall, 0, w, 1e-6)
+    oq, os_ = P.gdn_norm_quant(x, zall, w, 1e-6)
+    assert_same_qs(q, s, oq, os_, "gdn every z")
+
+
 def test_split_rows_equal_one_workgroup_rows(gpu_lib):
     """The two small-M silu paths on the same device inputs: identical codes and scales, a NaN row
     included (gate values over the whole exp range)."""

@@ -15,7 +15,7 @@ import threading
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libw4a8_mxfp4.so")
 ABI_VERSION = 2
 (KERNEL_AUTO, KERNEL_SKINNY, KERNEL_TILE, KERNEL_STREAM, KERNEL_RING, KERNEL_TILE_AT,
- KERNEL_RING_AT) = range(7)
+ KERNEL_RING_AT, KERNEL_BAND) = range(8)
 Q_ROWS, Q_TILED = 0, 1          # layouts of a producer's q
 
 _c = ctypes
@@ -42,6 +42,7 @@ SIGNATURES = {
     "w4a8_variant_count": (_int, [_int]),
     "w4a8_variant_info": (_int, [_int, _int, _pint, _pint, _pint, _pint]),
     "w4a8_tile_config": (_int, [_int, _pint, _pint, _pint, _pint, _pint]),
+    "w4a8_variant_serves": (_int, [_int, _int, _int, _int, _int, _int]),
     "w4a8_scratch_bytes": (_int, [_int, _int, _int, _psz, _psz]),
     "w4a8_workspace_bytes": (_int, [_int, _int, _psz, _psz]),
     "w4a8_linear": (_int, [_vp, _long, _vp, _vp, _vp, _vp, _vp, _int, _int, _int, _vp]),
@@ -55,6 +56,7 @@ SIGNATURES = {
     "w4a8_gdn_norm_quant": (_int, [_vp, _vp, _long, _vp, _vp, _vp, _int, _int, _c.c_float, _vp,
                                    _int]),
     "w4a8_mfma_probe": (_int, [_int, _vp, _int, _int, _c.POINTER(_c.c_double), _vp]),
+    "w4a8_silu_f32": (_int, [_vp, _vp, _int, _vp]),
     "w4a8_read_probe": (_int, [_vp, _long, _vp, _vp]),
     "w4a8_read_probe_variants": (_int, []),
     "w4a8_read_probe_variant_info": (_int, [_int, _pint, _pint, _pint, _pint]),
@@ -120,6 +122,14 @@ def gemm_noalloc(a_ptr, as_ptr, wq_ptr, sq_ptr, c_ptr, M, N, K, stream, kernel=K
 def gemm_at(a_ptr, as_ptr, wq_ptr, sq_ptr, c_ptr, M, N, K, stream):
     """The GEMM on fragment-tiled activations (a producer's q written with Q_TILED)."""
     check(lib().w4a8_gemm_at(a_ptr, as_ptr, wq_ptr, sq_ptr, c_ptr, M, N, K, stream))
+
+
+def variant_serves(kernel, variant, M, N, K, split_k=1) -> bool:
+    """Does a forced plan (kernel, variant, split_k) serve this shape (no launch)."""
+    r = lib().w4a8_variant_serves(kernel, variant, M, N, K, split_k)
+    if r < 0:
+        check(1)
+    return bool(r)
 
 
 def tiled_bytes(M: int, K: int) -> int:
@@ -223,6 +233,11 @@ def workspace_bytes(max_m: int, max_n: int):
     a, b = _sz(), _sz()
     check(lib().w4a8_workspace_bytes(max_m, max_n, _c.byref(a), _c.byref(b)))
     return a.value, b.value
+
+
+def silu_f32(x_ptr, y_ptr, n, stream) -> None:
+    """The producers' fp32 silu of n bf16 values (n % 8 == 0), unrounded (a diagnostic)."""
+    check(lib().w4a8_silu_f32(x_ptr, y_ptr, n, stream))
 
 
 def read_probe(buf_ptr, nbytes, out_ptr, stream) -> None:

@@ -21,7 +21,7 @@ LIB_PATH = os.path.join(PKG, LIB_NAME)
 ARCH = "gfx950"
 
 SOURCES = ["w4a8_api.hip", "w4a8_quant.hip", "w4a8_repack.hip", "w4a8_gemm_skinny.hip",
-           "w4a8_gemm_stream.hip", "w4a8_gemm_ring.hip", "w4a8_gemm_tile.hip",
+           "w4a8_gemm_stream.hip", "w4a8_gemm_ring.hip", "w4a8_gemm_tile.hip", "w4a8_gemm_band.hip",
            "w4a8_producers.hip", "w4a8_probe.hip"]
 
 FLAGS = [

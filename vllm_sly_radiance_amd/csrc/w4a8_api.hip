@@ -319,8 +319,28 @@ void plan_impl(int M, int N, int K, int dev, const Scratch& sc, int* kernel, int
     *split_k = ks;
     return;
   }
+  const DeviceInfo d = device_info(dev);
+  if (M > 32 && M <= 48 && N >= 8192) {
+    // 33 .. 48 tokens on the wide shapes: the band kernel (weight waves and activation waves),
+    // measured on MI355X against the plan's tiles, graph replays over rotating weights: qkv
+    // (10240 x 5120) 10.95 against 11.67 us at M = 48, gate_up (17408 x 5120) 14.15 against
+    // 14.58 us; on the narrow shapes and at M <= 32 or 64 the tiles are as fast or faster
+    // (the 48-token variant with the fewest n-tiles per workgroup that covers the shape: fewer
+    // registers, and qkv on 3 n-tiles measured 10.95 against 11.63 us on 5)
+    int best = -1;
+    for (int v = 0; v < band_variant_count(); ++v)
+      if (band_variant(v).mf == 3 && band_fits(v, M, N, K, d.cus, 1, d.lds) &&
+          (best < 0 || band_variant(v).nt < band_variant(best).nt))
+        best = v;
+    if (best >= 0) {
+      *kernel = W4A8_KERNEL_BAND;
+      *variant = best;
+      *split_k = 1;
+      return;
+    }
+  }
   *kernel = W4A8_KERNEL_TILE;
-  *split_k = band_split(M, N, K, device_info(dev).cus, sc, variant);
+  *split_k = band_split(M, N, K, d.cus, sc, variant);
   if (*split_k == 1) *variant = plan_tile(M, N, dev);
 }
 
@@ -450,6 +470,19 @@ int gemm_dispatch(const void* a, const float* as, const void* wq, const void* sq
       return fail(W4A8_EINVAL, "%s: ring variant %d does not serve M=%d N=%d K=%d", who, variant,
                   M, N, K);
     return hip_status(launch_ring(g, variant, d.cus, kernel == W4A8_KERNEL_RING_AT, st), who);
+  }
+  if (kernel == W4A8_KERNEL_BAND) {
+    if (variant < 0 || variant >= band_variant_count())
+      return fail(W4A8_EINVAL, "%s: band variant %d out of range", who, variant);
+    const DeviceInfo d = device_info(current_device());
+    const int splits = split_k > 1 ? split_k : 1;
+    if (!band_fits(variant, M, N, K, d.cus, splits, d.lds))
+      return fail(W4A8_EINVAL, "%s: band variant %d does not serve M=%d N=%d K=%d split_k=%d", who,
+                  variant, M, N, K, split_k);
+    if (band_split_bytes(M, N, splits) > sc.partial_bytes)
+      return fail(W4A8_ESCRATCH, "%s: band split_k=%d needs %zu B of partials; %s holds %zu B",
+                  who, split_k, band_split_bytes(M, N, splits), sc.what, sc.partial_bytes);
+    return hip_status(launch_band(g, variant, d.cus, splits, sc.partial, st), who);
   }
   if (kernel == W4A8_KERNEL_STREAM) {
     if (variant < 0 || variant >= stream_variant_count())
@@ -599,8 +632,39 @@ W4A8_API int w4a8_variant_count(int kernel) {
   if (kernel == W4A8_KERNEL_TILE || kernel == W4A8_KERNEL_TILE_AT) return tile_variant_count();
   if (kernel == W4A8_KERNEL_STREAM) return stream_variant_count();
   if (kernel == W4A8_KERNEL_RING || kernel == W4A8_KERNEL_RING_AT) return ring_variant_count();
+  if (kernel == W4A8_KERNEL_BAND) return band_variant_count();
   fail(W4A8_EINVAL, "w4a8_variant_count: unknown kernel %d", kernel);
   return -1;
+}
+
+W4A8_API int w4a8_variant_serves(int kernel, int variant, int M, int N, int K, int split_k) {
+  if (M < 1 || N < 1 || K < 1 || K % 32) return 0;
+  const DeviceInfo d = device_info(current_device());
+  const int splits = split_k > 1 ? split_k : 1;
+  switch (kernel) {
+    case W4A8_KERNEL_SKINNY:
+      return variant >= 0 && variant < skinny_variant_count() &&
+             M <= 16 * skinny_variant(variant).mt && splits <= 64;
+    case W4A8_KERNEL_TILE:
+    case W4A8_KERNEL_TILE_AT: {
+      if (variant < 0 || variant >= tile_variant_count() || !tile_fits(M, N, K)) return 0;
+      if (kernel == W4A8_KERNEL_TILE_AT && K % kKTile) return 0;
+      if (splits == 1) return 1;
+      return tile_splits(variant) && splits <= padded_k(K) / (kKTile * kKGroup) && N % kNTile == 0;
+    }
+    case W4A8_KERNEL_STREAM:
+      return variant >= 0 && variant < stream_variant_count() &&
+             stream_fits(variant, M, N, K, d.cus, d.lds);
+    case W4A8_KERNEL_RING:
+    case W4A8_KERNEL_RING_AT:
+      return variant >= 0 && variant < ring_variant_count() &&
+             ring_fits(variant, M, N, K, d.cus, d.lds) &&
+             (kernel == W4A8_KERNEL_RING || K % kKTile == 0);
+    case W4A8_KERNEL_BAND:
+      return band_fits(variant, M, N, K, d.cus, splits, d.lds);
+    default:
+      return fail(W4A8_EINVAL, "w4a8_variant_serves: unknown kernel %d", kernel), -1;
+  }
 }
 
 W4A8_API int w4a8_tile_config(int variant, int* bm, int* bn, int* stages, int* waves,
@@ -632,6 +696,9 @@ W4A8_API int w4a8_variant_info(int kernel, int variant, int* p0, int* p1, int* p
              variant < ring_variant_count()) {
     const RingCfg c = ring_variant(variant);
     v[0] = c.mf; v[1] = c.nt; v[2] = c.d; v[3] = c.waves;
+  } else if (kernel == W4A8_KERNEL_BAND && variant >= 0 && variant < band_variant_count()) {
+    const BandCfg c = band_variant(variant);
+    v[0] = c.mf; v[1] = c.nt; v[2] = c.sg; v[3] = c.r;
   } else {
     return fail(W4A8_EINVAL, "w4a8_variant_info: no variant %d of kernel %d", variant, kernel);
   }
@@ -875,6 +942,14 @@ W4A8_API int w4a8_gdn_norm_quant(const void* x, const void* z, long z_stride, co
   return hip_status(launch_gdn_norm_quant(x, z, z_stride, weight, (uint8_t*)q, scale, M, N, eps,
                                           q_layout == W4A8_Q_TILED, (hipStream_t)stream),
                     "w4a8_gdn_norm_quant");
+}
+
+W4A8_API int w4a8_silu_f32(const void* x, float* y, int n, void* stream) {
+  if (n < 0 || n % 8 || n > (1 << 28))
+    return fail(W4A8_EINVAL, "w4a8_silu_f32: n=%d must be a multiple of 8 in 0 .. 2^28", n);
+  if (n && (!x || !y || !aligned(x, 16) || !aligned(y, 4)))
+    return fail(W4A8_EINVAL, "w4a8_silu_f32: x needs 16-byte alignment, y 4-byte");
+  return hip_status(launch_silu_probe(x, y, n / 8, (hipStream_t)stream), "w4a8_silu_f32");
 }
 
 W4A8_API int w4a8_read_probe(const void* buf, long bytes, int* out, void* stream) {

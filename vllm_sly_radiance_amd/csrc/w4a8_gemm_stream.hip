@@ -244,10 +244,11 @@ __device__ __forceinline__ void fq_signal(int* counter) {
 template <int NT, int KPW, int W, bool SILU>
 __global__ __launch_bounds__(kFqWaves * 64) void gemm_stream_fq(
     const uint8_t* __restrict__ X, const uint8_t* __restrict__ Wq, const uint32_t* __restrict__ Sq,
-    int M, int K, int NTILES, int G, int ldx, uint16_t* __restrict__ C, int N, int vec_out) {
+    uint16_t* __restrict__ C, int M, int K, int N, int G, int ldx) {
   constexpr int Q = kFqWaves - W;                // quantizing waves
   static_assert(KPW % 4 == 0 && NT >= 1 && W >= 1 && Q >= 4 && Q <= 12, "fq variant");
   const int KT = K / kKTile, KG = KT / kKGroup;  // K % 512 == 0
+  const int NTILES = (N + kNTile - 1) / kNTile;
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
   uint8_t* const codes = lds;
   float* const tsc = reinterpret_cast<float*>(lds + KT * 1024);
@@ -383,18 +384,30 @@ __global__ __launch_bounds__(kFqWaves * 64) void gemm_stream_fq(
     for (int t = 0; t < NT; ++t) red[(wave * NT + t) * 64 + lane] = acc[t];
   }
 
-  // ---- the W partial sums of each n-tile, added in wave order ----
+  // ---- the W partial sums of each n-tile, added in wave order: only the lanes of tokens < M
+  //      (slot c of an n-tile: token c % 8, column group c / 8, lane 16 (c / 8) + c % 8), one
+  //      slot per thread, every partial read before the first add ----
   __syncthreads();
-  const bool vec = vec_out != 0;
-  const int m = lane & 15;
-  const float tok_scale = cnt[2] ? __builtin_nanf("") : tsc[m & 7];
-  for (int slot = tid; slot < nth * 64; slot += kFqWaves * 64) {
-    const int t = slot >> 6;                     // slot lane == this thread's lane
-    v4f v = red[t * 64 + lane];
-#pragma unroll 4
-    for (int w = 1; w < W; ++w) v += red[(w * NT + t) * 64 + lane];
-    const int n = (ntb0 + t) * kNTile + 4 * (lane >> 4);
-    if (m < M) store_out4(C, N, m, n, N, v, tok_scale, vec);
+  const int om = tid & 7;
+  if (tid < nth * 32 && om < M) {
+    const int t = tid >> 5, c = tid & 31, cl = ((c >> 3) << 4) | om;
+    const float tok_scale = cnt[2] ? __builtin_nanf("") : tsc[om];
+    v4f p[W];
+#pragma unroll
+    for (int w = 0; w < W; ++w) p[w] = red[(w * NT + t) * 64 + cl];
+    v4f v = p[0];
+#pragma unroll
+    for (int w = 1; w < W; ++w) v += p[w];
+    const int n = (ntb0 + t) * kNTile + 4 * (c >> 3);
+    uint16_t* row = C + (size_t)om * N;
+    if (N % 4 == 0 && ((uintptr_t)C & 7) == 0 && n + 3 < N) {
+      *reinterpret_cast<uint2*>(row + n) = make_uint2(bf16x2_rne(v[0] * tok_scale, v[1] * tok_scale),
+                                                      bf16x2_rne(v[2] * tok_scale, v[3] * tok_scale));
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (n + i < N) row[n + i] = (uint16_t)f32_to_bf16(v[i] * tok_scale);
+    }
   }
 }
 
@@ -478,8 +491,6 @@ bool stream_linear_fits(int variant, int M, int N, int K, long ldx, int cus, siz
 // kernel); otherwise g.a is e4m3 [M, K] and g.a_scale its per-token scales
 hipError_t launch_stream(const GemmArgs& g, int variant, int cus, bool fused, long lda,
                          hipStream_t stream, bool silu) {
-  const int NTILES = padded_n(g.N) / kNTile;
-  const int vec_out = (g.N % 4 == 0 && ((uintptr_t)g.c % 8) == 0) ? 1 : 0;
   const dim3 grid(stream_grid(g.N, cus)), block(kStream[variant].waves * 64);
   const size_t lds = stream_lds_bytes(variant, g.M, g.K, fused);
   int idx = 0;
@@ -503,15 +514,13 @@ hipError_t launch_stream(const GemmArgs& g, int variant, int cus, bool fused, lo
       if (fused && silu) {                                                                       \
         W4A8_STREAM_ATTR((gemm_stream_fq<nt, kpw, w, true>))                                     \
         hipLaunchKernelGGL((gemm_stream_fq<nt, kpw, w, true>), grid, dim3(kFqWaves * 64), lds,    \
-                           stream, g.a, g.wq, g.sq, g.M, g.K, NTILES, (int)grid.x, (int)lda,     \
-                           g.c, g.N, vec_out);                                                   \
+                           stream, g.a, g.wq, g.sq, g.c, g.M, g.K, g.N, (int)grid.x, (int)lda);  \
         return hipGetLastError();                                                                \
       }                                                                                          \
       if (fused) {                                                                               \
         W4A8_STREAM_ATTR((gemm_stream_fq<nt, kpw, w, false>))                                    \
         hipLaunchKernelGGL((gemm_stream_fq<nt, kpw, w, false>), grid, dim3(kFqWaves * 64), lds,   \
-                           stream, g.a, g.wq, g.sq, g.M, g.K, NTILES, (int)grid.x, (int)lda,     \
-                           g.c, g.N, vec_out);                                                   \
+                           stream, g.a, g.wq, g.sq, g.c, g.M, g.K, g.N, (int)grid.x, (int)lda);  \
         return hipGetLastError();                                                                \
       }                                                                                          \
     }                                                                                            \

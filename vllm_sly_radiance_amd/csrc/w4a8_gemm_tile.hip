@@ -568,6 +568,15 @@ __global__ __launch_bounds__(256) void split_reduce(const float* __restrict__ P,
   store_out4(C, ldc, m, n, N, v, As[m], vec_out != 0);
 }
 
+hipError_t launch_split_reduce(const float* partial, const GemmArgs& g, int splits,
+                               hipStream_t stream) {
+  const long threads = (long)g.M * (g.N / 4);
+  hipLaunchKernelGGL(split_reduce, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
+                     partial, g.a_scale, g.c, g.M, g.N, g.ldc, splits,
+                     (g.ldc % 4 == 0 && ((uintptr_t)g.c % 8) == 0) ? 1 : 0);
+  return hipGetLastError();
+}
+
 hipError_t launch_tile(const GemmArgs& g, int variant, bool a_tiled, hipStream_t stream,
                        float* partial, int splits) {
   const TileCfg c = kTile[variant];
@@ -585,11 +594,7 @@ hipError_t launch_tile(const GemmArgs& g, int variant, bool a_tiled, hipStream_t
     const hipError_t e = launch_tile_body(g, variant, a_tiled, stream, P, splits, KTp, KTe, KG,
                                           NTILES, grid_m, grid_n, vec_out, grid, block);
     if (e != hipSuccess) return e;
-    const long threads = (long)g.M * (g.N / 4);
-    hipLaunchKernelGGL(split_reduce, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
-                       P, g.a_scale, g.c, g.M, g.N, g.ldc, splits,
-                       (g.ldc % 4 == 0 && ((uintptr_t)g.c % 8) == 0) ? 1 : 0);
-    return hipGetLastError();
+    return launch_split_reduce(P, g, splits, stream);
   }
   return launch_tile_body(g, variant, a_tiled, stream, nullptr, 1, KTp, KTe, KG, NTILES, grid_m,
                           grid_n, vec_out, grid, block);

@@ -127,6 +127,8 @@ size_t producer_split_bytes(int M, int N);
 hipError_t launch_silu_mul_quant(const void* gate_up, uint8_t* q, float* scale, void* out, int M,
                                  int N, void* part, size_t part_bytes, bool tiled,
                                  hipStream_t stream);
+// diagnostic: the producers' fp32 silu of 8 * groups bf16 inputs (16-byte aligned), unrounded
+hipError_t launch_silu_probe(const void* x, float* y, int groups, hipStream_t stream);
 hipError_t launch_gdn_norm_quant(const void* x, const void* z, long zs, const void* w, uint8_t* q,
                                  float* scale, int M, int N, float eps, bool tiled,
                                  hipStream_t stream);
@@ -165,6 +167,20 @@ hipError_t launch_stream(const GemmArgs& g, int variant, int cus, bool fused, lo
 // Pipelined streaming family (M <= 16 * MF): grid = at most one workgroup per CU, each with the
 // same number of n-tiles (at most nt) and all of K; each of the `waves` waves streams a contiguous
 // k-range with d k-tile stages in flight. variant indexes the instantiated table.
+// decode-band kernel (16 < M <= 64): weight waves and activation waves, optional K split over
+// grid rows (fp32 partials, then split_reduce)
+struct BandCfg { int mf, nt, sg, r, d, l; };
+int band_variant_count();
+BandCfg band_variant(int v);
+int band_grid(int N, int cus, int splits);
+bool band_fits(int variant, int M, int N, int K, int cus, int splits, size_t lds_limit);
+size_t band_split_bytes(int M, int N, int splits);
+hipError_t launch_band(const GemmArgs& g, int variant, int cus, int splits, float* partial,
+                       hipStream_t stream);
+// adds `splits` fp32 partial planes P[s][M][N] in split order, scales and stores bf16 into g.c
+hipError_t launch_split_reduce(const float* partial, const GemmArgs& g, int splits,
+                               hipStream_t stream);
+
 struct RingCfg { int mf, nt, d, waves; };
 int ring_variant_count();
 RingCfg ring_variant(int v);

@@ -261,7 +261,28 @@ __global__ __launch_bounds__(64) void silu_mul_quant_split(const uint4* __restri
   split_tail<kQuant>(nb, in, q, scale, part, row, chunk, S, nv, tiled);
 }
 
+// Diagnostic: the fp32 silu of every producer (silu8, as the gated norm and SiLU-and-mul call
+// it) on 8 bf16 inputs per thread, written unrounded, so tests can compare the quotient itself
+// with the exactly dividing oracle for every bf16 input.
+__global__ __launch_bounds__(256) void silu_probe(const uint4* __restrict__ x, float* __restrict__ y,
+                                                  int groups) {
+  const int g = blockIdx.x * 256 + threadIdx.x;
+  if (g >= groups) return;
+  float a[8], s[8];
+  unpack8(x[g], a);
+  silu8(a, s);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) y[8 * g + j] = s[j];
+}
+
 }  // namespace
+
+hipError_t launch_silu_probe(const void* x, float* y, int groups, hipStream_t stream) {
+  if (groups == 0) return hipSuccess;
+  hipLaunchKernelGGL(silu_probe, dim3(ceil_div(groups, 256)), dim3(256), 0, stream,
+                     (const uint4*)x, y, groups);
+  return hipGetLastError();
+}
 
 // Rows at or below which silu_mul splits rows of more than 2048 groups (N > 16384) over one-wave
 // workgroups (when the caller registered scratch for the partial maxima); at 128 rows one

@@ -45,8 +45,11 @@ __device__ __forceinline__ float exp_f32(float y_in) {
 // has |x| <= 44 (1 <= d <= 2^64: the reciprocal is a normal number, nothing is infinite or NaN)
 // the quotient comes from the hardware reciprocal and one Markstein correction, y = rcp(d),
 // q = x y, r = fma(-d, q, x), q + r y, with x's sign (a -0 quotient would otherwise come out +0):
-// five operations instead of the division's ten. Any other group (rare) divides. Every bf16 x is
-// checked against the IEEE quotient on the GPU (the silu tests run all 65536 gate patterns).
+// five operations instead of the division's ten. Any other group (rare) divides. Markstein's
+// correction is proven correctly rounded only from a correctly rounded reciprocal, and v_rcp_f32
+// is within 1 ulp, so the unrounded quotient is checked on the GPU instead, against the IEEE
+// quotient for every bf16 x on both paths (w4a8_silu_f32; the SiLU-and-mul and gated-norm tests
+// also run every bf16 gate through the producers themselves).
 __device__ __forceinline__ void silu8(const float (&x)[8], float (&s)[8]) {
 #pragma clang fp contract(off)
   float d[8];
