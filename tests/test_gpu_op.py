@@ -182,3 +182,31 @@ def test_checkpoint_ingestion_end_to_end(kernel, tmp_path):
     w, ws = np.concatenate([g, u], 0), np.concatenate([gs, us], 0)
     q, s = O.quant_per_token(x)
     assert_gemm_close(host_u16(y), q, s, w, ws, "checkpoint gate_up M=8")
+
+
+def test_in_situ_exact_check_and_shape_log(kernel, monkeypatch, capsys):
+    """RADIANCE_MXFP4_CHECKALL and RADIANCE_MXFP4_MHIST on the device: every checked call of the
+    listed shape (one-launch and two-launch linears, the pre-quantized op, SiLU-mul + down) agrees
+    with the torch fp32 dequant-matmul, and each (N, K, M) is logged once with its plan."""
+    from vllm_sly_radiance_amd import diagnostics as D
+    N, K = 5120, 8704
+    monkeypatch.setattr(D, "CHECK_ALL", {(N, K)})
+    monkeypatch.setattr(D, "MHIST", True)
+    monkeypatch.setattr(D, "_seen", set())
+    w, ws = synthetic.weights(N, K, seed=41)
+    layer = Layer(w, ws)
+    kernel.process_weights_after_loading(layer)
+    before = (R.STATS.get("checked", 0), R.STATS.get("wrong", 0))
+    for M in (1, 8, 40):
+        x = bf16_dev(synthetic.activations(M, K, seed=M))
+        kernel.apply_weights(layer, x)
+        kernel.apply_weights(layer, R.quant_per_token(x))
+    gu = bf16_dev(synthetic.activations(1, 2 * K, seed=5))
+    torch.ops.radiance.silu_mul_mxfp4_linear(gu, layer.weight, layer.weight_scale,
+                                             layer.radiance_wref)
+    torch.cuda.synchronize()
+    err = capsys.readouterr().err
+    assert R.STATS["checked"] - before[0] == 7
+    assert R.STATS.get("wrong", 0) == before[1], err
+    for M in (1, 8, 40):
+        assert err.count(f"[radiance.mxfp4.mhist] N={N} K={K} M={M} ") == 1

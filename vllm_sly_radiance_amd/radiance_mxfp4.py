@@ -26,6 +26,7 @@ from collections import OrderedDict
 import torch
 
 from . import _native
+from . import diagnostics as _diag
 
 ENABLED = os.environ.get("RADIANCE_MXFP4_W4A8", "0") == "1"
 # The registered split-K scratch covers every automatic plan up to these M and N (the decode band,
@@ -204,6 +205,7 @@ def mxfp4_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tens
     beside the streaming GEMM, else two launches; the bits are the same either way. N and K come
     from weight_ref's shape (see module docstring)."""
     STATS["calls"] += 1
+    _diag.report_stats(STATS)
     N, K = weight_ref.shape[0], weight_ref.shape[1]
     if x.dim() != 2 or x.shape[1] != K:
         raise RuntimeError(f"[radiance.mxfp4] x {tuple(x.shape)} does not match K={K}")
@@ -216,6 +218,9 @@ def mxfp4_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tens
     s = torch.empty((M,), dtype=torch.float32, device=x.device)
     _native.linear(x.data_ptr(), x.stride(0), q.data_ptr(), s.data_ptr(), weight.data_ptr(),
                    weight_scale.data_ptr(), out.data_ptr(), M, N, K, _stream())
+    if _diag.enabled():
+        # the one-launch form keeps q in LDS: the check quantizes again (the same bits)
+        _diag.after_call(STATS, lambda: quant_per_token(x), None, weight, weight_scale, out, N, K)
     return out
 
 
@@ -233,6 +238,7 @@ def mxfp4_linear_pq(x_fp8: torch.Tensor, x_scale: torch.Tensor, weight: torch.Te
     tiled M x K is an [M, K] view over padded storage, so the shape is M either way).
     allow_tiled=False skips the lookup, for callers that quantized row-major themselves."""
     STATS["calls_pq"] += 1
+    _diag.report_stats(STATS)
     N, K = weight_ref.shape[0], weight_ref.shape[1]
     if x_fp8.dim() != 2 or x_fp8.shape[1] != K or not x_fp8.is_contiguous():
         raise RuntimeError(f"[radiance.mxfp4] x_fp8 {tuple(x_fp8.shape)} must be contiguous "
@@ -248,8 +254,11 @@ def mxfp4_linear_pq(x_fp8: torch.Tensor, x_scale: torch.Tensor, weight: torch.Te
         out = torch.empty((M, N), dtype=torch.bfloat16, device=x_fp8.device)
         _native.gemm_at(x_fp8.data_ptr(), xs.data_ptr(), weight.data_ptr(),
                         weight_scale.data_ptr(), out.data_ptr(), M, N, K, _stream())
-        return out
-    return gemm(x_fp8, xs, weight, weight_scale, N, K)
+        return out                  # fragment-tiled q: the row-major check does not apply
+    out = gemm(x_fp8, xs, weight, weight_scale, N, K)
+    if _diag.enabled():
+        _diag.after_call(STATS, x_fp8, xs, weight, weight_scale, out, N, K)
+    return out
 
 
 @mxfp4_linear_pq.register_fake
@@ -267,6 +276,7 @@ def silu_mul_mxfp4_linear(gate_up: torch.Tensor, weight: torch.Tensor, weight_sc
     825-860). At M <= 2 one launch: the streaming GEMM's quantizing waves form and quantize the
     SiLU-and-mul stage while its weight waves stream; otherwise the producer and the GEMM."""
     STATS["calls_silu"] += 1
+    _diag.report_stats(STATS)
     N, K = weight_ref.shape[0], weight_ref.shape[1]
     if gate_up.dim() != 2 or gate_up.shape[1] != 2 * K:
         raise RuntimeError(f"[radiance.mxfp4] gate_up {tuple(gate_up.shape)} does not match "
@@ -281,6 +291,15 @@ def silu_mul_mxfp4_linear(gate_up: torch.Tensor, weight: torch.Tensor, weight_sc
     if M:
         _native.silu_mul_linear(gate_up.data_ptr(), q.data_ptr(), s.data_ptr(), weight.data_ptr(),
                                 weight_scale.data_ptr(), out.data_ptr(), M, N, K, _stream())
+    if _diag.enabled():
+        def _quantized(gate_up=gate_up, M=M, K=K):
+            # the SiLU-and-mul producer's (q, scale): the one-launch form keeps them in LDS
+            q2 = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=gate_up.device)
+            s2 = torch.empty((M,), dtype=torch.float32, device=gate_up.device)
+            _native.silu_mul_quant(gate_up.data_ptr(), q2.data_ptr(), s2.data_ptr(), M, K,
+                                   _stream())
+            return q2, s2
+        _diag.after_call(STATS, _quantized, None, weight, weight_scale, out, N, K)
     return out
 
 
