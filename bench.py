@@ -973,7 +973,10 @@ def main():
                    "plan": list(v["plan"])},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic("verify")},
+                     "traffic": measured_traffic("verify"),
+                     "traffic_source": "profiles/traffic.json (rocprofv3 --pmc FETCH_SIZE, then "
+                                       "WRITE_SIZE, of bench.py --profile; not measured in this "
+                                       "run)"},
         "cpu_baseline": cpu,
         "kernel_us": round(v["kernel_us"], 3),
         "event_pair_us_median": round(v["event_pair_us_median"], 3),

@@ -115,7 +115,7 @@ def canon_nan(c):
                                      (4096, 5120, None), (4096, 8704, None), (300, 5120, None),
                                      (257, 8704, 8712),
                                      (256, 24, None), (261, 10240, None), (256, 10248, None),
-                                     (258, 1000, 1001)])
+                                     (258, 1000, 1001), (16, 16384, None), (100, 12304, None)])
 def test_quant_bit_exact(gpu_lib, M, K, ldx):
     x = synthetic.activations(M, K, seed=M * 7 + K)
     q, s = gpu_quant(x, ldx)

@@ -30,14 +30,21 @@ __device__ __forceinline__ uint32_t wave_max(uint32_t v) {
   return v;
 }
 
-// Row-wide max over the workgroup (all threads get the result).
-__device__ __forceinline__ uint32_t block_max(uint32_t v) {
-  __shared__ uint32_t red[kThreads / 64];
+// Row-wide max over a workgroup of T threads (all threads get the result).
+template <int T>
+__device__ __forceinline__ uint32_t block_max_t(uint32_t v) {
+  static_assert(T % 64 == 0 && T >= 64 && T <= 1024, "threads");
+  __shared__ uint32_t red[T / 64];
   v = wave_max(v);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
-  return max(max(red[0], red[1]), max(red[2], red[3]));
+  uint32_t m = red[0];
+#pragma unroll
+  for (int i = 1; i < T / 64; ++i) m = max(m, red[i]);
+  return m;
 }
+
+__device__ __forceinline__ uint32_t block_max(uint32_t v) { return block_max_t<kThreads>(v); }
 
 __device__ __forceinline__ uint32_t abs_bits_max8(const uint4 v) {
   uint32_t m = max(v.x & 0x7FFFu, (v.x >> 16) & 0x7FFFu);
