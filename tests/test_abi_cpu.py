@@ -126,6 +126,25 @@ def test_plan_bands(lib):
     assert lib.w4a8_plan(8, 17408, 5000, ctypes.byref(k), ctypes.byref(v), ctypes.byref(s)) == 1
 
 
+@pytest.mark.parametrize("M,N,K,band_nt", [
+    (33, 17408, 5120, 5), (40, 17408, 5120, 5), (48, 17408, 5120, 5), (48, 10240, 5120, 3),
+    (33, 10240, 5120, 3), (32, 17408, 5120, None), (49, 17408, 5120, None), (64, 10240, 5120, None),
+    (48, 5120, 8704, None), (48, 5120, 6144, None), (40, 8192, 5120, 2)])
+def test_plan_band_kernel_between_33_and_48_tokens(lib, M, N, K, band_nt):
+    """The band kernel (weight waves + activation waves) is the plan for 33..48 tokens on shapes of
+    at least 8192 columns, with 48-token fragments and the fewest n-tiles per workgroup that cover
+    the shape in one round; elsewhere in the band the macro tiles."""
+    k, v, s = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    assert lib.w4a8_plan(M, N, K, ctypes.byref(k), ctypes.byref(v), ctypes.byref(s)) == 0
+    if band_nt is None:
+        assert k.value == _native.KERNEL_TILE
+        return
+    assert (k.value, s.value) == (_native.KERNEL_BAND, 1)
+    mf, nt = _native.variants(_native.KERNEL_BAND)[v.value][:2]
+    assert (mf, nt) == (3, band_nt)
+    assert lib.w4a8_variant_serves(_native.KERNEL_BAND, v.value, M, N, K, 1) == 1
+
+
 def test_one_launch_linear_where_it_pays(lib):
     """w4a8_linear runs as one launch (quantizing waves beside the streaming GEMM's weight waves)
     at M <= 2, and up to M = 4 where a workgroup holds 3 or more n-tiles or a quantizing wave
