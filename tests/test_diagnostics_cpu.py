@@ -97,3 +97,30 @@ def test_parse_shapes_and_report_stats(capsys, monkeypatch):
     D.report_stats({"fast": 9, "refused": 9})
     err = capsys.readouterr().err
     assert err.count("[radiance.mxfp4] linear layers: 3/4 on the gfx950 W4A8 kernels, 1 refused") == 1
+
+
+def test_sanitize_zeroes_non_finite_inputs(monkeypatch):
+    x = torch.tensor([[1.0, float("nan"), float("inf"), -float("inf"), -2.5]], dtype=torch.bfloat16)
+    monkeypatch.setattr(D, "SANITIZE_X", False)
+    assert D.sanitize(x) is x
+    monkeypatch.setattr(D, "SANITIZE_X", True)
+    y = D.sanitize(x)
+    assert y.dtype == torch.bfloat16 and y.tolist() == [[1.0, 0.0, 0.0, 0.0, -2.5]]
+    assert torch.isnan(x[0, 1])                              # the input itself is left alone
+
+
+def test_health_report_once_per_shape_and_capped(diag, capsys, monkeypatch):
+    q, s, wq, sq, out, N, K = _case()
+    monkeypatch.setattr(D, "CHECK_X", True)
+    monkeypatch.setattr(D, "CHECK_ALL", None)
+    monkeypatch.setattr(D, "MHIST", False)
+    x = torch.ones((out.shape[0], K), dtype=torch.bfloat16)
+    x[0, 0] = float("nan")
+    D.after_call({}, q, s, wq, sq, out, N, K, x=x)
+    D.after_call({}, q, s, wq, sq, out, N, K, x=x)
+    err = capsys.readouterr().err
+    assert err.count("[radiance.mxfp4.x] N=32 K=512 M=4 ") == 1 and "x_nonfin=1 " in err
+    assert "out_nonfin=0" in err
+    monkeypatch.setattr(D, "CHECK_X_MAX", 1)
+    D.after_call({}, q, s, wq, sq, out[:2], N, K)               # a new shape past the cap
+    assert capsys.readouterr().err == ""

@@ -210,3 +210,34 @@ def test_in_situ_exact_check_and_shape_log(kernel, monkeypatch, capsys):
     assert R.STATS.get("wrong", 0) == before[1], err
     for M in (1, 8, 40):
         assert err.count(f"[radiance.mxfp4.mhist] N={N} K={K} M={M} ") == 1
+
+
+def test_sanitize_and_sync_switches(kernel, monkeypatch):
+    """RADIANCE_MXFP4_SANITIZE zeroes NaN and inf in the bf16 activations before the quantizer: a
+    row holding a NaN gives the output of the cleaned row instead of a NaN row (one-launch and
+    two-launch forms). RADIANCE_MXFP4_SYNC only synchronizes: the same bits."""
+    from vllm_sly_radiance_amd import diagnostics as D
+    N, K = 5120, 5120
+    w, ws = synthetic.weights(N, K, seed=43)
+    layer = Layer(w, ws)
+    kernel.process_weights_after_loading(layer)
+    for M in (1, 8):
+        x = bf16_dev(synthetic.activations(M, K, seed=7 + M))
+        bad = x.clone()
+        bad[0, 5] = float("nan")
+        bad[M - 1, 9] = float("inf")
+        clean = bad.clone()
+        clean[0, 5] = 0.0
+        clean[M - 1, 9] = 0.0
+        monkeypatch.setattr(D, "SANITIZE_X", False)
+        y_bad = kernel.apply_weights(layer, bad)
+        assert torch.isnan(y_bad[0].float()).all()
+        y_clean = kernel.apply_weights(layer, clean)
+        monkeypatch.setattr(D, "SANITIZE_X", True)
+        assert torch.equal(kernel.apply_weights(layer, bad), y_clean)
+        assert torch.isnan(bad[0, 5])                        # the caller's tensor is untouched
+        monkeypatch.setattr(D, "SANITIZE_X", False)
+        for mode in ("1", "2"):
+            monkeypatch.setattr(D, "SYNC", mode)
+            assert torch.equal(kernel.apply_weights(layer, x), kernel.apply_weights(layer, x))
+        monkeypatch.setattr(D, "SYNC", "0")

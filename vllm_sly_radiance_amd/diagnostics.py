@@ -1,6 +1,6 @@
 """In-situ diagnostics of the linear path, off by default and free when off.
 
-The reference's op body carries three of them, and they keep its switch names:
+The reference's op body carries these, and they keep its switch names:
   RADIANCE_MXFP4_CHECKALL="N:K,N:K"  every call of the listed shapes with M <= CHECK_MAX_M
                                      (RADIANCE_MXFP4_CHECK_MAX_M, default 128) is compared with an
                                      fp32 dequant-then-matmul of the same e4m3 activations and the
@@ -10,6 +10,15 @@ The reference's op body carries three of them, and they keep its switch names:
                                      (sly/mxfp4/radiance_mxfp4.py:470-477, :761-785).
   RADIANCE_MXFP4_MHIST=1             every distinct (N, K, M) is reported once, with the plan the
                                      library takes for it (:500-502, :755-760).
+  RADIANCE_MXFP4_CHECKX=1            each distinct (N, K, M), the first 60, reports the health of
+                                     its input and output: mean and max magnitude and non-finite
+                                     counts (:468-469, :786-799)
+  RADIANCE_MXFP4_SYNC=1 / 2          synchronize the op's stream / the whole device after every
+                                     call, to tell ordering faults from wrong values (:425-431,
+                                     :800-803)
+  RADIANCE_MXFP4_SANITIZE=1          zero NaN and inf in the bf16 activations before they are
+                                     quantized (a NaN otherwise makes its row's scale, and so the
+                                     whole output row, NaN; :450-466, :715-716)
   report_stats()                     the one-shot tally of layers on the HIP kernel and layers
                                      refused at load (:941-957). It is called from op bodies only:
                                      they are opaque to dynamo, so a stderr write there cannot
@@ -43,6 +52,10 @@ def parse_shapes(spec: str):
 CHECK_ALL = parse_shapes(os.environ.get("RADIANCE_MXFP4_CHECKALL", ""))
 CHECK_MAX_M = int(os.environ.get("RADIANCE_MXFP4_CHECK_MAX_M", "128"))
 MHIST = os.environ.get("RADIANCE_MXFP4_MHIST", "0") == "1"
+CHECK_X = os.environ.get("RADIANCE_MXFP4_CHECKX", "0") == "1"
+SYNC = os.environ.get("RADIANCE_MXFP4_SYNC", "0")
+SANITIZE_X = os.environ.get("RADIANCE_MXFP4_SANITIZE", "0") == "1"
+CHECK_X_MAX = 60
 WRONG_REL = 0.02
 
 KERNEL_NAMES = {_native.KERNEL_SKINNY: "skinny", _native.KERNEL_TILE: "tile",
@@ -101,13 +114,46 @@ def report_stats(stats: dict) -> None:
 
 
 def enabled() -> bool:
-    return MHIST or CHECK_ALL is not None
+    return MHIST or CHECK_ALL is not None or CHECK_X or SYNC in ("1", "2")
 
 
-def after_call(stats: dict, x_fp8, x_scale, wq, sq, out, N: int, K: int) -> None:
-    """Run the enabled diagnostics on one finished call. x_fp8 / x_scale are the call's e4m3
-    activations and token scales, or a callable returning them (computed only if a check runs)."""
+def sanitize(x: torch.Tensor) -> torch.Tensor:
+    """x with NaN and inf zeroed when RADIANCE_MXFP4_SANITIZE=1 (a new tensor), else x itself."""
+    if not SANITIZE_X:
+        return x
+    return torch.nan_to_num(x, nan=0.0, posinf=0.0, neginf=0.0)
+
+
+def _health(x: torch.Tensor | None, out: torch.Tensor, N: int, K: int) -> None:
     M = int(out.shape[0])
+    key = ("x", N, K, M)
+    if key in _seen or sum(1 for k in _seen if k[0] == "x") >= CHECK_X_MAX:
+        return
+    _seen.add(key)
+    of = out.float()
+    head = f"[radiance.mxfp4.x] N={N} K={K} M={M} "
+    if x is not None:
+        xf = x.float()
+        head += (f"|x|={xf.abs().mean().item():.5f} xmax={xf.abs().max().item():.5f} "
+                 f"x_nonfin={int((~torch.isfinite(xf)).sum().item())} | ")
+    sys.stderr.write(head + f"|out|={of.abs().mean().item():.5f} "
+                     f"outmax={of.abs().max().item():.5f} "
+                     f"out_nonfin={int((~torch.isfinite(of)).sum().item())}\n")
+    sys.stderr.flush()
+
+
+def after_call(stats: dict, x_fp8, x_scale, wq, sq, out, N: int, K: int, x=None) -> None:
+    """Run the enabled diagnostics on one finished call. x_fp8 / x_scale are the call's e4m3
+    activations and token scales, or a callable returning them (computed only if a check runs);
+    x is the bf16 input where the op has one (for the health report)."""
+    M = int(out.shape[0])
+    capturing = torch.cuda.is_current_stream_capturing()
+    if SYNC == "1" and not capturing:
+        torch.cuda.current_stream().synchronize()
+    elif SYNC == "2" and not capturing:
+        torch.cuda.synchronize()
+    if CHECK_X and not capturing and M:
+        _health(x, out, N, K)
     if MHIST and ("m", N, K, M) not in _seen:
         _seen.add(("m", N, K, M))
         k, v, s = _native.plan(M, N, K) if M else (0, -1, 1)
@@ -116,7 +162,7 @@ def after_call(stats: dict, x_fp8, x_scale, wq, sq, out, N: int, K: int) -> None
         sys.stderr.flush()
     if CHECK_ALL is None or (N, K) not in CHECK_ALL or M == 0 or M > CHECK_MAX_M:
         return
-    if torch.cuda.is_current_stream_capturing():
+    if capturing:
         return
     if callable(x_fp8):
         x_fp8, x_scale = x_fp8()

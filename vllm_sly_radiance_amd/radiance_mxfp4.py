@@ -213,6 +213,7 @@ def mxfp4_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tens
         raise RuntimeError(f"[radiance.mxfp4] x must be bf16 with unit column stride, got "
                            f"{x.dtype} stride {x.stride()}")
     M = x.shape[0]
+    x = _diag.sanitize(x)
     out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
     q = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=x.device)
     s = torch.empty((M,), dtype=torch.float32, device=x.device)
@@ -220,7 +221,8 @@ def mxfp4_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tens
                    weight_scale.data_ptr(), out.data_ptr(), M, N, K, _stream())
     if _diag.enabled():
         # the one-launch form keeps q in LDS: the check quantizes again (the same bits)
-        _diag.after_call(STATS, lambda: quant_per_token(x), None, weight, weight_scale, out, N, K)
+        _diag.after_call(STATS, lambda: quant_per_token(x), None, weight, weight_scale, out, N, K,
+                         x=x)
     return out
 
 
@@ -299,7 +301,7 @@ def silu_mul_mxfp4_linear(gate_up: torch.Tensor, weight: torch.Tensor, weight_sc
             _native.silu_mul_quant(gate_up.data_ptr(), q2.data_ptr(), s2.data_ptr(), M, K,
                                    _stream())
             return q2, s2
-        _diag.after_call(STATS, _quantized, None, weight, weight_scale, out, N, K)
+        _diag.after_call(STATS, _quantized, None, weight, weight_scale, out, N, K, x=gate_up)
     return out
 
 
