@@ -1,8 +1,8 @@
 """CPU oracle for the MXFP4 W4A8 linear path. TEST INFRASTRUCTURE ONLY.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
-import this module, and only as the checker. The product path (``vllm_sly_radiance_amd``) never
-imports it and fails loudly when its HIP library is missing.
+import this module, and only as the reference their results are compared with. The product path
+(``vllm_sly_radiance_amd``) never imports it and fails loudly when its HIP library is missing.
 
 Everything here is plain numpy on the host. bf16 tensors are carried as their raw ``uint16`` bit
 patterns and fp8 e4m3fn / e8m0 / packed e2m1 as ``uint8``, so no array ever depends on a torch

@@ -1,6 +1,7 @@
 """CPU oracle for the fused fp8 activation producers. TEST INFRASTRUCTURE ONLY.
 
-Only ``tests/`` may import this module, and only as the checker; the product path never does.
+Only ``tests/`` may import this module, and only as the reference their results are compared
+with; the product path never does.
 
 The producers sit in front of the W4A8 GEMMs and end in the same per-token e4m3 quantizer as
 ``mxfp4_oracle.quant_per_token`` (the reference's ``_traced_quant``), so the (q, scale) pair they

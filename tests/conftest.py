@@ -14,8 +14,8 @@ def pytest_configure(config):
 
 @pytest.fixture(scope="session")
 def gpu_lib():
-    """The C-ABI library on a GPU, or a skip when there is no GPU. On a GPU box a missing or
-    unloadable library is an error, never a skip."""
+    """The C-ABI library on a GPU, or a skip when there is no GPU. On a machine with a GPU a
+    missing or unloadable library is an error, never a skip."""
     import torch
     if not torch.cuda.is_available():
         pytest.skip("no GPU")

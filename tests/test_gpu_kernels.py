@@ -589,7 +589,7 @@ def test_band_split_plan_for_down(gpu_lib):
 
 
 # ---- diagnostics --------------------------------------------------------------------------------
-BASELINE_SHAPES = [(10240, 5120), (5120, 6144), (17408, 5120), (5120, 8704)]
+MODEL_SHAPES = [(10240, 5120), (5120, 6144), (17408, 5120), (5120, 8704)]
 
 
 def test_plugin_scratch_covers_every_automatic_plan(gpu_lib):
@@ -604,7 +604,7 @@ def test_plugin_scratch_covers_every_automatic_plan(gpu_lib):
     assert part.numel() * 4 < 8 << 20, "the plugin scratch should be a few MB at most"
     big_p = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
     big_c = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
-    shapes = BASELINE_SHAPES + [(n, k) for n in range(16, 2049, 16) for k in (1056, 4128)]
+    shapes = MODEL_SHAPES + [(n, k) for n in range(16, 2049, 16) for k in (1056, 4128)]
     ms = list(range(1, 65))
     try:
         plans = {}
