@@ -63,6 +63,35 @@ __device__ __forceinline__ uint32_t block_max_t(uint32_t v) {
   return m;
 }
 
+// Groups tid, tid + T, ... of one row (of two rows, interleaved) into registers, zeros past the
+// row's nv groups. The loads go through a buffer resource that ends at the row, so they need no
+// branch (past the end the hardware returns zeros without an access), and callers load everything
+// a row needs before they use any of it: every load is then in flight at once. A load behind a
+// branch, a store or a reduction waits for the previous one's round trip.
+__device__ __forceinline__ uint4 load_group(const __amdgpu_buffer_rsrc_t r, int g) {
+  const v4i t = __builtin_amdgcn_raw_buffer_load_b128(r, g * 16, 0, 0);
+  return make_uint4(t[0], t[1], t[2], t[3]);
+}
+
+template <int G, int T>
+__device__ __forceinline__ void load_groups(const uint4* a, int nv, uint4 (&av)[G]) {
+  const auto ra = __builtin_amdgcn_make_buffer_rsrc((void*)a, 0, nv * 16, kBufferWord3);
+#pragma unroll
+  for (int i = 0; i < G; ++i) av[i] = load_group(ra, threadIdx.x + i * T);
+}
+
+template <int G, int T>
+__device__ __forceinline__ void load_groups(const uint4* a, int nv, uint4 (&av)[G],
+                                            uint4 (&bv)[G], const uint4* b) {
+  const auto ra = __builtin_amdgcn_make_buffer_rsrc((void*)a, 0, nv * 16, kBufferWord3);
+  const auto rb = __builtin_amdgcn_make_buffer_rsrc((void*)b, 0, nv * 16, kBufferWord3);
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    av[i] = load_group(ra, threadIdx.x + i * T);
+    bv[i] = load_group(rb, threadIdx.x + i * T);
+  }
+}
+
 // Byte offset of 8-element group g of row `row` in q (nv groups per row): row-major, or the
 // fragment-tiled layout the tile GEMM reads (16-token blocks of 16 x K bytes; in block b, k-tile t,
 // half h, lane l's 16 bytes at ((b KT + t) 2 + h) 1024 + 16 l hold token 16 b + l % 16, k-bytes
@@ -108,20 +137,17 @@ __global__ __launch_bounds__(kThreads) void add_rms_quant(
   res_out += (size_t)row * nv;
   float v[G][8];
   float part = 0.0f;
-  // the weight groups are requested with the row, so no load waits behind the row's reduction
-  uint4 wv[G];
-#pragma unroll
-  for (int i = 0; i < G; ++i) {
-    const int g = tid + i * kThreads;
-    wv[i] = g < nv ? w[g] : make_uint4(0, 0, 0, 0);
-  }
+  // the weight groups are requested with the row and last, as they are used after its reduction
+  uint4 yv[G], rv[G], wv[G];
+  load_groups<G, kThreads>(y, nv, yv, rv, res);
+  load_groups<G, kThreads>(w, nv, wv);
 #pragma unroll
   for (int i = 0; i < G; ++i) {
     const int g = tid + i * kThreads;
     if (g < nv) {
       float a[8], b[8];
-      unpack8(y[g], a);
-      unpack8(res[g], b);
+      unpack8(yv[i], a);
+      unpack8(rv[i], b);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         v[i][j] = a[j] + b[j];
@@ -158,11 +184,12 @@ __global__ __launch_bounds__(T) void silu_mul_quant(const uint4* __restrict__ gu
   const int row = blockIdx.x, tid = threadIdx.x, nv = N >> 3;
   const uint4* gate = gu + (size_t)row * 2 * nv;
   const uint4* up = gate + nv;
-  uint4 nb[G];
+  uint4 gv[G], uv[G], nb[G];
+  load_groups<G, T>(gate, nv, gv, uv, up);
 #pragma unroll
   for (int i = 0; i < G; ++i) {
     const int g = tid + i * T;
-    if (g < nv) nb[i] = silu_mul_group(gate[g], up[g]);
+    if (g < nv) nb[i] = silu_mul_group(gv[i], uv[i]);
   }
   if (out) {
 #pragma unroll
@@ -175,23 +202,23 @@ __global__ __launch_bounds__(T) void silu_mul_quant(const uint4* __restrict__ gu
   quant_tail<G, T>(nb, nv, q, scale, row, tiled);
 }
 
-// One 8-element group of the per-head gated RMSNorm. All 16 lanes of a head call it together
-// (`in` is the same for the whole head); lanes past the row return zeros.
-__device__ __forceinline__ uint4 gdn_group(const uint4* __restrict__ x,
-                                           const uint4* __restrict__ zr,
-                                           const uint4* __restrict__ w, int g, bool in, float eps) {
+// One 8-element group of the per-head gated RMSNorm from its loaded x, z and weight groups. All 16
+// lanes of a head call it together. It runs on every lane of a wave that holds part of the row: a
+// group past the row holds zeros (the result is finite and never stored), and with no branch per
+// group the compiler cannot sink a group's z load behind x's round trip.
+__device__ __forceinline__ uint4 gdn_group(const uint4 xv, const uint4 zv, const uint4 wv,
+                                           float eps) {
   float v[8];
-  unpack8(in ? x[g] : make_uint4(0, 0, 0, 0), v);
+  unpack8(xv, v);
   float part = 0.0f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) part = part + v[j] * v[j];
 #pragma unroll
   for (int o = 8; o > 0; o >>= 1) part = part + __shfl_xor(part, o, 16);
-  if (!in) return make_uint4(0, 0, 0, 0);
   const float inv = 1.0f / sqrtf(part * (1.0f / 128.0f) + eps);
   float zz[8], sz[8], wf[8], n[8];
-  unpack8(zr[g], zz);
-  unpack8(w[g & 15], wf);
+  unpack8(zv, zz);
+  unpack8(wv, wf);
   silu8(zz, sz);
 #pragma unroll
   for (int j = 0; j < 8; ++j) n[j] = ((v[j] * inv) * wf[j]) * sz[j];
@@ -210,11 +237,17 @@ __global__ __launch_bounds__(T) void gdn_norm_quant(
   const int row = blockIdx.x, tid = threadIdx.x, nv = N >> 3;
   x += (size_t)row * nv;
   const uint4* zr = reinterpret_cast<const uint4*>(z + (size_t)row * zs);
-  uint4 nb[G];
+  uint4 xv[G], zv[G], wv[G], nb[G];
+  load_groups<G, T>(x, nv, xv, zv, zr);
+  const auto rw = __builtin_amdgcn_make_buffer_rsrc((void*)w, 0, 16 * 16, kBufferWord3);
 #pragma unroll
   for (int i = 0; i < G; ++i) {
-    const int g = tid + i * T;
-    nb[i] = gdn_group(x, zr, w, g, g < nv, eps);
+    wv[i] = load_group(rw, (tid + i * T) & 15);                     // the head's 16 groups
+    nb[i] = make_uint4(0, 0, 0, 0);
+  }
+  if ((tid & ~63) < nv) {                     // the same for the whole wave: waves past the row skip
+#pragma unroll
+    for (int i = 0; i < G; ++i) nb[i] = gdn_group(xv[i], zv[i], wv[i], eps);
   }
   quant_tail<G, T>(nb, nv, q, scale, row, tiled);
 }
