@@ -24,10 +24,64 @@ constexpr int kThreads = 256;
 constexpr float kInv448 = 1.0f / 448.0f;            // fl32(1/448), folded at compile time
 constexpr float kMinScale = 1.0f / (448.0f * 512.0f);
 
+// Cross-lane exchange for xor butterflies, in registers (no LDS round trip per step).
+//  * lane ^ 32 and lane ^ 16: v_permlane32_swap / v_permlane16_swap with both operands v leave
+//    each lane holding its own value in one result and its partner's in the other, so the step
+//    combines the pair (a sum is exact in either operand order, as a + b == b + a);
+//  * lane ^ 8, 4, 2, 1: DPP moves within rows of 16 lanes: quad_perm [1,0,3,2] (^1),
+//    [2,3,0,1] (^2); half-row mirror then quad_perm [3,2,1,0] (^4); row mirror then half-row
+//    mirror (^8).
+template <int Ctrl>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, Ctrl, 0xF, 0xF, false);
+}
+
+// The value lane (l ^ O) holds, O in {1, 2, 4, 8}.
+template <int O>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+  static_assert(O == 1 || O == 2 || O == 4 || O == 8, "within a row of 16 lanes");
+  if constexpr (O == 1) return dpp<0xB1>(v);
+  else if constexpr (O == 2) return dpp<0x4E>(v);
+  else if constexpr (O == 4) return dpp<0x1B>(dpp<0x141>(v));
+  else return dpp<0x141>(dpp<0x140>(v));
+}
+
+// {own, partner} for partner lane l ^ 32 (Half = 32) or l ^ 16 (Half = 16), in some order.
+template <int Half>
+__device__ __forceinline__ uint2 swap_pair(uint32_t v) {
+  static_assert(Half == 16 || Half == 32, "lane halves");
+  if constexpr (Half == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return make_uint2(r[0], r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return make_uint2(r[0], r[1]);
+  }
+}
+
+// Wave-wide max by an xor butterfly (every lane gets it).
 __device__ __forceinline__ uint32_t wave_max(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, 64));
-  return v;
+  uint2 p = swap_pair<32>(v);
+  v = max(p.x, p.y);
+  p = swap_pair<16>(v);
+  v = max(p.x, p.y);
+  v = max(v, xor_lane<8>(v));
+  v = max(v, xor_lane<4>(v));
+  v = max(v, xor_lane<2>(v));
+  return max(v, xor_lane<1>(v));
+}
+
+// Wave-wide sum in the fixed xor-butterfly order 32, 16, 8, 4, 2, 1: at each step every lane
+// adds its value and lane (l ^ o)'s, so every lane ends with the same, reproducible sum.
+__device__ __forceinline__ float wave_sum_xor(float v) {
+  uint2 p = swap_pair<32>(__float_as_uint(v));
+  v = __uint_as_float(p.x) + __uint_as_float(p.y);
+  p = swap_pair<16>(__float_as_uint(v));
+  v = __uint_as_float(p.x) + __uint_as_float(p.y);
+  v = v + __uint_as_float(xor_lane<8>(__float_as_uint(v)));
+  v = v + __uint_as_float(xor_lane<4>(__float_as_uint(v)));
+  v = v + __uint_as_float(xor_lane<2>(__float_as_uint(v)));
+  return v + __uint_as_float(xor_lane<1>(__float_as_uint(v)));
 }
 
 // Row-wide max over a workgroup of T threads (all threads get the result).

@@ -40,8 +40,7 @@ using namespace prod;
 // Row sum over the workgroup in the fixed order (every thread gets the result).
 __device__ __forceinline__ float block_sum_fixed(float v) {
   __shared__ float red[kThreads / 64];
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o, 64);
+  v = wave_sum_xor(v);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
   float t = red[0];
@@ -213,8 +212,10 @@ __device__ __forceinline__ uint4 gdn_group(const uint4 xv, const uint4 zv, const
   float part = 0.0f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) part = part + v[j] * v[j];
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) part = part + __shfl_xor(part, o, 16);
+  part = part + __uint_as_float(xor_lane<8>(__float_as_uint(part)));
+  part = part + __uint_as_float(xor_lane<4>(__float_as_uint(part)));
+  part = part + __uint_as_float(xor_lane<2>(__float_as_uint(part)));
+  part = part + __uint_as_float(xor_lane<1>(__float_as_uint(part)));
   const float inv = 1.0f / sqrtf(part * (1.0f / 128.0f) + eps);
   float zz[8], sz[8], wf[8], n[8];
   unpack8(zv, zz);
