@@ -7,6 +7,7 @@ import torch
 
 from oracle import mxfp4_oracle as O
 from oracle import producers_oracle as P
+from tests import _orders as ORD
 from tests._check import bf16_dev, host_u16, host_u8, to_dev
 from vllm_sly_radiance_amd import _native, synthetic
 from vllm_sly_radiance_amd import radiance_fused_norm as FN
@@ -87,6 +88,20 @@ def test_add_rms_quant_special_rows(gpu_lib):
     oq, os_, orr = P.add_rms_quant(y, res, w, 1e-6)
     assert np.array_equal(r, orr)
     assert_same_qs(q, s, oq, os_, "add_rms special rows")
+
+
+@pytest.mark.parametrize("M", [1, 130])
+def test_add_rms_quant_sum_order_pinned(gpu_lib, M):
+    """Rows on which each plausible other order of the sum of squares (sequential, the butterfly
+    reversed, the waves or a thread's groups reversed) gives another row scale than the fixed
+    order (tests/_orders.py), run as M copies of each row: the kernel matches the oracle."""
+    for y, w, tells in ORD.add_rms_cases():
+        yy = np.repeat(y, M, axis=0)
+        res = np.zeros_like(yy)
+        q, s, r = gpu_add_rms(yy, res, w, 1e-6)
+        oq, os_, orr = P.add_rms_quant(yy, res, w, 1e-6)
+        assert np.array_equal(r, orr)
+        assert_same_qs(q, s, oq, os_, f"add_rms M={M}, a row telling the fixed order from {tells}")
 
 
 def test_add_rms_quant_sampled_rows_at_prefill_size(gpu_lib):
@@ -201,6 +216,18 @@ def test_gdn_norm_quant_bit_exact(gpu_lib, M, heads, extra):
     q, s = gpu_gdn(x, zw, extra, w, 1e-6)
     oq, os_ = P.gdn_norm_quant(x, zw[:, extra:extra + N], w, 1e-6)
     assert_same_qs(q, s, oq, os_, f"gdn M={M} heads={heads} z offset {extra}")
+
+
+@pytest.mark.parametrize("M", [1, 130])
+def test_gdn_norm_quant_head_sum_order_pinned(gpu_lib, M):
+    """Rows on which a sequential head sum or the 16-lane butterfly reversed gives another row
+    scale than the fixed order (tests/_orders.py), as M copies (the 1024- and the 256-thread
+    rows): the kernel matches the oracle."""
+    for x, z, w, tells in ORD.gdn_cases():
+        xx, zz = np.repeat(x, M, axis=0), np.repeat(z, M, axis=0)
+        q, s = gpu_gdn(xx, zz, 0, w, 1e-6)
+        oq, os_ = P.gdn_norm_quant(xx, zz, w, 1e-6)
+        assert_same_qs(q, s, oq, os_, f"gdn M={M}, a row telling the fixed order from {tells}")
 
 
 def _silu_groups(bits):
