@@ -124,3 +124,46 @@ def test_health_report_once_per_shape_and_capped(diag, capsys, monkeypatch):
     monkeypatch.setattr(D, "CHECK_X_MAX", 1)
     D.after_call({}, q, s, wq, sq, out[:2], N, K)               # a new shape past the cap
     assert capsys.readouterr().err == ""
+
+
+def test_debug_reports_each_shape_once(diag, capsys, monkeypatch):
+    """RADIANCE_MXFP4_DEBUG: one exact comparison per (N, K, M), ok or wrong, up to DEBUG_MAX
+    shapes, not above M = 128 and not under capture; no tally is kept."""
+    monkeypatch.setattr(D, "CHECK_ALL", None)
+    monkeypatch.setattr(D, "MHIST", False)
+    monkeypatch.setattr(D, "DEBUG", True)
+    q, s, wq, sq, out, N, K = _case()
+    stats = {}
+    D.after_call(stats, q, s, wq, sq, out, N, K)
+    err = capsys.readouterr().err
+    assert "[radiance.mxfp4.exact] N=32 K=512 M=4 rel_vs_fp32=" in err and err.rstrip().endswith("ok")
+    D.after_call(stats, q, s, wq, sq, out, N, K)
+    assert capsys.readouterr().err == ""                      # once per shape
+    q2, s2, _, _, out2, _, _ = _case(M=2)
+    bad = out2.clone()
+    bad[:, :16] = -bad[:, :16]
+    D.after_call(stats, q2, s2, wq, sq, bad, N, K)
+    assert "M=2" in (e := capsys.readouterr().err) and "**WRONG**" in e
+    assert stats == {}
+    monkeypatch.setattr(D, "DEBUG_MAX", 2)                    # two shapes seen: no more
+    q3, s3, _, _, out3, _, _ = _case(M=3)
+    D.after_call(stats, q3, s3, wq, sq, out3, N, K)
+    assert capsys.readouterr().err == ""
+
+
+def test_padded_and_cloned_output(monkeypatch):
+    """RADIANCE_MXFP4_PADOUT=n: the output is an [M, N] view n elements into a slab with n spare
+    elements on each side. RADIANCE_MXFP4_CLONE=1: the op returns a copy."""
+    monkeypatch.setattr(D, "PAD_OUT", 0)
+    o = D.new_out(3, 40, "cpu")
+    assert o.shape == (3, 40) and o.dtype == torch.bfloat16 and o.untyped_storage().nbytes() == 240
+    monkeypatch.setattr(D, "PAD_OUT", 5)
+    o = D.new_out(3, 40, "cpu")
+    assert o.shape == (3, 40) and o.is_contiguous() and o.storage_offset() == 5
+    assert o.untyped_storage().nbytes() == 2 * (120 + 10)
+    monkeypatch.setattr(D, "CLONE_OUT", False)
+    assert D.returned(o) is o
+    monkeypatch.setattr(D, "CLONE_OUT", True)
+    o.fill_(1.5)
+    c = D.returned(o)
+    assert c.data_ptr() != o.data_ptr() and torch.equal(c, o)

@@ -241,3 +241,45 @@ def test_sanitize_and_sync_switches(kernel, monkeypatch):
             monkeypatch.setattr(D, "SYNC", mode)
             assert torch.equal(kernel.apply_weights(layer, x), kernel.apply_weights(layer, x))
         monkeypatch.setattr(D, "SYNC", "0")
+
+
+def test_padded_cloned_output_and_debug_switches(kernel, monkeypatch, capsys):
+    """RADIANCE_MXFP4_PADOUT (an output 3 elements into a padded slab, so every kernel's epilogue
+    meets a pointer that is only 2-byte aligned), RADIANCE_MXFP4_CLONE and RADIANCE_MXFP4_DEBUG:
+    the same bits as the plain output on every path the ops take (one launch, stream, tile K split,
+    band kernel, mid tile, the pre-quantized op, SiLU-mul + down in one launch and in two), and one
+    exact-check line per shape, all ok."""
+    from vllm_sly_radiance_amd import diagnostics as D
+    monkeypatch.setattr(D, "_seen", set())
+    cases = [((5120, 8704), (1, 8, 40, 600)), ((17408, 5120), (40,))]
+    for (N, K), Ms in cases:
+        w, ws = synthetic.weights(N, K, seed=47)
+        layer = Layer(w, ws)
+        kernel.process_weights_after_loading(layer)
+        for M in Ms:
+            x = bf16_dev(synthetic.activations(M, K, seed=M + 3))
+            qx = R.quant_per_token(x)
+            gu = bf16_dev(synthetic.activations(M, 2 * K, seed=M + 4)) if N == 5120 and M < 8 else None
+            print(f"[op] padded output N={N} K={K} M={M}", flush=True)
+
+            def run():
+                ys = [kernel.apply_weights(layer, x), kernel.apply_weights(layer, qx)]
+                if gu is not None:
+                    ys.append(torch.ops.radiance.silu_mul_mxfp4_linear(
+                        gu, layer.weight, layer.weight_scale, layer.radiance_wref))
+                torch.cuda.synchronize()
+                return ys
+            monkeypatch.setattr(D, "PAD_OUT", 0)
+            monkeypatch.setattr(D, "CLONE_OUT", False)
+            monkeypatch.setattr(D, "DEBUG", False)
+            plain = run()
+            monkeypatch.setattr(D, "PAD_OUT", 3)
+            monkeypatch.setattr(D, "CLONE_OUT", True)
+            monkeypatch.setattr(D, "DEBUG", M <= 128)
+            padded = run()
+            for a, b in zip(plain, padded):
+                assert b.shape == a.shape and torch.equal(a.view(torch.int16), b.view(torch.int16))
+    monkeypatch.setattr(D, "DEBUG", False)
+    err = capsys.readouterr().err
+    lines = [ln for ln in err.splitlines() if ln.startswith("[radiance.mxfp4.exact]")]
+    assert len(lines) == 4 and all(ln.endswith(" ok") for ln in lines), err

@@ -19,6 +19,13 @@ The reference's op body carries these, and they keep its switch names:
   RADIANCE_MXFP4_SANITIZE=1          zero NaN and inf in the bf16 activations before they are
                                      quantized (a NaN otherwise makes its row's scale, and so the
                                      whole output row, NaN; :450-466, :715-716)
+  RADIANCE_MXFP4_DEBUG=1             each distinct (N, K, M) with M <= 128, the first 40, is compared
+                                     once with the same exact fp32 product and reported ok or
+                                     wrong (:557-577, :804-805)
+  RADIANCE_MXFP4_CLONE=1             the op returns a copy of its output buffer (:433-436, :816)
+  RADIANCE_MXFP4_PADOUT=n            the output is allocated inside a slab with n spare bf16
+                                     elements before and after it, so nothing live is adjacent
+                                     (:437-442, :733-736)
   report_stats()                     the one-shot tally of layers on the HIP kernel and layers
                                      refused at load (:941-957). It is called from op bodies only:
                                      they are opaque to dynamo, so a stderr write there cannot
@@ -55,7 +62,11 @@ MHIST = os.environ.get("RADIANCE_MXFP4_MHIST", "0") == "1"
 CHECK_X = os.environ.get("RADIANCE_MXFP4_CHECKX", "0") == "1"
 SYNC = os.environ.get("RADIANCE_MXFP4_SYNC", "0")
 SANITIZE_X = os.environ.get("RADIANCE_MXFP4_SANITIZE", "0") == "1"
+DEBUG = os.environ.get("RADIANCE_MXFP4_DEBUG", "0") == "1"
+CLONE_OUT = os.environ.get("RADIANCE_MXFP4_CLONE", "0") == "1"
+PAD_OUT = int(os.environ.get("RADIANCE_MXFP4_PADOUT", "0"))
 CHECK_X_MAX = 60
+DEBUG_MAX = 40
 WRONG_REL = 0.02
 
 KERNEL_NAMES = {_native.KERNEL_SKINNY: "skinny", _native.KERNEL_TILE: "tile",
@@ -114,7 +125,21 @@ def report_stats(stats: dict) -> None:
 
 
 def enabled() -> bool:
-    return MHIST or CHECK_ALL is not None or CHECK_X or SYNC in ("1", "2")
+    return MHIST or CHECK_ALL is not None or CHECK_X or DEBUG or SYNC in ("1", "2")
+
+
+def new_out(M: int, N: int, device) -> torch.Tensor:
+    """The op's bf16 [M, N] output: torch.empty, or with RADIANCE_MXFP4_PADOUT=n a view into a
+    slab holding n spare elements on each side (the kernels store through any 2-byte alignment)."""
+    if PAD_OUT <= 0:
+        return torch.empty((M, N), dtype=torch.bfloat16, device=device)
+    slab = torch.empty(M * N + 2 * PAD_OUT, dtype=torch.bfloat16, device=device)
+    return slab[PAD_OUT:PAD_OUT + M * N].view(M, N)
+
+
+def returned(out: torch.Tensor) -> torch.Tensor:
+    """What the op hands back: its output, or a copy of it with RADIANCE_MXFP4_CLONE=1."""
+    return out.clone() if CLONE_OUT else out
 
 
 def sanitize(x: torch.Tensor) -> torch.Tensor:
@@ -160,13 +185,25 @@ def after_call(stats: dict, x_fp8, x_scale, wq, sq, out, N: int, K: int, x=None)
         sys.stderr.write(f"[radiance.mxfp4.mhist] N={N} K={K} M={M} "
                          f"plan={KERNEL_NAMES.get(k, k)} variant={v} split_k={s}\n")
         sys.stderr.flush()
-    if CHECK_ALL is None or (N, K) not in CHECK_ALL or M == 0 or M > CHECK_MAX_M:
-        return
-    if capturing:
+    debug = (DEBUG and not capturing and 0 < M <= 128 and ("d", N, K, M) not in _seen
+             and sum(1 for k in _seen if k[0] == "d") < DEBUG_MAX)
+    check = not (CHECK_ALL is None or (N, K) not in CHECK_ALL or M == 0 or M > CHECK_MAX_M
+                 or capturing)
+    if not (debug or check):
         return
     if callable(x_fp8):
         x_fp8, x_scale = x_fp8()
     ref = exact_linear(x_fp8, x_scale, wq, sq, N, K)
+    if debug:
+        _seen.add(("d", N, K, M))
+        rel = ((out.float() - ref).norm() / ref.norm().clamp_min(1e-9)).item()
+        sys.stderr.write(f"[radiance.mxfp4.exact] N={N} K={K} M={M} rel_vs_fp32={rel:.5f} "
+                         f"|ours|={out.float().abs().mean().item():.5f} "
+                         f"|ref|={ref.abs().mean().item():.5f} "
+                         f"{'ok' if rel <= WRONG_REL else '**WRONG**'}\n")
+        sys.stderr.flush()
+    if not check:
+        return
     rel = ((out.float() - ref).norm() / ref.norm().clamp_min(1e-9)).item()
     stats["checked"] = stats.get("checked", 0) + 1
     if not rel <= WRONG_REL:                                 # NaN counts as wrong

@@ -214,7 +214,7 @@ def mxfp4_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tens
                            f"{x.dtype} stride {x.stride()}")
     M = x.shape[0]
     x = _diag.sanitize(x)
-    out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    out = _diag.new_out(M, N, x.device)
     q = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=x.device)
     s = torch.empty((M,), dtype=torch.float32, device=x.device)
     _native.linear(x.data_ptr(), x.stride(0), q.data_ptr(), s.data_ptr(), weight.data_ptr(),
@@ -223,7 +223,7 @@ def mxfp4_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tens
         # the one-launch form keeps q in LDS: the check quantizes again (the same bits)
         _diag.after_call(STATS, lambda: quant_per_token(x), None, weight, weight_scale, out, N, K,
                          x=x)
-    return out
+    return _diag.returned(out)
 
 
 @mxfp4_linear.register_fake
@@ -253,14 +253,14 @@ def mxfp4_linear_pq(x_fp8: torch.Tensor, x_scale: torch.Tensor, weight: torch.Te
         raise RuntimeError(f"[radiance.mxfp4] x_scale must be {M} contiguous fp32 values")
     if allow_tiled and A_TILED_MIN_M and a_tiled_take(x_fp8, M, K):
         STATS["calls_tiled"] += 1
-        out = torch.empty((M, N), dtype=torch.bfloat16, device=x_fp8.device)
+        out = _diag.new_out(M, N, x_fp8.device)
         _native.gemm_at(x_fp8.data_ptr(), xs.data_ptr(), weight.data_ptr(),
                         weight_scale.data_ptr(), out.data_ptr(), M, N, K, _stream())
-        return out                  # fragment-tiled q: the row-major check does not apply
-    out = gemm(x_fp8, xs, weight, weight_scale, N, K)
+        return _diag.returned(out)  # fragment-tiled q: the row-major check does not apply
+    out = gemm(x_fp8, xs, weight, weight_scale, N, K, out=_diag.new_out(M, N, x_fp8.device))
     if _diag.enabled():
         _diag.after_call(STATS, x_fp8, xs, weight, weight_scale, out, N, K)
-    return out
+    return _diag.returned(out)
 
 
 @mxfp4_linear_pq.register_fake
@@ -287,7 +287,7 @@ def silu_mul_mxfp4_linear(gate_up: torch.Tensor, weight: torch.Tensor, weight_sc
         raise RuntimeError(f"[radiance.mxfp4] gate_up must be bf16, got {gate_up.dtype}")
     gate_up = gate_up.contiguous()
     M = gate_up.shape[0]
-    out = torch.empty((M, N), dtype=torch.bfloat16, device=gate_up.device)
+    out = _diag.new_out(M, N, gate_up.device)
     q = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=gate_up.device)
     s = torch.empty((M,), dtype=torch.float32, device=gate_up.device)
     if M:
@@ -302,7 +302,7 @@ def silu_mul_mxfp4_linear(gate_up: torch.Tensor, weight: torch.Tensor, weight_sc
                                    _stream())
             return q2, s2
         _diag.after_call(STATS, _quantized, None, weight, weight_scale, out, N, K, x=gate_up)
-    return out
+    return _diag.returned(out)
 
 
 @silu_mul_mxfp4_linear.register_fake
