@@ -31,6 +31,9 @@ constexpr float kMinScale = 1.0f / (448.0f * 512.0f);
 //  * lane ^ 8, 4, 2, 1: DPP moves within rows of 16 lanes: quad_perm [1,0,3,2] (^1),
 //    [2,3,0,1] (^2); half-row mirror then quad_perm [3,2,1,0] (^4); row mirror then half-row
 //    mirror (^8).
+// Every lane of the wave must be active where these run (a read from an inactive lane returns 0
+// or a stale value): callers pass a neutral value from lanes that hold nothing instead of
+// branching around the call.
 template <int Ctrl>
 __device__ __forceinline__ uint32_t dpp(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, Ctrl, 0xF, 0xF, false);
