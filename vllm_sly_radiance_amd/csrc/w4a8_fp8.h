@@ -1,8 +1,9 @@
 // Per-token e4m3 quantization of bf16 rows held in registers, shared by the quantizer and the
 // fused producers. Semantics: s = max(amax(|x|) * fl32(1/448), 1/(448*512)) (a NaN in the row
 // propagates to s); q = e4m3_rne(clamp(x / s, -448, 448)) with the IEEE fp32 quotient x / s. One
-// 256-thread workgroup (4 wave64) per row; the amax runs on the bf16 bit patterns (|x| bits =
-// x & 0x7FFF), which is exact, orders like the magnitudes and ranks NaN above inf. Codes come
+// workgroup per row (of 256 threads; of 512 or 1024 where few rows leave each row's chain as the
+// latency); the amax runs on the bf16 bit patterns (|x| bits = x & 0x7FFF), which is exact,
+// orders like the magnitudes and ranks NaN above inf. Codes come
 // from the hardware e4m3 converter (v_cvt_pk_fp8_f32, round to nearest even) on clamped inputs;
 // rows whose scale is not finite take a per-element path that maps NaN quotients to 0x7F.
 //
