@@ -120,7 +120,8 @@ def report_stats(stats: dict) -> None:
     _reported[0] = True
     n = stats["fast"] + stats["refused"]
     sys.stderr.write(f"[radiance.mxfp4] linear layers: {stats['fast']}/{n} on the gfx950 W4A8 "
-                     f"kernels, {stats['refused']} refused at load (another kernel serves them)\n")
+                     f"kernels, {stats['refused']} refused at load (not a checkpoint layout "
+                     f"they serve)\n")
     sys.stderr.flush()
 
 
