@@ -4,8 +4,9 @@ the CPU (tests/fp_identities.c, built here with gcc):
 * the per-token quantizer divides by Markstein's correction (y = 1/s once per row, then
   q0 = x*y, r = fma(-s, q0, x), q = fma(r, y, q0) with x's sign) instead of a full IEEE division:
   over every finite row scale and every bf16 x the row can hold, the e4m3 code is the same;
-* exp_f32 in the fused producers is branch-free (a clamp, then NaN put back): equal to the
-  branching form, which the oracle restates, for every fp32 input.
+* exp_f32 in the fused producers is branch-free (a clamp): equal to the branching form, which the
+  oracle restates, for every non-NaN fp32 input; for a NaN, silu's dividing path (every group
+  holding a NaN takes it) gives the same bits with either form.
 A planted mistake (no sign fix, a clamp that is too narrow) is caught by the same checks."""
 import os
 import shutil

@@ -19,14 +19,18 @@ constexpr float kExpHi = 0x1.62e43p+6f;           // 88.7228394: above, e^y over
 constexpr float kExpLo = -0x1.9fe368p+6f;         // fl32(-150 ln 2): below, e^y rounds to +0
 static_assert(kExpHi < 89.0f && kExpLo > -104.0f, "exp_f32's clamp must bracket its range");
 
-// e^y for y in [kExpLo, kExpHi] as described above; NaN stays NaN, above kExpHi it is +inf and
-// below kExpLo +0. Branch-free: y is first clamped to [-104, 89], where the same steps already
-// give +inf at and above kExpHi (n = 128 and e^r > 1) and +0 below kExpLo (p * 2^-150 < 2^-150
-// rounds to zero); a NaN is put back at the end. Over all 2^32 inputs this equals the branching
-// form bit for bit (checked on the CPU with the same operations).
-__device__ __forceinline__ float exp_f32(float y_in) {
+// e^y for y in [kExpLo, kExpHi] as described above; above kExpHi it is +inf and below kExpLo +0.
+// Branch-free: y is first clamped to [-104, 89], where the same steps already give +inf at and
+// above kExpHi (n = 128 and e^r > 1) and +0 below kExpLo (p * 2^-150 < 2^-150 rounds to zero).
+// Over all non-NaN inputs this equals the branching form bit for bit (checked on the CPU with the
+// same operations). A NaN input gives a finite value (the clamp returns a bound): silu8, the only
+// caller, sends every group holding a NaN down its dividing path, where x / d is x's NaN for any
+// d, as the exp that kept the NaN gave.
+__device__ __forceinline__ float exp_f32(float y) {
 #pragma clang fp contract(off)
-  const float y = fminf(fmaxf(y_in, -104.0f), 89.0f);
+  // the clamp as one v_med3_f32: fminf(fmaxf()) would first canonicalize y, one more operation
+  // per element; for every non-NaN y both are the same clamp
+  y = __builtin_amdgcn_fmed3f(y, -104.0f, 89.0f);
   const float n = rintf(y * kLog2e);
   const float r = __builtin_fmaf(-n, kLn2Lo, __builtin_fmaf(-n, kLn2Hi, y));
   float p = 0x1.a01a02p-13f;                      // 1/k!, k = 7 .. 2, rounded to fp32
@@ -37,8 +41,7 @@ __device__ __forceinline__ float exp_f32(float y_in) {
   p = __builtin_fmaf(p, r, 0.5f);
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
-  const float e = ldexpf(p, (int)n);
-  return y_in != y_in ? y_in : e;
+  return ldexpf(p, (int)n);
 }
 
 // silu of 8 values, x / (1 + exp_f32(-x)) with the IEEE quotient. Where every value of the group
