@@ -116,6 +116,13 @@ __device__ __forceinline__ float clamp448(float v) {
   return v < -448.0f ? -448.0f : v;
 }
 
+// clamp448 for a quotient that cannot be NaN: one v_med3_f32 instead of two compare-and-selects.
+// With a finite row scale every element of the row is finite (a NaN or inf would have made the
+// row's amax, and so its scale, non-finite), and so is every quotient.
+__device__ __forceinline__ float clamp448_finite(float v) {
+  return __builtin_amdgcn_fmed3f(v, -448.0f, 448.0f);
+}
+
 __device__ __forceinline__ float lo_bf16(uint32_t d) { return __uint_as_float(d << 16); }
 __device__ __forceinline__ float hi_bf16(uint32_t d) { return __uint_as_float(d & 0xFFFF0000u); }
 
@@ -142,8 +149,10 @@ __device__ __forceinline__ float div_rcp(float x, float s, float y) {
 }
 
 __device__ __forceinline__ uint32_t quant_dword(uint32_t d0, uint32_t d1, float s, float y) {
-  const float a = clamp448(div_rcp(lo_bf16(d0), s, y)), b = clamp448(div_rcp(hi_bf16(d0), s, y));
-  const float c = clamp448(div_rcp(lo_bf16(d1), s, y)), d = clamp448(div_rcp(hi_bf16(d1), s, y));
+  const float a = clamp448_finite(div_rcp(lo_bf16(d0), s, y));
+  const float b = clamp448_finite(div_rcp(hi_bf16(d0), s, y));
+  const float c = clamp448_finite(div_rcp(lo_bf16(d1), s, y));
+  const float d = clamp448_finite(div_rcp(hi_bf16(d1), s, y));
   return pack4(a, b, c, d);
 }
 
