@@ -3,7 +3,7 @@
 //
 //   markstein  For every finite per-token scale s = max(fl32(amax * fl32(1/448)), 1/(448*512)),
 //              amax any finite bf16 magnitude, and every bf16 x with |x| <= amax (both signs):
-//              copysign(fma(fma(-s, q0, x), y, q0), x) with y = fl32(1/s), q0 = fl32(x*y) equals
+//              fma(-fma(s, q0, -x), y, q0) with y = fl32(1/s), q0 = fl32(x*y) equals
 //              the IEEE quotient fl32(x/s), or both quotients are below 2^-12 in magnitude with
 //              the same sign (where e4m3 rounds both to the same signed zero).
 //   exp        The branch-free exp_f32 (a clamp to [-104, 89]) equals the branching form
@@ -36,7 +36,7 @@ static int markstein(void) {
         const float x = f32((xb << 16) | (neg ? 0x80000000u : 0u));
         const float q = x / s;
         const float q0 = x * y;
-        const float q1 = copysignf(fmaf(fmaf(-s, q0, x), y, q0), x);
+        const float q1 = fmaf(-fmaf(s, q0, -x), y, q0);
         ++total;
         if (bits(q1) == bits(q)) continue;
         if (fabsf(q) < 0x1p-12f && fabsf(q1) < 0x1p-12f && signbit(q) == signbit(q1)) continue;

@@ -2,12 +2,14 @@
 the CPU (tests/fp_identities.c, built here with gcc):
 
 * the per-token quantizer divides by Markstein's correction (y = 1/s once per row, then
-  q0 = x*y, r = fma(-s, q0, x), q = fma(r, y, q0) with x's sign) instead of a full IEEE division:
-  over every finite row scale and every bf16 x the row can hold, the e4m3 code is the same;
+  q0 = x*y, r = fma(s, q0, -x), q = fma(-r, y, q0)) instead of a full IEEE division: over every
+  finite row scale and every bf16 x the row can hold, the e4m3 code is the same (x = -0 included:
+  the residual formed the other way round, fma(x - s q0, y, q0), gives +0 there);
 * exp_f32 in the fused producers is branch-free (a clamp): equal to the branching form, which the
   oracle restates, for every non-NaN fp32 input; for a NaN, silu's dividing path (every group
   holding a NaN takes it) gives the same bits with either form.
-A planted mistake (no sign fix, a clamp that is too narrow) is caught by the same checks."""
+A planted mistake (the residual the other way round, a clamp that is too narrow) is caught by the
+same checks."""
 import os
 import shutil
 import subprocess
@@ -51,7 +53,7 @@ def test_branch_free_exp_equals_the_branching_form(checker):
 def test_planted_mistakes_are_caught(checker, tmp_path):
     """The same checks on copies of the identities with a known mistake must fail."""
     src = open(os.path.join(HERE, "fp_identities.c")).read()
-    bad = (src.replace("copysignf(fmaf(fmaf(-s, q0, x), y, q0), x)", "fmaf(fmaf(-s, q0, x), y, q0)")
+    bad = (src.replace("fmaf(-fmaf(s, q0, -x), y, q0)", "fmaf(fmaf(-s, q0, x), y, q0)")
               .replace("fminf(fmaxf(y_in, -104.0f), 89.0f)", "fminf(fmaxf(y_in, -90.0f), 89.0f)"))
     assert bad != src
     p = tmp_path / "planted.c"

@@ -9,8 +9,10 @@
 //
 // Rows with a finite scale divide by Markstein's correction (P. Markstein, "Computation of
 // elementary functions on the IBM RISC System/6000 processor", IBM J. Res. Dev. 34(1), 1990):
-// y = 1/s once per row (IEEE division), then per element q0 = x*y, r = fma(-s, q0, x) and
-// q = fma(r, y, q0) with the sign of x: three operations instead of a full division. Over every
+// y = 1/s once per row (IEEE division), then per element q0 = x*y, the residual formed negated,
+// r = fma(s, q0, -x), and q = fma(-r, y, q0): three operations instead of a full division (the
+// same value as q0 + (x - s q0) y, round to nearest being symmetric, and -0 for x = -0 with no
+// sign fix, where fma(x - s q0, y, q0) would give +0). Over every
 // finite row amax and every bf16 x with |x| <= amax (both signs, 1.07e9 pairs) the result equals
 // the IEEE quotient except for quotients below 2^-12, where both round to the same signed zero in
 // e4m3 (tests/fp_identities.c, run by tests/test_fp_identities_cpu.py, makes that exhaustive
@@ -144,8 +146,8 @@ __device__ __forceinline__ uint32_t pack4_any(float a, float b, float c, float d
 // x / s for a finite s > 0 and y = 1/s (Markstein's correction; see the file header)
 __device__ __forceinline__ float div_rcp(float x, float s, float y) {
   const float q0 = x * y;
-  const float r = __builtin_fmaf(-s, q0, x);
-  return __builtin_copysignf(__builtin_fmaf(r, y, q0), x);
+  const float r = __builtin_fmaf(s, q0, -x);
+  return __builtin_fmaf(-r, y, q0);
 }
 
 __device__ __forceinline__ uint32_t quant_dword(uint32_t d0, uint32_t d1, float s, float y) {

@@ -47,8 +47,9 @@ __device__ __forceinline__ float exp_f32(float y) {
 // silu of 8 values, x / (1 + exp_f32(-x)) with the IEEE quotient. Where every value of the group
 // has |x| <= 44 (1 <= d <= 2^64: the reciprocal is a normal number, nothing is infinite or NaN)
 // the quotient comes from the hardware reciprocal and one Markstein correction, y = rcp(d),
-// q = x y, r = fma(-d, q, x), q + r y, with x's sign (a -0 quotient would otherwise come out +0):
-// five operations instead of the division's ten. Any other group (rare) divides. Markstein's
+// q = x y, the residual formed negated, r = fma(d, q, -x), then fma(-r, y, q): four operations
+// instead of the division's ten (the same value as q + (x - d q) y, and -0 for x = -0 with no
+// sign fix). Any other group (rare) divides. Markstein's
 // correction is proven correctly rounded only from a correctly rounded reciprocal, and v_rcp_f32
 // is within 1 ulp, so the unrounded quotient is checked on the GPU instead, against the IEEE
 // quotient for every bf16 x on both paths (w4a8_silu_f32; the SiLU-and-mul and gated-norm tests
@@ -62,8 +63,8 @@ __device__ __forceinline__ void silu8(const float (&x)[8], float (&s)[8]) {
     d[j] = 1.0f + exp_f32(-x[j]);
     const float y = __builtin_amdgcn_rcpf(d[j]);
     const float q = x[j] * y;
-    const float r = __builtin_fmaf(-d[j], q, x[j]);
-    s[j] = __builtin_copysignf(__builtin_fmaf(r, y, q), x[j]);
+    const float r = __builtin_fmaf(d[j], q, -x[j]);
+    s[j] = __builtin_fmaf(-r, y, q);
     wide |= !(__builtin_fabsf(x[j]) <= 44.0f);
   }
   if (__builtin_expect(wide, 0)) {
