@@ -74,15 +74,20 @@ __device__ __forceinline__ v8i load_x_frag(const uint8_t* row, int k0, int g, in
 
 // Two bf16 of the hardware convert (v_cvt_pk_bf16_f32: round to nearest even, the same bits as
 // f32_to_bf16 for every non-NaN input), NaNs put back to f32_to_bf16's canonical 0x7FC0 | sign.
+// The convert quiets a NaN, so a NaN half has a magnitude of 0x7FC0 or more, and every other
+// half (inf included) at most 0x7F80: the packed 16-bit minimum of the magnitudes with 0x7FC0,
+// under the sign bits, makes exactly the canonical NaNs and leaves everything else alone. Four
+// operations for the pair, no compares.
 typedef __bf16 w4a8_bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float w4a8_f32x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned short w4a8_u16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t bf16x2_rne(float lo, float hi) {
   const uint32_t r =
       __builtin_bit_cast(uint32_t, __builtin_convertvector(w4a8_f32x2_t{lo, hi}, w4a8_bf16x2_t));
-  const uint32_t l = lo != lo ? (((__float_as_uint(lo) >> 16) & 0x8000u) | 0x7FC0u) : r & 0xFFFFu;
-  const uint32_t h = hi != hi ? ((__float_as_uint(hi) & 0x80000000u) | 0x7FC00000u)
-                              : r & 0xFFFF0000u;
-  return l | h;
+  const w4a8_u16x2_t mag = __builtin_bit_cast(w4a8_u16x2_t, r & 0x7FFF7FFFu);
+  const uint32_t m = __builtin_bit_cast(
+      uint32_t, __builtin_elementwise_min(mag, w4a8_u16x2_t{0x7FC0, 0x7FC0}));
+  return (r & 0x80008000u) | m;
 }
 
 // Four consecutive outputs of one token, scaled and rounded, as one 8-byte store when aligned.
