@@ -673,3 +673,36 @@ def test_gemm_random_shapes_planned(gpu_lib, M, N, K):
     print(f"[random] M={M} N={N} K={K} plan {plan}", flush=True)
     out = gpu_gemm(q, s, wq, sq, N, K)
     assert_gemm_close(out, q, s, w, ws, f"random M={M} N={N} K={K} plan {plan}")
+
+
+NAN_SCALES = [0x7FC00000, 0xFFC00000, 0x7FC12345, 0xFFFFFFFF, 0x7F800001]
+
+
+@pytest.mark.parametrize("M,N,K,kernel,variant,split,path", [
+    (8, 512, 1024, 0, -1, 0, "stream"),
+    (40, 17408, 5120, 0, -1, 0, "band"),
+    (256, 1024, 1024, TILE, 2, 1, "tile, full tiles (staged stores)"),
+    (200, 1000, 1024, TILE, 2, 1, "tile, edge tiles (direct stores)"),
+    (24, 5120, 8704, 0, -1, 0, "tile K split + reduce"),
+])
+def test_nan_token_scales_give_canonical_nan_rows(gpu_lib, M, N, K, kernel, variant, split, path):
+    """A NaN token scale (any payload, either sign, quiet or signalling) makes its whole output row
+    the canonical bf16 NaN 0x7FC0 | sign on every epilogue (the hardware convert plus the packed
+    minimum, or the software rounding); the other rows stay finite."""
+    w, ws = synthetic.weights(N, K, seed=M + 1)
+    wq, sq = gpu_repack(w, ws)
+    q, s = O.quant_per_token(synthetic.activations(M, K, seed=M + 2))
+    s = s.astype(np.float32).copy()
+    rows = [(3 * i + 1) % M for i in range(len(NAN_SCALES))]
+    for r, bits in zip(rows, NAN_SCALES):
+        s.view(np.uint32)[r] = bits
+    print(f"[kernels] NaN token scales, {path}, M={M} N={N} K={K}", flush=True)
+    c = gpu_gemm(q, s, wq, sq, N, K, kernel, variant, split)
+    if kernel == 0:
+        assert _native.plan(M, N, K)[0] == {"stream": STREAM, "band": _native.KERNEL_BAND}.get(
+            path, TILE), _native.plan(M, N, K)
+    for r, bits in zip(rows, NAN_SCALES):
+        want = 0x7FC0 | ((bits >> 16) & 0x8000)
+        assert (c[r] == want).all(), (path, r, hex(bits), np.unique(c[r])[:4])
+    others = np.setdiff1d(np.arange(M), rows)
+    assert not np.isnan(O.bf16_to_f32(c[others])).any()
