@@ -7,6 +7,7 @@ import torch
 from oracle import mxfp4_oracle as O
 from tests._check import assert_gemm_close, bf16_dev, host_u16, host_u8, to_dev
 from vllm_sly_radiance_amd import _native, radiance_mxfp4 as R
+from vllm_sly_radiance_amd import radiance_fused_norm  # noqa: F401  (registers radiance::*_quant)
 from vllm_sly_radiance_amd import synthetic
 
 pytestmark = pytest.mark.gpu
@@ -64,6 +65,34 @@ def test_leading_dims_are_flattened(kernel):
     y2 = kernel.apply_weights(layer, bf16_dev(x))
     y3 = kernel.apply_weights(layer, bf16_dev(x).view(2, 3, K))
     assert tuple(y3.shape) == (2, 3, N) and torch.equal(y3.reshape(6, N), y2)
+
+
+def test_zero_tokens(kernel):
+    """An empty batch (vLLM's dummy and padded runs can hand one over): every entry returns
+    empty outputs of the right shapes and launches nothing."""
+    N, K = 5120, 5120
+    w, ws = synthetic.weights(N, K, seed=11)
+    layer = Layer(w, ws)
+    kernel.process_weights_after_loading(layer)
+    x = torch.zeros(0, K, device="cuda", dtype=torch.bfloat16)
+    y = kernel.apply_weights(layer, x)
+    assert y.dtype == torch.bfloat16 and tuple(y.shape) == (0, N)
+    q, s = R.quant_per_token(x)
+    assert tuple(q.shape) == (0, K) and tuple(s.shape) == (0,)
+    assert tuple(kernel.apply_weights(layer, (q, s)).shape) == (0, N)
+    assert tuple(kernel.apply_weights(layer, x.view(0, 1, K)).shape) == (0, 1, N)
+    e = torch.zeros(0, K, device="cuda", dtype=torch.bfloat16)
+    qa, sa, ra = torch.ops.radiance.add_rms_quant(e, e, torch.zeros(K, device="cuda",
+                                                                    dtype=torch.bfloat16), 1e-6)
+    assert tuple(qa.shape) == (0, K) and tuple(sa.shape) == (0,) and tuple(ra.shape) == (0, K)
+    qg, sg = torch.ops.radiance.gdn_norm_quant(e, e, torch.zeros(128, device="cuda",
+                                                                 dtype=torch.bfloat16), 1e-6)
+    assert tuple(qg.shape) == (0, K) and tuple(sg.shape) == (0,)
+    gu = torch.zeros(0, 2 * K, device="cuda", dtype=torch.bfloat16)
+    yd = torch.ops.radiance.silu_mul_mxfp4_linear(gu, layer.weight, layer.weight_scale,
+                                                  layer.radiance_wref)
+    assert tuple(yd.shape) == (0, N)
+    torch.cuda.synchronize()
 
 
 def test_op_refuses_mismatched_activation(kernel):
