@@ -484,7 +484,7 @@ def bench_read_probe(steps, warmup):
     traffic, the same rotation over 16 copies and the same timing (direct launches behind the
     graph warm-up), nothing but reads. First the fixed probe (the GEMM's launch shape), then the
     launch-shape sweep (READ_SWEEP, 256 launches each), whose fastest shape is the ceiling the
-    GEMM is held against."""
+    GEMM is held against; last the GEMM against its own load pattern (bench_gemm_loads)."""
     import torch
     nbytes = gemm_bytes(VERIFY["M"], VERIFY["N"], VERIFY["K"])
     g = ReadProbe(nbytes, COPIES)
@@ -506,6 +506,42 @@ def bench_read_probe(steps, warmup):
     best = min(shapes, key=lambda r: r["us"])
     res["sweep"] = shapes
     res["best"] = dict(best, frac=round(best["gbs"] / HBM_PEAK_GBS, 4))
+    del g
+    torch.cuda.empty_cache()
+    res["gemm_loads"] = bench_gemm_loads()
+    return res
+
+
+class StreamLoads:
+    """A Gemm's operands read by w4a8_stream_load_probe: the streaming GEMM's own loads (one of
+    the three load sets), without its math."""
+
+    def __init__(self, g, parts):
+        self.g, self.w, self.parts = g, g.w, parts
+
+    def launch(self, i, stream):
+        g = self.g
+        g._native.stream_load_probe(g.q.data_ptr(), g.s.data_ptr(), g.w[i].data_ptr(),
+                                    g.ws[i].data_ptr(), g.M, g.N, g.K, self.parts,
+                                    g.probe_out.data_ptr(), stream)
+
+
+def bench_gemm_loads(steps=256):
+    """What the verify GEMM's load pattern costs without its math: the GEMM and its loads alone
+    (weight granules; and scale dwords; and activation fragments with token scales, every load it
+    issues), each `steps` direct launches over the same 16 weight copies, µs per launch."""
+    import torch
+    from vllm_sly_radiance_amd import _native
+    M, N, K = VERIFY["M"], VERIFY["N"], VERIFY["K"]
+    g = Gemm(M, N, K, COPIES, seed=1)
+    g.probe_out = torch.zeros(1, dtype=torch.int32, device="cuda")
+    res = dict(steps=steps)
+    for key, obj in (("gemm_us", g), ("weights_us", StreamLoads(g, _native.STREAM_LOADS_WEIGHTS)),
+                     ("weights_scales_us", StreamLoads(g, _native.STREAM_LOADS_SCALES)),
+                     ("all_loads_us", StreamLoads(g, _native.STREAM_LOADS_ALL))):
+        sec, _, _, _ = graph_timed(obj, steps, 16, warm_seconds=0.2, direct=True)
+        res[key] = round(sec / steps * 1e6, 3)
+    print(f"[bench] verify GEMM against its own loads: {res}", file=sys.stderr, flush=True)
     del g
     torch.cuda.empty_cache()
     return res

@@ -306,6 +306,16 @@ int w4a8_read_probe_variant_info(int variant, int* waves, int* units, int* windo
 int w4a8_read_probe_shape(const void* buf, long bytes, int* out, int blocks, int variant,
                           void* stream);
 
+/* Diagnostic: the loads of the streaming GEMM that w4a8_gemm runs for (M, N, K) (M 1..8; the plan
+ * must be W4A8_KERNEL_STREAM), issued exactly as that kernel issues them (same grid, buffer
+ * resources, offsets, cache policies and order, all before any is used), without the MFMAs, the
+ * reduction and the stores. parts: 1 the weight granules, 3 and the scale dwords, 7 and the
+ * activation fragments with the token scales (every load of the GEMM). The operands are those of
+ * w4a8_gemm; out (one int) receives nothing unless the data xor to a fixed pattern. The caller
+ * times it, against the GEMM and the read probe. No counterpart in the reference. */
+int w4a8_stream_load_probe(const void* a, const float* a_scale, const void* wq, const void* sq,
+                           int M, int N, int K, int parts, int* out, void* stream);
+
 /* Diagnostic: `count` independent scaled MFMAs (16x16x128, fp4 e2m1 A x fp8 e4m3 B, the instruction
  * every GEMM here issues) on raw lane operands, one wave per tile: a [count][64][4] dwords (16 fp4
  * bytes per lane), b [count][64][8] dwords (32 fp8 bytes per lane), sa / sb [count][64] scale

@@ -371,6 +371,23 @@ def test_read_probe_shape_validates_before_launch(lib):
     assert b"w4a8_read_probe_shape" in lib.w4a8_last_error()
 
 
+def test_stream_load_probe_validates_before_launch(lib):
+    """The streaming GEMM's loads alone: only shapes the plan sends to the streaming kernel at
+    M <= 8, the three load sets, and the GEMM's operand checks."""
+    p = 4096
+    assert lib.w4a8_stream_load_probe(p, p, p, p, 0, 17408, 5120, 7, p, None) == 1
+    assert lib.w4a8_stream_load_probe(p, p, p, p, 9, 17408, 5120, 7, p, None) == 1
+    for parts in (0, 2, 4, 5, 8):
+        assert lib.w4a8_stream_load_probe(p, p, p, p, 8, 17408, 5120, parts, p, None) == 1
+    assert b"parts" in lib.w4a8_last_error()
+    assert lib.w4a8_stream_load_probe(p, p, p, p, 8, 17408, 5000, 7, p, None) == 1
+    assert lib.w4a8_stream_load_probe(None, p, p, p, 8, 17408, 5120, 7, p, None) == 1
+    assert lib.w4a8_stream_load_probe(p, p, p, p, 8, 17408, 5120, 7, None, None) == 1
+    assert lib.w4a8_stream_load_probe(p + 4, p, p, p, 8, 17408, 5120, 7, p, None) == 1
+    assert lib.w4a8_stream_load_probe(p, p, p, p, 8, 33, 640, 7, p, None) == 1   # skinny plan
+    assert b"not the streaming GEMM" in lib.w4a8_last_error()
+
+
 def test_workspace_bytes_covers_the_band_split_in_4_mib(lib):
     """The scratch the plugin registers, sized by the library's own plan: the skinny kernel's
     split-K partials for small-N shapes at M <= 16, SiLU-mul's split-row maxima, and the band's

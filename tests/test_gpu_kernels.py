@@ -647,6 +647,31 @@ def test_read_probe_reads_without_writing(gpu_lib, nbytes):
     assert out.cpu().tolist() == [0, 0]
 
 
+@pytest.mark.parametrize("M,N,K", [(8, 17408, 5120), (1, 10240, 5120), (8, 5120, 8704),
+                                   (4, 5120, 6144), (3, 1000, 1024)])
+def test_stream_load_probe_runs_without_writing(gpu_lib, M, N, K):
+    """The streaming GEMM's loads alone, each load set, on operands of the GEMM's own sizes (zero
+    data never xors to the pattern): it runs and writes nothing; a shape the plan does not stream
+    is refused."""
+    assert _native.plan(M, N, K)[0] == _native.KERNEL_STREAM
+    wb, sb = _native.packed_bytes(N, K)
+    q = torch.zeros((M, K), dtype=torch.uint8, device="cuda")
+    s = torch.ones(M, dtype=torch.float32, device="cuda")
+    wq = torch.zeros(wb, dtype=torch.uint8, device="cuda")
+    sq = torch.zeros(sb, dtype=torch.uint8, device="cuda")
+    out = torch.zeros(2, dtype=torch.int32, device="cuda")
+    for parts in (_native.STREAM_LOADS_WEIGHTS, _native.STREAM_LOADS_SCALES,
+                  _native.STREAM_LOADS_ALL):
+        print(f"[probe] stream loads M={M} N={N} K={K} parts={parts}", flush=True)
+        _native.stream_load_probe(q.data_ptr(), s.data_ptr(), wq.data_ptr(), sq.data_ptr(), M, N,
+                                  K, parts, out.data_ptr(), stream())
+    torch.cuda.synchronize()
+    assert out.cpu().tolist() == [0, 0]
+    with pytest.raises(RuntimeError, match="not the streaming GEMM"):
+        _native.stream_load_probe(q.data_ptr(), s.data_ptr(), wq.data_ptr(), sq.data_ptr(), M, 33,
+                                  640, 7, out.data_ptr(), stream())
+
+
 def random_shapes(count, seed):
     """Seeded (M, N, K): M over the decode, skinny and tile bands, ragged N, K any multiple of 32."""
     rng = np.random.default_rng(seed)

@@ -61,6 +61,7 @@ SIGNATURES = {
     "w4a8_read_probe_variants": (_int, []),
     "w4a8_read_probe_variant_info": (_int, [_int, _pint, _pint, _pint, _pint]),
     "w4a8_read_probe_shape": (_int, [_vp, _long, _vp, _int, _int, _vp]),
+    "w4a8_stream_load_probe": (_int, [_vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp, _vp]),
     "w4a8_mfma_tile": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _vp]),
 }
 
@@ -256,6 +257,16 @@ def read_probe_variants():
 
 def read_probe_shape(buf_ptr, nbytes, out_ptr, blocks, variant, stream) -> None:
     check(lib().w4a8_read_probe_shape(buf_ptr, nbytes, out_ptr, blocks, variant, stream))
+
+
+# parts of w4a8_stream_load_probe: the weight granules; and the scale dwords; and the activation
+# fragments with the token scales (every load of the streaming GEMM)
+STREAM_LOADS_WEIGHTS, STREAM_LOADS_SCALES, STREAM_LOADS_ALL = 1, 3, 7
+
+
+def stream_load_probe(a_ptr, as_ptr, wq_ptr, sq_ptr, M, N, K, parts, out_ptr, stream) -> None:
+    check(lib().w4a8_stream_load_probe(a_ptr, as_ptr, wq_ptr, sq_ptr, M, N, K, parts, out_ptr,
+                                       stream))
 
 
 def mfma_probe(shape, out_ptr, blocks, iters, stream) -> float:

@@ -983,6 +983,27 @@ W4A8_API int w4a8_read_probe_shape(const void* buf, long bytes, int* out, int bl
                     "w4a8_read_probe_shape");
 }
 
+W4A8_API int w4a8_stream_load_probe(const void* a, const float* a_scale, const void* wq,
+                                    const void* sq, int M, int N, int K, int parts, int* out,
+                                    void* stream) {
+  const char* who = "w4a8_stream_load_probe";
+  if (int e = check_gemm_shape(who, M, N, K)) return e;
+  if (M < 1 || M > 8) return fail(W4A8_EINVAL, "%s: M must be 1..8 (got %d)", who, M);
+  if (parts != 1 && parts != 3 && parts != 7)
+    return fail(W4A8_EINVAL, "%s: parts must be 1, 3 or 7 (got %d)", who, parts);
+  if (int e = check_gemm_ptrs(who, a, a_scale, wq, sq, out)) return e;
+  const int dev = current_device();
+  int kernel = 0, variant = -1, split_k = 1;
+  plan_impl(M, N, K, dev, registered_scratch(dev), &kernel, &variant, &split_k);
+  if (kernel != W4A8_KERNEL_STREAM)
+    return fail(W4A8_EINVAL, "%s: the plan for M=%d N=%d K=%d is not the streaming GEMM", who, M,
+                N, K);
+  const GemmArgs g{(const uint8_t*)a, a_scale, (const uint8_t*)wq, (const uint32_t*)sq, nullptr,
+                   M, N, K, N};
+  return hip_status(
+      launch_stream_loads(g, variant, device_info(dev).cus, parts, out, (hipStream_t)stream), who);
+}
+
 W4A8_API int w4a8_mfma_probe(int shape, float* out, int blocks, int iters, double* flop,
                              void* stream) {
   if ((shape != 0 && shape != 1) || !out || !flop || blocks <= 0 || iters <= 0)

@@ -196,6 +196,98 @@ __global__ __launch_bounds__(W * 64) void gemm_stream(
   }
 }
 
+// gemm_stream<NT, KPW, W, true>'s loads alone (M <= 8), to measure what its load pattern costs
+// without the MFMAs, the reduction and the stores. The statements of the GEMM's sections 1 and 2
+// and its token-scale load: the same grid, buffer resources, offsets, cache policies and order,
+// every load issued before any is used. PARTS (kStreamLoad*) picks the weight granules, the
+// scale dwords, and the activation fragments with the token scale. The xor of everything read
+// goes to out[0] only if it equals a fixed pattern, so the compiler cannot drop a load.
+constexpr int kStreamLoadWeights = 1, kStreamLoadScales = 2, kStreamLoadActivations = 4;
+
+template <int NT, int KPW, int W, int PARTS>
+__global__ __launch_bounds__(W * 64) void gemm_stream_loads(
+    const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
+    const uint32_t* __restrict__ Sq, int* __restrict__ out, int M, int K, int N, int G) {
+  static_assert(KPW % 4 == 0 && NT >= 1 && W >= 1 && W <= 16, "stream variant");
+  const int KT = K / kKTile, KG = KT / kKGroup;  // K % 512 == 0
+  const int NTILES = (N + kNTile - 1) / kNTile;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int b = blockIdx.x;
+  const int ntb0 = b * NTILES / G, nth = (b + 1) * NTILES / G - ntb0;
+  const int om = tid & 7;
+  const int kr0 = 4 * (KG * wave / W), kr1 = 4 * (KG * (wave + 1) / W);
+  const int m = lane & 15, g = lane >> 4;
+  v4i xlo[KPW];
+  uint32_t sv[NT][KPW / 4];
+  v4i wv[KPW][NT];
+  float tok_scale = 0.0f;
+#pragma unroll
+  for (int u = 0; u < KPW; ++u) {
+    xlo[u] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < NT; ++t) wv[u][t] = v4i{0, 0, 0, 0};
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int q = 0; q < KPW / 4; ++q) sv[t][q] = 0;
+  if constexpr ((PARTS & kStreamLoadActivations) != 0) {
+    const auto a_src = __builtin_amdgcn_make_buffer_rsrc((void*)A, 0, M * K, kBufferWord3);
+#pragma unroll
+    for (int u = 0; u < KPW; ++u) {
+      const int kt = min(kr0 + u, KT - 1);
+      xlo[u] = __builtin_amdgcn_raw_buffer_load_b128(
+          a_src, (m & 7) * K + kt * kKTile + 64 * (m >> 3) + 16 * g, 0, 0);
+    }
+  }
+  {
+    __amdgpu_buffer_rsrc_t w_src[NT], s_src[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const bool have = t < nth;
+      w_src[t] = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(Wq + (size_t)(ntb0 + t) * KT * kGranuleBytes), 0,
+          have ? kr1 * kGranuleBytes : 0, kBufferWord3);
+      s_src[t] = __builtin_amdgcn_make_buffer_rsrc((void*)(Sq + (size_t)(ntb0 + t) * KG * 64), 0,
+                                                   have ? (kr1 >> 2) * 256 : 0, kBufferWord3);
+    }
+    if constexpr ((PARTS & kStreamLoadScales) != 0) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int q = 0; q < KPW / 4; ++q)
+          sv[t][q] = __builtin_amdgcn_raw_buffer_load_b32(
+              s_src[t], (((kr0 >> 2) + q) * 64 + lane) * 4, 0, 0);
+    }
+    if constexpr ((PARTS & kStreamLoadWeights) != 0) {
+#pragma unroll
+      for (int u = 0; u < KPW; ++u)
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+          wv[u][t] = __builtin_amdgcn_raw_buffer_load_b128(
+              w_src[t], (kr0 + u) * kGranuleBytes + lane * 16, 0, kBufferNT);
+    }
+  }
+  if constexpr ((PARTS & kStreamLoadActivations) != 0) {
+    const auto as_src = __builtin_amdgcn_make_buffer_rsrc((void*)As, 0, M * 4, kBufferWord3);
+    tok_scale = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(as_src, om * 4, 0, 0));
+  }
+  __builtin_amdgcn_sched_barrier(0);             // every load above is issued before any is used
+  v4i acc = {0, 0, 0, __float_as_int(tok_scale)};
+#pragma unroll
+  for (int u = 0; u < KPW; ++u) {
+    acc ^= xlo[u];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc ^= wv[u][t];
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int q = 0; q < KPW / 4; ++q) acc[t & 3] ^= (int)sv[t][q];
+  if ((acc[0] ^ acc[1] ^ acc[2] ^ acc[3]) == 0x5A17C0DE) out[0] = b;
+}
+
 // The whole linear in one launch (bf16 activations, M <= 8): the W weight waves stream the GEMM
 // as gemm_stream does, without loading activations, while the other Q = 16 - W waves of the
 // workgroup quantize the bf16 rows into LDS, each a 1/Q column range of every row. Nothing
@@ -532,6 +624,30 @@ hipError_t launch_stream(const GemmArgs& g, int variant, int cus, bool fused, lo
 #undef W4A8_STREAM_LAUNCH
 #undef W4A8_STREAM_GO
 #undef W4A8_STREAM_ATTR
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_stream_loads(const GemmArgs& g, int variant, int cus, int parts, int* out,
+                               hipStream_t stream) {
+  const dim3 grid(stream_grid(g.N, cus)), block(kStream[variant].waves * 64);
+  int idx = 0;
+#define W4A8_STREAM_LOADS_GO(nt, kpw, w, p)                                                      \
+  if (parts == (p)) {                                                                            \
+    hipLaunchKernelGGL((gemm_stream_loads<nt, kpw, w, (p)>), grid, block, 0, stream, g.a,        \
+                       g.a_scale, g.wq, g.sq, out, g.M, g.K, g.N, (int)grid.x);                 \
+    return hipGetLastError();                                                                    \
+  }
+#define W4A8_STREAM_LOADS(nt, kpw, w)                                                            \
+  if (idx++ == variant) {                                                                        \
+    W4A8_STREAM_LOADS_GO(nt, kpw, w, kStreamLoadWeights)                                         \
+    W4A8_STREAM_LOADS_GO(nt, kpw, w, kStreamLoadWeights | kStreamLoadScales)                     \
+    W4A8_STREAM_LOADS_GO(nt, kpw, w,                                                             \
+                         kStreamLoadWeights | kStreamLoadScales | kStreamLoadActivations)        \
+    return hipErrorInvalidValue;                                                                 \
+  }
+  W4A8_STREAM_TABLE(W4A8_STREAM_LOADS)
+#undef W4A8_STREAM_LOADS
+#undef W4A8_STREAM_LOADS_GO
   return hipErrorInvalidValue;
 }
 

@@ -168,6 +168,11 @@ bool stream_linear_fits(int variant, int M, int N, int K, long ldx, int cus, siz
 // stage (M <= 2)
 hipError_t launch_stream(const GemmArgs& g, int variant, int cus, bool fused, long lda,
                          hipStream_t stream, bool silu = false);
+// gemm_stream's loads alone (M <= 8; parts 1: weight granules, 3: and scale dwords, 7: and the
+// activation fragments with the token scale), on the GEMM's grid; out: one int, written only if
+// the data xor to a fixed pattern
+hipError_t launch_stream_loads(const GemmArgs& g, int variant, int cus, int parts, int* out,
+                               hipStream_t stream);
 
 // Pipelined streaming family (M <= 16 * MF): grid = at most one workgroup per CU, each with the
 // same number of n-tiles (at most nt) and all of K; each of the `waves` waves streams a contiguous
