@@ -12,7 +12,12 @@
 //    LDS reads (every wave re-read its 16-row activation fragments for every granule).
 // So:
 //  * The grid is at most one workgroup per CU, sized so every workgroup owns the same number of
-//    n-tiles: workgroup b owns [b * NTILES / G, (b + 1) * NTILES / G), at most NT of them.
+//    n-tiles S (the last one what is left): workgroup b owns [b S, min((b + 1) S, NTILES)), at
+//    most NT of them. S comes from the host, so no wave divides by the grid size, and the buffer
+//    resources of its n-tiles are one 64-bit base plus 32-bit offsets. The CU's waves share one
+//    scalar unit, and this prologue runs before any wave's first request: cutting it from ~170
+//    to ~100 scalar instructions per wave (the divisions, then the per-n-tile 64-bit products)
+//    made every streaming shape 0.04-0.13 us faster (A/B on MI355X, same bits).
 //  * Wave w owns the k-groups [KG w / W, KG (w + 1) / W) (4 k-tiles each, so one scale dword per
 //    n-tile) of every n-tile of the workgroup. It loads its activation fragments for those
 //    k-tiles straight into registers (lane l: token l % 16, k 16 (l / 16).. and 64 + 16 (l / 16)..;
@@ -65,7 +70,7 @@ __device__ __forceinline__ void lds_barrier() {
 template <int NT, int KPW, int W, bool H8>
 __global__ __launch_bounds__(W * 64) void gemm_stream(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
-    const uint32_t* __restrict__ Sq, uint16_t* __restrict__ C, int M, int K, int N, int G) {
+    const uint32_t* __restrict__ Sq, uint16_t* __restrict__ C, int M, int K, int N, int S) {
   static_assert(KPW % 4 == 0 && NT >= 1 && W >= 1 && W <= 16, "stream variant");
   const int KT = K / kKTile, KG = KT / kKGroup;  // K % 512 == 0
   const int NTILES = (N + kNTile - 1) / kNTile;
@@ -74,7 +79,11 @@ __global__ __launch_bounds__(W * 64) void gemm_stream(
   // Wave-uniform work selection in scalar registers; 32-bit products only (the host bounds them).
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int b = blockIdx.x;
-  const int ntb0 = b * NTILES / G, nth = (b + 1) * NTILES / G - ntb0;
+  const int ntb0 = b * S, nth = min(S, NTILES - ntb0);
+  // the workgroup's first granule stripe and scale rows (one 64-bit product); an n-tile's stripe
+  // is t KT KiB further, below 2^31 for the NT n-tiles of a workgroup (the host checks it)
+  const uint8_t* const wbase = Wq + (size_t)ntb0 * KT * kGranuleBytes;
+  const uint32_t* const sbase = Sq + (size_t)ntb0 * KG * 64;
   // the epilogue: thread tid adds the partials of output slot tid (below); at M <= 8 a slot is one
   // of the 32 lanes of an n-tile that hold tokens 0..7
   constexpr int LIVE = H8 ? 32 : 64;
@@ -124,9 +133,9 @@ __global__ __launch_bounds__(W * 64) void gemm_stream(
     for (int t = 0; t < NT; ++t) {
       const bool have = t < nth;
       w_src[t] = __builtin_amdgcn_make_buffer_rsrc(
-          (void*)(Wq + (size_t)(ntb0 + t) * KT * kGranuleBytes), 0,
+          (void*)(wbase + (uint32_t)(t * KT * kGranuleBytes)), 0,
           have ? kr1 * kGranuleBytes : 0, kBufferWord3);
-      s_src[t] = __builtin_amdgcn_make_buffer_rsrc((void*)(Sq + (size_t)(ntb0 + t) * KG * 64), 0,
+      s_src[t] = __builtin_amdgcn_make_buffer_rsrc((void*)(sbase + (uint32_t)(t * KG * 64)), 0,
                                                    have ? (kr1 >> 2) * 256 : 0, kBufferWord3);
     }
 #pragma unroll
@@ -234,14 +243,18 @@ constexpr int kStreamLoadWeights = 1, kStreamLoadScales = 2, kStreamLoadActivati
 template <int NT, int KPW, int W, int PARTS>
 __global__ __launch_bounds__(W * 64) void gemm_stream_loads(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
-    const uint32_t* __restrict__ Sq, int* __restrict__ out, int M, int K, int N, int G) {
+    const uint32_t* __restrict__ Sq, int* __restrict__ out, int M, int K, int N, int S) {
   static_assert(KPW % 4 == 0 && NT >= 1 && W >= 1 && W <= 16, "stream variant");
   const int KT = K / kKTile, KG = KT / kKGroup;  // K % 512 == 0
   const int NTILES = (N + kNTile - 1) / kNTile;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int b = blockIdx.x;
-  const int ntb0 = b * NTILES / G, nth = (b + 1) * NTILES / G - ntb0;
+  const int ntb0 = b * S, nth = min(S, NTILES - ntb0);
+  // the workgroup's first granule stripe and scale rows (one 64-bit product); an n-tile's stripe
+  // is t KT KiB further, below 2^31 for the NT n-tiles of a workgroup (the host checks it)
+  const uint8_t* const wbase = Wq + (size_t)ntb0 * KT * kGranuleBytes;
+  const uint32_t* const sbase = Sq + (size_t)ntb0 * KG * 64;
   const int om = tid & 7;
   const int kr0 = 4 * (KG * wave / W), kr1 = 4 * (KG * (wave + 1) / W);
   const int m = lane & 15, g = lane >> 4;
@@ -280,9 +293,9 @@ __global__ __launch_bounds__(W * 64) void gemm_stream_loads(
     for (int t = 0; t < NT; ++t) {
       const bool have = t < nth;
       w_src[t] = __builtin_amdgcn_make_buffer_rsrc(
-          (void*)(Wq + (size_t)(ntb0 + t) * KT * kGranuleBytes), 0,
+          (void*)(wbase + (uint32_t)(t * KT * kGranuleBytes)), 0,
           have ? kr1 * kGranuleBytes : 0, kBufferWord3);
-      s_src[t] = __builtin_amdgcn_make_buffer_rsrc((void*)(Sq + (size_t)(ntb0 + t) * KG * 64), 0,
+      s_src[t] = __builtin_amdgcn_make_buffer_rsrc((void*)(sbase + (uint32_t)(t * KG * 64)), 0,
                                                    have ? (kr1 >> 2) * 256 : 0, kBufferWord3);
     }
     if constexpr ((PARTS & kStreamLoadScales) != 0) {
@@ -371,7 +384,7 @@ __device__ __forceinline__ void fq_signal(int* counter) {
 template <int NT, int KPW, int W, bool SILU>
 __global__ __launch_bounds__(kFqWaves * 64) void gemm_stream_fq(
     const uint8_t* __restrict__ X, const uint8_t* __restrict__ Wq, const uint32_t* __restrict__ Sq,
-    uint16_t* __restrict__ C, int M, int K, int N, int G, int ldx) {
+    uint16_t* __restrict__ C, int M, int K, int N, int S, int ldx) {
   constexpr int Q = kFqWaves - W;                // quantizing waves
   static_assert(KPW % 4 == 0 && NT >= 1 && W >= 1 && Q >= 4 && Q <= 12, "fq variant");
   const int KT = K / kKTile, KG = KT / kKGroup;  // K % 512 == 0
@@ -386,7 +399,11 @@ __global__ __launch_bounds__(kFqWaves * 64) void gemm_stream_fq(
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int b = blockIdx.x;
-  const int ntb0 = b * NTILES / G, nth = (b + 1) * NTILES / G - ntb0;
+  const int ntb0 = b * S, nth = min(S, NTILES - ntb0);
+  // the workgroup's first granule stripe and scale rows (one 64-bit product); an n-tile's stripe
+  // is t KT KiB further, below 2^31 for the NT n-tiles of a workgroup (the host checks it)
+  const uint8_t* const wbase = Wq + (size_t)ntb0 * KT * kGranuleBytes;
+  const uint32_t* const sbase = Sq + (size_t)ntb0 * KG * 64;
   if (wave >= W) {
     // ---- quantizing wave q: chunk columns [c0, c1) of every row (a chunk: 8 elements, 16 B),
     //      column c0 + lane + 64 i in register i. The row loads go out before the barrier below
@@ -463,10 +480,10 @@ __global__ __launch_bounds__(kFqWaves * 64) void gemm_stream_fq(
       for (int t = 0; t < NT; ++t) {
         const bool have = t < nth;
         w_src[t] = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(Wq + (size_t)(ntb0 + t) * KT * kGranuleBytes), 0,
+            (void*)(wbase + (uint32_t)(t * KT * kGranuleBytes)), 0,
             have ? kr1 * kGranuleBytes : 0, kBufferWord3);
         s_src[t] = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(Sq + (size_t)(ntb0 + t) * KG * 64), 0, have ? (kr1 >> 2) * 256 : 0,
+            (void*)(sbase + (uint32_t)(t * KG * 64)), 0, have ? (kr1 >> 2) * 256 : 0,
             kBufferWord3);
       }
 #pragma unroll
@@ -619,6 +636,7 @@ bool stream_linear_fits(int variant, int M, int N, int K, long ldx, int cus, siz
 hipError_t launch_stream(const GemmArgs& g, int variant, int cus, bool fused, long lda,
                          hipStream_t stream, bool silu) {
   const dim3 grid(stream_grid(g.N, cus)), block(kStream[variant].waves * 64);
+  const int share = ceil_div(padded_n(g.N) / kNTile, (int)grid.x);   // n-tiles per workgroup
   const size_t lds = stream_lds_bytes(variant, g.M, g.K, fused);
   int idx = 0;
 #define W4A8_STREAM_ATTR(kern)                                                                   \
@@ -632,7 +650,7 @@ hipError_t launch_stream(const GemmArgs& g, int variant, int cus, bool fused, lo
   {                                                                                              \
     W4A8_STREAM_ATTR((gemm_stream<nt, kpw, w, h8>))                                              \
     hipLaunchKernelGGL((gemm_stream<nt, kpw, w, h8>), grid, block, lds, stream, g.a, g.a_scale,  \
-                       g.wq, g.sq, g.c, g.M, g.K, g.N, (int)grid.x);                            \
+                       g.wq, g.sq, g.c, g.M, g.K, g.N, share);                            \
     return hipGetLastError();                                                                    \
   }
 #define W4A8_STREAM_LAUNCH(nt, kpw, w)                                                           \
@@ -641,13 +659,13 @@ hipError_t launch_stream(const GemmArgs& g, int variant, int cus, bool fused, lo
       if (fused && silu) {                                                                       \
         W4A8_STREAM_ATTR((gemm_stream_fq<nt, kpw, w, true>))                                     \
         hipLaunchKernelGGL((gemm_stream_fq<nt, kpw, w, true>), grid, dim3(kFqWaves * 64), lds,    \
-                           stream, g.a, g.wq, g.sq, g.c, g.M, g.K, g.N, (int)grid.x, (int)lda);  \
+                           stream, g.a, g.wq, g.sq, g.c, g.M, g.K, g.N, share, (int)lda);  \
         return hipGetLastError();                                                                \
       }                                                                                          \
       if (fused) {                                                                               \
         W4A8_STREAM_ATTR((gemm_stream_fq<nt, kpw, w, false>))                                    \
         hipLaunchKernelGGL((gemm_stream_fq<nt, kpw, w, false>), grid, dim3(kFqWaves * 64), lds,   \
-                           stream, g.a, g.wq, g.sq, g.c, g.M, g.K, g.N, (int)grid.x, (int)lda);  \
+                           stream, g.a, g.wq, g.sq, g.c, g.M, g.K, g.N, share, (int)lda);  \
         return hipGetLastError();                                                                \
       }                                                                                          \
     }                                                                                            \
@@ -665,11 +683,12 @@ hipError_t launch_stream(const GemmArgs& g, int variant, int cus, bool fused, lo
 hipError_t launch_stream_loads(const GemmArgs& g, int variant, int cus, int parts, int* out,
                                hipStream_t stream) {
   const dim3 grid(stream_grid(g.N, cus)), block(kStream[variant].waves * 64);
+  const int share = ceil_div(padded_n(g.N) / kNTile, (int)grid.x);
   int idx = 0;
 #define W4A8_STREAM_LOADS_GO(nt, kpw, w, p)                                                      \
   if (parts == (p)) {                                                                            \
     hipLaunchKernelGGL((gemm_stream_loads<nt, kpw, w, (p)>), grid, block, 0, stream, g.a,        \
-                       g.a_scale, g.wq, g.sq, out, g.M, g.K, g.N, (int)grid.x);                 \
+                       g.a_scale, g.wq, g.sq, out, g.M, g.K, g.N, share);                 \
     return hipGetLastError();                                                                    \
   }
 #define W4A8_STREAM_LOADS(nt, kpw, w)                                                            \
