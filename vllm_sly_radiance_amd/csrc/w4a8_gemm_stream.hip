@@ -16,8 +16,9 @@
 //    most NT of them. S comes from the host, so no wave divides by the grid size, and the buffer
 //    resources of its n-tiles are one 64-bit base plus 32-bit offsets. The CU's waves share one
 //    scalar unit, and this prologue runs before any wave's first request: cutting it from ~170
-//    to ~100 scalar instructions per wave (the divisions, then the per-n-tile 64-bit products)
-//    made every streaming shape 0.04-0.13 us faster (A/B on MI355X, same bits).
+//    to ~85 scalar instructions per wave (the divisions, the per-n-tile 64-bit products, then
+//    unsigned shifts and byte offsets) made every streaming shape 0.05-0.2 us faster (A/B on
+//    MI355X, same bits).
 //  * Wave w owns the k-groups [KG w / W, KG (w + 1) / W) (4 k-tiles each, so one scale dword per
 //    n-tile) of every n-tile of the workgroup. It loads its activation fragments for those
 //    k-tiles straight into registers (lane l: token l % 16, k 16 (l / 16).. and 64 + 16 (l / 16)..;
@@ -72,8 +73,9 @@ __global__ __launch_bounds__(W * 64) void gemm_stream(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
     const uint32_t* __restrict__ Sq, uint16_t* __restrict__ C, int M, int K, int N, int S) {
   static_assert(KPW % 4 == 0 && NT >= 1 && W >= 1 && W <= 16, "stream variant");
-  const int KT = K / kKTile, KG = KT / kKGroup;  // K % 512 == 0
-  const int NTILES = (N + kNTile - 1) / kNTile;
+  // K % 512 == 0; K, N > 0 (unsigned shifts: no sign fix-ups in the scalar prologue)
+  const int KT = (int)((unsigned)K / kKTile), KG = (int)((unsigned)KT / kKGroup);
+  const int NTILES = (int)(((unsigned)N + kNTile - 1) / kNTile);
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   // Wave-uniform work selection in scalar registers; 32-bit products only (the host bounds them).
@@ -83,12 +85,13 @@ __global__ __launch_bounds__(W * 64) void gemm_stream(
   // the workgroup's first granule stripe and scale rows (one 64-bit product); an n-tile's stripe
   // is t KT KiB further, below 2^31 for the NT n-tiles of a workgroup (the host checks it)
   const uint8_t* const wbase = Wq + (size_t)ntb0 * KT * kGranuleBytes;
-  const uint32_t* const sbase = Sq + (size_t)ntb0 * KG * 64;
+  const uint8_t* const sbase = reinterpret_cast<const uint8_t*>(Sq) + (size_t)ntb0 * KG * 256;
   // the epilogue: thread tid adds the partials of output slot tid (below); at M <= 8 a slot is one
   // of the 32 lanes of an n-tile that hold tokens 0..7
   constexpr int LIVE = H8 ? 32 : 64;
   const int om = H8 ? (tid & 7) : (tid & 15), og = (tid % LIVE) / (H8 ? 8 : 16);
-  const int kr0 = 4 * (KG * wave / W), kr1 = 4 * (KG * (wave + 1) / W);
+  const int kr0 = 4 * (int)((unsigned)(KG * wave) / W);
+  const int kr1 = 4 * (int)((unsigned)(KG * (wave + 1)) / W);
 
   // ---- 1. the activation fragments of k-tiles kr0.. (L2), the scale dwords (one per n-tile and
   //         k-group) and the granules k-tile by k-tile. Where a wave's range is one k-group
@@ -135,7 +138,7 @@ __global__ __launch_bounds__(W * 64) void gemm_stream(
       w_src[t] = __builtin_amdgcn_make_buffer_rsrc(
           (void*)(wbase + (uint32_t)(t * KT * kGranuleBytes)), 0,
           have ? kr1 * kGranuleBytes : 0, kBufferWord3);
-      s_src[t] = __builtin_amdgcn_make_buffer_rsrc((void*)(sbase + (uint32_t)(t * KG * 64)), 0,
+      s_src[t] = __builtin_amdgcn_make_buffer_rsrc((void*)(sbase + (uint32_t)(t * KG * 256)), 0,
                                                    have ? (kr1 >> 2) * 256 : 0, kBufferWord3);
     }
 #pragma unroll
@@ -245,8 +248,9 @@ __global__ __launch_bounds__(W * 64) void gemm_stream_loads(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
     const uint32_t* __restrict__ Sq, int* __restrict__ out, int M, int K, int N, int S) {
   static_assert(KPW % 4 == 0 && NT >= 1 && W >= 1 && W <= 16, "stream variant");
-  const int KT = K / kKTile, KG = KT / kKGroup;  // K % 512 == 0
-  const int NTILES = (N + kNTile - 1) / kNTile;
+  // K % 512 == 0; K, N > 0 (unsigned shifts: no sign fix-ups in the scalar prologue)
+  const int KT = (int)((unsigned)K / kKTile), KG = (int)((unsigned)KT / kKGroup);
+  const int NTILES = (int)(((unsigned)N + kNTile - 1) / kNTile);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int b = blockIdx.x;
@@ -254,9 +258,10 @@ __global__ __launch_bounds__(W * 64) void gemm_stream_loads(
   // the workgroup's first granule stripe and scale rows (one 64-bit product); an n-tile's stripe
   // is t KT KiB further, below 2^31 for the NT n-tiles of a workgroup (the host checks it)
   const uint8_t* const wbase = Wq + (size_t)ntb0 * KT * kGranuleBytes;
-  const uint32_t* const sbase = Sq + (size_t)ntb0 * KG * 64;
+  const uint8_t* const sbase = reinterpret_cast<const uint8_t*>(Sq) + (size_t)ntb0 * KG * 256;
   const int om = tid & 7;
-  const int kr0 = 4 * (KG * wave / W), kr1 = 4 * (KG * (wave + 1) / W);
+  const int kr0 = 4 * (int)((unsigned)(KG * wave) / W);
+  const int kr1 = 4 * (int)((unsigned)(KG * (wave + 1)) / W);
   const int m = lane & 15, g = lane >> 4;
   v4i xlo[KPW];
   uint32_t sv[NT][KPW / 4];
@@ -295,7 +300,7 @@ __global__ __launch_bounds__(W * 64) void gemm_stream_loads(
       w_src[t] = __builtin_amdgcn_make_buffer_rsrc(
           (void*)(wbase + (uint32_t)(t * KT * kGranuleBytes)), 0,
           have ? kr1 * kGranuleBytes : 0, kBufferWord3);
-      s_src[t] = __builtin_amdgcn_make_buffer_rsrc((void*)(sbase + (uint32_t)(t * KG * 64)), 0,
+      s_src[t] = __builtin_amdgcn_make_buffer_rsrc((void*)(sbase + (uint32_t)(t * KG * 256)), 0,
                                                    have ? (kr1 >> 2) * 256 : 0, kBufferWord3);
     }
     if constexpr ((PARTS & kStreamLoadScales) != 0) {
@@ -387,8 +392,9 @@ __global__ __launch_bounds__(kFqWaves * 64) void gemm_stream_fq(
     uint16_t* __restrict__ C, int M, int K, int N, int S, int ldx) {
   constexpr int Q = kFqWaves - W;                // quantizing waves
   static_assert(KPW % 4 == 0 && NT >= 1 && W >= 1 && Q >= 4 && Q <= 12, "fq variant");
-  const int KT = K / kKTile, KG = KT / kKGroup;  // K % 512 == 0
-  const int NTILES = (N + kNTile - 1) / kNTile;
+  // K % 512 == 0; K, N > 0 (unsigned shifts: no sign fix-ups in the scalar prologue)
+  const int KT = (int)((unsigned)K / kKTile), KG = (int)((unsigned)KT / kKGroup);
+  const int NTILES = (int)(((unsigned)N + kNTile - 1) / kNTile);
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
   uint8_t* const codes = lds;
   float* const tsc = reinterpret_cast<float*>(lds + KT * 1024);
@@ -403,7 +409,7 @@ __global__ __launch_bounds__(kFqWaves * 64) void gemm_stream_fq(
   // the workgroup's first granule stripe and scale rows (one 64-bit product); an n-tile's stripe
   // is t KT KiB further, below 2^31 for the NT n-tiles of a workgroup (the host checks it)
   const uint8_t* const wbase = Wq + (size_t)ntb0 * KT * kGranuleBytes;
-  const uint32_t* const sbase = Sq + (size_t)ntb0 * KG * 64;
+  const uint8_t* const sbase = reinterpret_cast<const uint8_t*>(Sq) + (size_t)ntb0 * KG * 256;
   if (wave >= W) {
     // ---- quantizing wave q: chunk columns [c0, c1) of every row (a chunk: 8 elements, 16 B),
     //      column c0 + lane + 64 i in register i. The row loads go out before the barrier below
@@ -470,7 +476,8 @@ __global__ __launch_bounds__(kFqWaves * 64) void gemm_stream_fq(
     fq_signal(&cnt[1]);
   } else {
     lds_barrier();                               // the quantizing waves' counters are cleared
-    const int kr0 = 4 * (KG * wave / W), kr1 = 4 * (KG * (wave + 1) / W);
+    const int kr0 = 4 * (int)((unsigned)(KG * wave) / W);
+    const int kr1 = 4 * (int)((unsigned)(KG * (wave + 1)) / W);
     // ---- scale dwords and granules, as in gemm_stream ----
     uint32_t sv[NT][KPW / 4];
     v4i wv[KPW][NT];
@@ -483,7 +490,7 @@ __global__ __launch_bounds__(kFqWaves * 64) void gemm_stream_fq(
             (void*)(wbase + (uint32_t)(t * KT * kGranuleBytes)), 0,
             have ? kr1 * kGranuleBytes : 0, kBufferWord3);
         s_src[t] = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(sbase + (uint32_t)(t * KG * 64)), 0, have ? (kr1 >> 2) * 256 : 0,
+            (void*)(sbase + (uint32_t)(t * KG * 256)), 0, have ? (kr1 >> 2) * 256 : 0,
             kBufferWord3);
       }
 #pragma unroll
