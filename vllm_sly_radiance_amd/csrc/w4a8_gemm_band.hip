@@ -92,7 +92,7 @@ __device__ __forceinline__ void band_post(int* counter, int v) {
 template <int MF, int NT, int SG, int R, int D, int L>
 __device__ __forceinline__ void band_body(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
-    const uint32_t* __restrict__ Sq, void* __restrict__ out, int mks, int K, int N, int G) {
+    const uint32_t* __restrict__ Sq, void* __restrict__ out, int mks, int K, int N, int S) {
   static_assert(MF >= 1 && MF <= 4 && NT >= 1 && SG >= 2 && R >= 1, "band variant");
   static_assert(L >= 1 && L <= D && (L - 1) * 2 * MF < 64, "an activation wave may not run past "
                 "the slots it owns, and its loads in flight fit the load counter");
@@ -105,13 +105,18 @@ __device__ __forceinline__ void band_body(
   const int M = mks & 0xFF, KS = mks >> 8;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int KT = K >> 7, KTW = (K + 511) / 512 * 4;      // activation / weight k-tiles
-  const int NTILES = (N + kNTile - 1) / kNTile;
+  // K, N > 0: unsigned shifts, no sign fix-ups in the scalar prologue (the CU's 8 waves share
+  // one scalar unit, and it runs before their first requests)
+  const int KT = (int)((unsigned)K / kKTile);                        // activation k-tiles
+  const int KTW = (int)(((unsigned)K + kKAlign - 1) / kKAlign) * 4;  // weight k-tiles
+  const int NTILES = (int)(((unsigned)N + kNTile - 1) / kNTile);
   const int b = blockIdx.x;
-  const int ntb0 = b * NTILES / G, nth = (b + 1) * NTILES / G - ntb0;
+  // S n-tiles per workgroup (from the host: no division by the grid size), the last what is left
+  const int ntb0 = b * S, nth = min(S, NTILES - ntb0);
   const int ks0 = KS ? (int)blockIdx.y * KS : 0, ks1 = KS ? min(ks0 + KS, KT) : KT;
   const int wv = wave & (WW - 1);
-  const int kb = ks0 + (ks1 - ks0) * wv / WW, ke = ks0 + (ks1 - ks0) * (wv + 1) / WW;
+  const int kb = ks0 + (int)((unsigned)((ks1 - ks0) * wv) / WW);
+  const int ke = ks0 + (int)((unsigned)((ks1 - ks0) * (wv + 1)) / WW);
   const int nk = ke - kb;
   if (tid <= 2 * WW) ctr[tid] = 0;
   band_barrier();
@@ -130,14 +135,18 @@ __device__ __forceinline__ void band_body(
     __amdgpu_buffer_rsrc_t w_src[NT];
     uint32_t sv[NT][SG];
     const int g0 = kb >> 2;
+    // the workgroup's first stripe and scale rows (one 64-bit product), then 32-bit offsets (the
+    // host keeps NT stripes below 2^31 bytes)
+    const uint8_t* const wbase = Wq + (size_t)ntb0 * KTW * kGranuleBytes;
+    const uint8_t* const sbase = reinterpret_cast<const uint8_t*>(Sq) + (size_t)ntb0 * KTW * 64;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const bool have = t < nth;
       w_src[t] = __builtin_amdgcn_make_buffer_rsrc(
-          (void*)(Wq + (size_t)(ntb0 + t) * KTW * kGranuleBytes), 0,
+          (void*)(wbase + (uint32_t)(t * KTW * kGranuleBytes)), 0,
           have ? ke * kGranuleBytes : 0, kBufferWord3);
       const auto s_src = __builtin_amdgcn_make_buffer_rsrc(
-          (void*)(Sq + (size_t)(ntb0 + t) * (KTW / kKGroup) * 64), 0,
+          (void*)(sbase + (uint32_t)(t * KTW * 64)), 0,
           have ? ((ke + 3) >> 2) * 256 : 0, kBufferWord3);
 #pragma unroll
       for (int q = 0; q < SG; ++q)
@@ -281,8 +290,8 @@ __device__ __forceinline__ void band_body(
 template <int MF, int NT, int SG, int R, int D, int L>
 __global__ __launch_bounds__(2 * kBandWW * 64) void gemm_band(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
-    const uint32_t* __restrict__ Sq, void* __restrict__ out, int mks, int K, int N, int G) {
-  band_body<MF, NT, SG, R, D, L>(A, As, Wq, Sq, out, mks, K, N, G);
+    const uint32_t* __restrict__ Sq, void* __restrict__ out, int mks, int K, int N, int S) {
+  band_body<MF, NT, SG, R, D, L>(A, As, Wq, Sq, out, mks, K, N, S);
 }
 
 // (MF, NT, SG, R, D, L): MF 16-token fragments, at most NT n-tiles per workgroup, SG scale dwords
@@ -332,8 +341,8 @@ bool band_fits(int variant, int M, int N, int K, int cus, int splits, size_t lds
   // a weight wave's k-range: at most ceil(KS / 4) k-tiles, spanning at most SG k-groups
   const int ks = ceil_div(KT, splits), kw = ceil_div(ks, kBandWW);
   if ((kw + 2) / 4 + 1 > c.sg) return false;
-  const bool small = (long)64 * K < (1L << 31) && (long)padded_k(K) / kKTile * kGranuleBytes <
-                     (1L << 31) && (long)padded_n(N) < (1L << 24) && ks < (1 << 23);
+  const bool small = (long)64 * K < (1L << 31) && (long)c.nt * padded_k(K) / kKTile *
+                     kGranuleBytes < (1L << 31) && (long)padded_n(N) < (1L << 24) && ks < (1 << 23);
   return small && band_lds_bytes(c) <= lds_limit;
 }
 
@@ -348,6 +357,7 @@ hipError_t launch_band(const GemmArgs& g, int variant, int cus, int splits, floa
   const int ks = splits > 1 ? ceil_div(KT, splits) : 0;
   const int rows = splits > 1 ? ceil_div(KT, ks) : 1;
   const int G = band_grid(g.N, cus, splits > 1 ? splits : 1);
+  const int share = ceil_div(padded_n(g.N) / kNTile, G);   // n-tiles per workgroup
   const size_t lds = band_lds_bytes(c);
   void* const out = splits > 1 ? (void*)partial : (void*)g.c;
   const int mks = g.M | (ks << 8);
@@ -361,7 +371,7 @@ hipError_t launch_band(const GemmArgs& g, int variant, int cus, int splits, floa
       if (e != hipSuccess) return e;                                                             \
     }                                                                                            \
     hipLaunchKernelGGL((gemm_band<mf, nt, sg, r, d, l>), dim3(G, rows), dim3(2 * kBandWW * 64),  \
-                       lds, stream, g.a, g.a_scale, g.wq, g.sq, out, mks, g.K, g.N, G);         \
+                       lds, stream, g.a, g.a_scale, g.wq, g.sq, out, mks, g.K, g.N, share);     \
     const hipError_t e = hipGetLastError();                                                      \
     if (e != hipSuccess || splits <= 1) return e;                                                \
     return launch_split_reduce(partial, g, rows, stream);                                        \
