@@ -135,17 +135,23 @@ __device__ __forceinline__ void tile_body(
   uint8_t* const junk = sring + RING * S::S_SLOT;  // where the surplus scale fills land
   uint8_t* const tscale = junk + 1024;             // the tile's per-token fp32 scales
 
-  // ---- tile order: XCD-contiguous runs, grouped by 8 row blocks ----
-  const int total = grid_m * grid_n;
-  int t = blockIdx.x;
-  if (total % 8 == 0) t = (t % 8) * (total / 8) + t / 8;
-  constexpr int GROUP = 8;
-  const int per_group = GROUP * grid_n;
-  const int first_m = (t / per_group) * GROUP;
-  const int gm = min(grid_m - first_m, GROUP);
-  const int bm = first_m + (t % per_group) % gm;
-  const int bn = (t % per_group) / gm;
-  const int m0 = bm * S::BM, nt_base = bn * (S::BN / 16);
+  // ---- tile order: XCD-contiguous runs, grouped by 8 row blocks. Unsigned, and no division at
+  //      all for one row of tiles (the decode band): the workgroup's waves share one scalar unit,
+  //      and this runs before their first requests ----
+  constexpr unsigned GROUP = 8;
+  const unsigned total = (unsigned)(grid_m * grid_n);
+  unsigned t = blockIdx.x;
+  if ((total & 7) == 0) t = (t & 7) * (total >> 3) + (t >> 3);
+  unsigned bm = 0, bn = t;
+  if (grid_m > 1) {
+    const unsigned per_group = GROUP * (unsigned)grid_n;
+    const unsigned grp = t / per_group, r = t - grp * per_group;
+    const unsigned first_m = grp * GROUP;
+    const unsigned gm = min((unsigned)grid_m - first_m, GROUP);
+    bn = r / gm;
+    bm = first_m + (r - bn * gm);
+  }
+  const int m0 = (int)bm * S::BM, nt_base = (int)bn * (S::BN / 16);
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
