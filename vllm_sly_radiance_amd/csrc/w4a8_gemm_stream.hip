@@ -475,7 +475,10 @@ __global__ __launch_bounds__(kFqWaves * 64) void gemm_stream_fq(
     }
     fq_signal(&cnt[1]);
   } else {
-    lds_barrier();                               // the quantizing waves' counters are cleared
+    // where a wave's range is one k-group its scale dwords and first k-tile's granules go out
+    // before the barrier (beside the quantizing waves' row loads), the rest after it
+    constexpr bool kHbmFirst = KPW == 4;
+    if constexpr (!kHbmFirst) lds_barrier();     // the quantizing waves' counters are cleared
     const int kr0 = 4 * (int)((unsigned)(KG * wave) / W);
     const int kr1 = 4 * (int)((unsigned)(KG * (wave + 1)) / W);
     // ---- scale dwords and granules, as in gemm_stream ----
@@ -500,11 +503,13 @@ __global__ __launch_bounds__(kFqWaves * 64) void gemm_stream_fq(
           sv[t][qq] = __builtin_amdgcn_raw_buffer_load_b32(
               s_src[t], (((kr0 >> 2) + qq) * 64 + lane) * 4, 0, 0);
 #pragma unroll
-      for (int u = 0; u < KPW; ++u)
+      for (int u = 0; u < KPW; ++u) {
+        if (kHbmFirst && u == 1) lds_barrier();  // the quantizing waves' counters are cleared
 #pragma unroll
         for (int t = 0; t < NT; ++t)
           wv[u][t] = __builtin_amdgcn_raw_buffer_load_b128(
               w_src[t], (kr0 + u) * kGranuleBytes + lane * 16, 0, kBufferNT);
+      }
     }
     __builtin_amdgcn_sched_barrier(0);           // every load above is issued before the wait
     fq_wait(&cnt[1], Q, &cnt[2]);                // the quantizing waves' codes
