@@ -475,12 +475,12 @@ __global__ __launch_bounds__(kFqWaves * 64) void gemm_stream_fq(
     }
     fq_signal(&cnt[1]);
   } else {
-    // where a wave's range is one k-group its scale dwords and first k-tile's granules go out
-    // before the barrier (beside the quantizing waves' row loads), the rest after it: gate_up at
-    // M = 1 / 2 0.34 / 0.23 us faster (A/B on MI355X, same bits); the longer-range variants
-    // (o_proj, down) measured 0.2-0.4 us slower that way and keep the barrier first
+    // the scale dwords go out before the barrier (beside the quantizing waves' row loads), and
+    // where a wave's range is one k-group the first k-tile's granules too, the rest after it:
+    // gate_up at M = 1 / 2 0.34 / 0.23 us faster (A/B on MI355X, same bits), qkv, o_proj and
+    // down 0.02-0.04 us; with their first granules early as well the longer-range variants
+    // (o_proj, down) measured 0.2-0.4 us slower
     constexpr bool kHbmFirst = KPW == 4;
-    if constexpr (!kHbmFirst) lds_barrier();     // the quantizing waves' counters are cleared
     const int kr0 = 4 * (int)((unsigned)(KG * wave) / W);
     const int kr1 = 4 * (int)((unsigned)(KG * (wave + 1)) / W);
     // ---- scale dwords and granules, as in gemm_stream ----
@@ -504,6 +504,7 @@ __global__ __launch_bounds__(kFqWaves * 64) void gemm_stream_fq(
         for (int qq = 0; qq < KPW / 4; ++qq)
           sv[t][qq] = __builtin_amdgcn_raw_buffer_load_b32(
               s_src[t], (((kr0 >> 2) + qq) * 64 + lane) * 4, 0, 0);
+      if constexpr (!kHbmFirst) lds_barrier();   // the quantizing waves' counters are cleared
 #pragma unroll
       for (int u = 0; u < KPW; ++u) {
         if (kHbmFirst && u == 1) lds_barrier();  // the quantizing waves' counters are cleared
