@@ -141,12 +141,16 @@ __global__ __launch_bounds__(W * 64) void gemm_stream(
       s_src[t] = __builtin_amdgcn_make_buffer_rsrc((void*)(sbase + (uint32_t)(t * KG * 256)), 0,
                                                    have ? (kr1 >> 2) * 256 : 0, kBufferWord3);
     }
+    // Scale dwords are read once, like the granules. Where they go out first at M <= 8, loading
+    // them non-temporal measured 0.06-0.11 us faster at N = 17408, K = 5120 (A/B on MI355X, three
+    // boxes). With KPW >= 8 (activations first) it was 0.03-0.12 us slower, at M > 8 it was within
+    // noise, and in gemm_stream_fq's weight waves it was slower (+0.19 us at M = 2).
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int q = 0; q < KPW / 4; ++q)
         sv[t][q] = __builtin_amdgcn_raw_buffer_load_b32(
-            s_src[t], (((kr0 >> 2) + q) * 64 + lane) * 4, 0, 0);
+            s_src[t], (((kr0 >> 2) + q) * 64 + lane) * 4, 0, kHbmFirst && H8 ? kBufferNT : 0);
 #pragma unroll
     for (int u = 0; u < KPW; ++u) {
       if constexpr (kHbmFirst) {
@@ -309,7 +313,7 @@ __global__ __launch_bounds__(W * 64) void gemm_stream_loads(
 #pragma unroll
         for (int q = 0; q < KPW / 4; ++q)
           sv[t][q] = __builtin_amdgcn_raw_buffer_load_b32(
-              s_src[t], (((kr0 >> 2) + q) * 64 + lane) * 4, 0, 0);
+              s_src[t], (((kr0 >> 2) + q) * 64 + lane) * 4, 0, kHbmFirst ? kBufferNT : 0);
     }
 #pragma unroll
     for (int u = 0; u < KPW; ++u) {
